@@ -1,0 +1,140 @@
+/*
+ * mtgemm.h -- C ABI of the MI355X (gfx950) fp32 GEMM backend for miniTensor.
+ *
+ * Every entry point takes plain pointers, element strides and sizes; no C++
+ * or torch types cross this boundary, so the library can be bound from the
+ * reference's C++ launchers, from ctypes, or from any other FFI.
+ *
+ * Conventions (they follow the reference's launch contract):
+ *   - Device pointers only.  `base` is the storage base (the reference's
+ *     Tensor::data(), include/Tensor.hpp:80) and `offset` is added inside the
+ *     library (Tensor::offset(), include/Tensor.hpp:83).  Strides are in
+ *     elements, may be 0 (a broadcast / expand view, include/TensorImpl.hpp:204-228)
+ *     and are never materialised.
+ *   - All work is enqueued asynchronously on `stream` (a hipStream_t; NULL is
+ *     the legacy default stream), like the reference's active_stream()
+ *     (include/GpuUtils.hpp:61-64).  No entry point synchronises the device or
+ *     allocates memory: scratch space is passed in by the caller
+ *     (`workspace`, sized by the matching *_workspace_* query), as the
+ *     reference takes it from its MemoryPool (src/gpu_ops.cpp:2264-2266).
+ *   - Return value 0 on success, a negative mt_status otherwise; nothing
+ *     throws across the ABI.  MT_ERR_INVALID maps to the reference's
+ *     std::invalid_argument, every other code to std::runtime_error
+ *     (include/GpuUtils.hpp:47-55).
+ *   - C must not overlap A, B or bias.
+ */
+#ifndef MTGEMM_H
+#define MTGEMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MTGEMM_VERSION 1
+
+typedef enum mt_status {
+    MT_OK = 0,
+    MT_ERR_INVALID = -1,     /* bad shape / stride / pointer argument        */
+    MT_ERR_WORKSPACE = -2,   /* workspace missing or smaller than required   */
+    MT_ERR_HIP = -3,         /* a HIP runtime call or kernel launch failed   */
+    MT_ERR_UNSUPPORTED = -4  /* valid request this build does not implement  */
+} mt_status;
+
+/* A (possibly batched) strided fp32 matrix view.
+ * Element (b, r, c) lives at base[offset + b*batch_stride + r*row_stride + c*col_stride]. */
+typedef struct mt_mat_f32 {
+    const float* base;
+    int64_t offset;
+    int64_t rows, cols;
+    int64_t row_stride, col_stride;
+    int64_t batch;          /* >= 1 */
+    int64_t batch_stride;   /* 0: the same matrix for every batch entry */
+} mt_mat_f32;
+
+typedef enum mt_bias_axis {
+    MT_BIAS_NONE = 0,
+    MT_BIAS_ROW = 1,   /* bias[m * bias_stride] added to row m    (conv, per output channel) */
+    MT_BIAS_COL = 2    /* bias[n * bias_stride] added to column n (Linear, per output feature) */
+} mt_bias_axis;
+
+/* Fused epilogue: C = A·B + bias + beta·C_old.  beta == 0 never reads C. */
+typedef struct mt_epilogue_f32 {
+    const float* bias;      /* device pointer, element 0 of the bias vector (offset applied) */
+    int64_t bias_stride;
+    int32_t bias_axis;      /* mt_bias_axis */
+    float beta;
+} mt_epilogue_f32;
+
+/* C[b] = A[b]·B[b] (+ epilogue) for b in [0, batch).
+ * A: [M,K], B: [K,N], C: [M,N] per batch entry; C->base is written.
+ * batch = C->batch; A->batch and B->batch must be 1 or equal to it.
+ * `ep` may be NULL (no bias, beta 0).  K == 0 writes bias (or zeros).
+ * Replaces matmul_gpu / matmul_gpu_v2 / matmul_gpu_bk16 / matmul_gpu_strided
+ * (reference src/gpu_ops.cpp:1103-1144, 1167-1223; declared in
+ * include/TensorOps.hpp:703-706) and the per-batch loop of bmm
+ * (include/TensorOps.hpp:933-991). */
+int mt_gemm_f32(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C,
+                const mt_epilogue_f32* ep, void* workspace, size_t ws_bytes,
+                void* stream);
+
+/* Workspace bytes mt_gemm_f32 needs for these operands (0 if none). */
+size_t mt_gemm_workspace_f32(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C);
+
+/* out[c] = beta*out[c] + sum_r X[r][c]: the bias gradient of Linear.
+ * Replaces the reference's unbroadcast -> sum_gpu(dY, 0, keepdims) path
+ * (include/TensorOps.hpp:1304-1346, src/gpu_ops.cpp:1306-1348). */
+int mt_colsum_f32(const mt_mat_f32* X, float* out, int64_t out_stride, float beta,
+                  void* stream);
+
+/* ---- Linear -------------------------------------------------------------
+ * PyTorch layout, as F::linear: X [B,in], W [out,in], bias [out], Y [B,out].
+ * The reference's Linear keeps W_ref = Wᵀ as [in,out] (include/Module.hpp:92-114);
+ * a caller holding W_ref passes it with row/col strides swapped.
+ * Forward:  Y = X·Wᵀ + b (bias fused into the GEMM epilogue).
+ * Backward: dX = dY·W, dW = dYᵀ·X (+ beta_w·dW_old), db = Σ_rows dY (+ beta_b·db_old).
+ * Any of dX, dW, db may be NULL to skip that gradient. */
+int mt_linear_forward_f32(const mt_mat_f32* X, const mt_mat_f32* W, const float* bias,
+                          int64_t bias_stride, const mt_mat_f32* Y,
+                          void* workspace, size_t ws_bytes, void* stream);
+size_t mt_linear_workspace_f32(int64_t batch_rows, int64_t in_features, int64_t out_features);
+int mt_linear_backward_f32(const mt_mat_f32* dY, const mt_mat_f32* X, const mt_mat_f32* W,
+                           const mt_mat_f32* dX, const mt_mat_f32* dW, float beta_w,
+                           float* db, int64_t db_stride, float beta_b,
+                           void* workspace, size_t ws_bytes, void* stream);
+
+/* ---- Conv2D forward as a GEMM ---------------------------------------------
+ * NCHW input [n,c_in,h,w], OIHW weight [c_out,c_in,kh,kw], bias [c_out] or NULL,
+ * output [n,c_out,h_out,w_out] with h_out = (h + 2*pad - kh)/stride + 1
+ * (0 when h + 2*pad < kh), as the reference's safe_out_size
+ * (include/TensorOps.hpp:17-20).  Tensors are dense NCHW (element offsets
+ * applied by the caller).  The GEMM is C[c_out, n*h_out*w_out] =
+ * W[c_out, c_in*kh*kw] · col[c_in*kh*kw, n*h_out*w_out] with the row bias fused
+ * and the output scattered straight into NCHW.  Replaces conv2d_gpu +
+ * im2col_kernel + batched_sgemm_kernel_v2 (reference src/gpu_ops.cpp:2237-2325,
+ * 1748-1825, 683-859; declared include/TensorOps.hpp:708). */
+typedef struct mt_conv2d_desc {
+    int64_t n, c_in, h, w;
+    int64_t c_out, kh, kw;
+    int64_t stride, pad;
+} mt_conv2d_desc;
+
+int mt_conv2d_fwd_f32(const mt_conv2d_desc* d, const float* input, const float* weight,
+                      const float* bias, float* output, void* workspace, size_t ws_bytes,
+                      void* stream);
+size_t mt_conv2d_workspace_f32(const mt_conv2d_desc* d);
+
+/* ---- diagnostics ---------------------------------------------------------- */
+const char* mt_strerror(int status);
+int mt_version(void);
+/* Name of the kernel configuration the last mt_gemm_f32 call on this thread
+ * selected (tile, operand layouts, split-K), for tests and benchmarks. */
+const char* mt_last_config(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MTGEMM_H */

@@ -1,0 +1,83 @@
+"""Build the gfx950 GEMM library (minitensor_amd/lib/libmtgemm.so) with hipcc.
+
+Every tile configuration is its own translation unit so the template
+instantiations compile in parallel.  The library is built in-tree so it
+travels with the source tree to the GPU machine; nothing is JIT-compiled.
+
+    python -m minitensor_amd.build          # or: python minitensor_amd/build.py
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+LIBDIR = PKG / "lib"
+OBJDIR = PKG / "_build"
+LIB = LIBDIR / "libmtgemm.so"
+
+ARCH = "gfx950"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+# -packed-fp32-ops: keep the compiler from emitting v_pk_{add,mul,fma}_f32.
+COMMON = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++20", "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{ROOT / 'include'}", f"-I{CSRC}",
+    "-Wno-unused-command-line-argument",
+]
+
+N_CFG = 3
+
+
+def _units():
+    units = []
+    for cfg in range(N_CFG):
+        units.append((CSRC / "gemm_instances.hip", OBJDIR / f"gemm_cfg{cfg}.o", [f"-DMT_CFG={cfg}"]))
+    units.append((CSRC / "mtgemm_api.hip", OBJDIR / "mtgemm_api.o", []))
+    return units
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every unit and link libmtgemm.so; raises on any compiler error."""
+    if not shutil.which(HIPCC) and not Path(HIPCC).exists():
+        raise RuntimeError(f"hipcc not found at {HIPCC}")
+    OBJDIR.mkdir(parents=True, exist_ok=True)
+    LIBDIR.mkdir(parents=True, exist_ok=True)
+    procs = []
+    for src, obj, extra in _units():
+        cmd = [HIPCC, *COMMON, *extra, "-c", str(src), "-o", str(obj)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                                            text=True)))
+    failed = []
+    for cmd, p in procs:
+        out, _ = p.communicate()
+        lines = [l for l in out.splitlines() if "packed-fp32-ops" not in l]
+        if p.returncode != 0:
+            failed.append((cmd, "\n".join(lines)))
+        elif verbose and lines:
+            print("\n".join(lines))
+    if failed:
+        msg = "\n\n".join(f"$ {' '.join(c)}\n{o}" for c, o in failed)
+        raise RuntimeError(f"hipcc failed:\n{msg}")
+    tmp = LIB.with_suffix(".so.tmp")
+    link = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
+            *[str(o) for _, o, _ in _units()]]
+    if verbose:
+        print(" ".join(link), flush=True)
+    r = subprocess.run(link, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{r.stdout}")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,36 @@
+// gemm_configs.hpp -- the tile configurations the dispatcher chooses from and
+// the launcher table each instantiation unit (gemm_instances.hip) exports.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "gemm_kernel.hpp"
+
+namespace mtk {
+
+// Block tile BM x BN x BK, wave tile WM x WN.  Threads = (BM/WM)*(BN/WN)*64.
+template <int CFG> struct TileCfg;
+// 256x256: one workgroup (8 waves, 2 per SIMD) fills a CU; 4096^2 -> 256 tiles.
+template <> struct TileCfg<0> { static constexpr int BM = 256, BN = 256, BK = 16, WM = 128, WN = 64; };
+// 128x128: 4 waves; several workgroups share a CU.
+template <> struct TileCfg<1> { static constexpr int BM = 128, BN = 128, BK = 16, WM = 64, WN = 64; };
+// 64x64: 4 waves of 32x32, for small and skinny problems (usually with split-K).
+template <> struct TileCfg<2> { static constexpr int BM = 64, BN = 64, BK = 16, WM = 32, WN = 32; };
+
+constexpr int kNumCfg = 3;
+constexpr int kNumLayout = 4;
+
+template <int CFG>
+constexpr int cfg_threads() {
+    return (TileCfg<CFG>::BM / TileCfg<CFG>::WM) * (TileCfg<CFG>::BN / TileCfg<CFG>::WN) * 64;
+}
+
+using GemmLaunchFn = hipError_t (*)(const GemmParams&, unsigned nblocks, hipStream_t);
+
+// Launcher of configuration CFG for (layout of A, layout of B); defined in the
+// instantiation unit built with MT_CFG == CFG.
+GemmLaunchFn launcher_cfg0(int la, int lb);
+GemmLaunchFn launcher_cfg1(int la, int lb);
+GemmLaunchFn launcher_cfg2(int la, int lb);
+
+}  // namespace mtk

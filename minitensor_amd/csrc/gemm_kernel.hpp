@@ -1,0 +1,331 @@
+// gemm_kernel.hpp -- fp32 GEMM on CDNA4 matrix cores (gfx950).
+//
+// One templated kernel computes C[b] = A[b]·B[b] (+ bias + beta·C) for every
+// operand layout the reference's matmul can hand over: row-major tensors,
+// transpose views (reference include/TensorImpl.hpp:194-202), row slices with
+// an offset (include/Tensor.hpp:52-74) and stride-0 expand views
+// (include/TensorImpl.hpp:204-228).  It replaces the reference's FMA kernels
+// sgemm_kernel_v2 (src/gpu_ops.cpp:932-1101), matmul_kernel_strided
+// (909-930) and batched_sgemm_kernel_v2 (683-859) with one MFMA design.
+//
+// Design (wave64, v_mfma_f32_32x32x2_f32):
+//   * A block tile BM x BN is split over (BM/WM) x (BN/WN) waves; each wave
+//     owns (WM/32) x (WN/32) accumulators of 32x32 fp32 (16 VGPR/AGPR each).
+//   * K advances in chunks of BK, double-buffered in LDS: chunk k+1 is fetched
+//     from HBM into registers while chunk k is multiplied, then written to the
+//     other LDS buffer; one barrier per chunk.
+//   * Each operand tile is stored in LDS in the layout that matches its
+//     contiguous global dimension, so every global load is a coalesced
+//     16-byte vector (or a scalar gather for unaligned / doubly strided views)
+//     and no view is ever materialised:
+//        k-contiguous operands  -> LDS [mn][BK+4]   (A row-major, Bᵀ views)
+//        mn-contiguous operands -> LDS [BK][BMN+4]  (B row-major, Aᵀ views)
+//   * K is permuted inside every 16-wide sub-chunk: at MFMA step s lanes 0-31
+//     contract k = 8h + s with h = lane/32 instead of 2s + h.  A sum does not
+//     depend on its order of terms, and both operands use the same
+//     permutation, so the product is unchanged; the gain is that a lane's 8
+//     k-values of one row are contiguous, one pair of ds_read_b128 for
+//     k-contiguous LDS tiles.
+//   * MFMA operand layout (v_mfma_f32_32x32x2_f32, CDNA3/CDNA4 ISA):
+//        A: lane l holds A[i = l%32][k = l/32];  B: lane l holds B[k = l/32][j = l%32]
+//        D: lane l, register r holds D[8*(r/4) + 4*(l/32) + r%4][l%32].
+//   * Work decomposition: one workgroup per (tile, split, batch) in a 1-D grid.
+//     Consecutive workgroup ids are dealt round-robin to the 8 XCDs, so ids
+//     are remapped to give each XCD a contiguous range of tiles, which are
+//     then ordered in groups of `group_m` tile rows for L2 reuse.
+//   * Split-K writes fp32 partials to a workspace that a second kernel sums
+//     in a fixed order (deterministic; no float atomics).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mtk {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Operand layout modes, in (mn, k) coordinates of the operand.
+enum : int {
+    L_KV = 0,  // k contiguous (stride 1), 16-byte vector loads
+    L_MV = 1,  // mn contiguous (stride 1), 16-byte vector loads
+    L_KS = 2,  // k-contiguous LDS tile, scalar gathers (any strides)
+    L_MS = 3   // mn-contiguous LDS tile, scalar gathers (any strides)
+};
+
+struct GemmParams {
+    const float* A; int64_t a_mn, a_k, a_b;   // A(m,k) = A[m*a_mn + k*a_k + b*a_b]
+    const float* B; int64_t b_mn, b_k, b_b;   // B(k,n) = B[n*b_mn + k*b_k + b*b_b]
+    float* C; int64_t c_m, c_n, c_b;          // C(m,n) = C[m*c_m + col(n) + b*c_b]
+    // col(n) = n*c_n when c_n_inner >= N, otherwise
+    // (n / c_n_inner)*c_n_outer + (n % c_n_inner)*c_n (NCHW scatter of a conv GEMM).
+    int64_t c_n_inner, c_n_outer;
+    const float* bias; int64_t bias_stride; int bias_axis;  // 0 none, 1 per row m, 2 per column n
+    float beta;
+    float* ws;                                // split-K partials [splits][batch][M][N]
+    int M, N, K, batch;
+    int splits, k_per_split;                  // k_per_split is a multiple of BK
+    int tiles_m, tiles_n, group_m;
+};
+
+template <int L>
+struct LayoutTraits {
+    static constexpr bool kc = (L == L_KV || L == L_KS);
+    static constexpr bool vec = (L == L_KV || L == L_MV);
+};
+
+// Geometry of one operand tile (BMN rows of the mn dimension by BK of k).
+template <int L, int BMN, int BK, int NT>
+struct TileGeom {
+    static constexpr bool kc = LayoutTraits<L>::kc;
+    static constexpr bool vec = LayoutTraits<L>::vec;
+    static constexpr int pitch = kc ? (BK + 4) : (BMN + 4);
+    static constexpr int lds_floats = kc ? BMN * pitch : BK * pitch;
+    static constexpr int items = vec ? (BMN * BK / 4) / NT : (BMN * BK) / NT;
+    static_assert(items >= 1, "tile too small for the thread count");
+    static_assert(vec ? ((BMN * BK / 4) % NT == 0) : ((BMN * BK) % NT == 0),
+                  "tile elements must divide evenly over the threads");
+    static_assert(pitch % 4 == 0, "LDS rows must stay 16-byte aligned");
+};
+
+// Global -> register -> LDS mover for one operand tile.
+template <int L, int BMN, int BK, int NT>
+struct TileLoader {
+    using G = TileGeom<L, BMN, BK, NT>;
+    static constexpr int NI = G::items;
+    using Reg = typename std::conditional<G::vec, f32x4, float>::type;
+
+    const float* ptr[NI];
+    int kofs[NI];
+    int lds_off[NI];
+    bool mn_ok[NI];
+    int64_t kstep;
+    Reg reg[NI];
+
+    __device__ __forceinline__ void init(const float* X, int64_t s_mn, int64_t s_k, int MN,
+                                         int mn0, int k0, int t) {
+        kstep = (int64_t)BK * s_k;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int v = t + i * NT;
+            int mn, kk, off;
+            if constexpr (G::vec && G::kc) {
+                const int kq = v % (BK / 4), r = v / (BK / 4);
+                mn = mn0 + r; kk = kq * 4; off = r * G::pitch + kk;
+            } else if constexpr (G::vec) {
+                const int mq = v % (BMN / 4), kr = v / (BMN / 4);
+                mn = mn0 + mq * 4; kk = kr; off = kr * G::pitch + mq * 4;
+            } else if constexpr (G::kc) {
+                const int k = v % BK, r = v / BK;
+                mn = mn0 + r; kk = k; off = r * G::pitch + k;
+            } else {
+                const int c = v % BMN, k = v / BMN;
+                mn = mn0 + c; kk = k; off = k * G::pitch + c;
+            }
+            mn_ok[i] = mn < MN;
+            kofs[i] = kk;
+            lds_off[i] = off;
+            ptr[i] = X + (int64_t)(mn_ok[i] ? mn : 0) * s_mn + (int64_t)(k0 + kk) * s_k;
+        }
+    }
+
+    // Fetch the chunk whose first k index is kbase; k >= kend reads as zero.
+    __device__ __forceinline__ void load(int kbase, int kend) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const bool ok = mn_ok[i] && (kbase + kofs[i] < kend);
+            if constexpr (G::vec) {
+                f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                reg[i] = ok ? *reinterpret_cast<const f32x4*>(ptr[i]) : z;
+            } else {
+                reg[i] = ok ? *ptr[i] : 0.f;
+            }
+            ptr[i] += kstep;
+        }
+    }
+
+    __device__ __forceinline__ void store(float* lds) const {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            if constexpr (G::vec) {
+                *reinterpret_cast<f32x4*>(lds + lds_off[i]) = reg[i];
+            } else {
+                lds[lds_off[i]] = reg[i];
+            }
+        }
+    }
+};
+
+// The 8 k-values (sub-chunk q, permuted order) of one 32-row MFMA block.
+template <int L, int BMN, int BK, int NT>
+__device__ __forceinline__ void read_frag(const float* lds, int row0, int q, int lane,
+                                          float (&f)[8]) {
+    using G = TileGeom<L, BMN, BK, NT>;
+    const int h = lane >> 5, c = lane & 31;
+    if constexpr (G::kc) {
+        const float* p = lds + (row0 + c) * G::pitch + q * 16 + h * 8;
+        const f32x4 x = *reinterpret_cast<const f32x4*>(p);
+        const f32x4 y = *reinterpret_cast<const f32x4*>(p + 4);
+        f[0] = x[0]; f[1] = x[1]; f[2] = x[2]; f[3] = x[3];
+        f[4] = y[0]; f[5] = y[1]; f[6] = y[2]; f[7] = y[3];
+    } else {
+        const float* p = lds + (q * 16 + h * 8) * G::pitch + row0 + c;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) f[s] = p[s * G::pitch];
+    }
+}
+
+__device__ __forceinline__ int xcd_remap(int bid, int nblk) {
+    // Hardware deals workgroup ids round-robin over the 8 XCDs; give each XCD
+    // a contiguous range of logical ids instead (only when it divides evenly).
+    if ((nblk & 7) == 0) return (bid & 7) * (nblk >> 3) + (bid >> 3);
+    return bid;
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int LA, int LB>
+__global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64)
+gemm_f32_mfma(GemmParams p) {
+    constexpr int WAVES_N = BN / WN;
+    constexpr int NT = (BM / WM) * WAVES_N * 64;
+    constexpr int MB = WM / 32, NB = WN / 32;
+    static_assert(BK % 16 == 0, "BK must be a multiple of 16");
+    static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be 32-aligned");
+    using GA = TileGeom<LA, BM, BK, NT>;
+    using GB = TileGeom<LB, BN, BK, NT>;
+
+    __shared__ __attribute__((aligned(16))) float smem[2 * (GA::lds_floats + GB::lds_floats)];
+
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+
+    // ---- workgroup -> (tile, split, batch) ------------------------------
+    const int bid = xcd_remap(blockIdx.x, gridDim.x);
+    const int ntiles = p.tiles_m * p.tiles_n;
+    const int tile = bid % ntiles;
+    const int rest = bid / ntiles;
+    const int split = rest % p.splits;
+    const int bz = rest / p.splits;
+    int tm, tn;
+    {
+        const int per_group = p.group_m * p.tiles_n;
+        const int g = tile / per_group;
+        const int first = g * p.group_m;
+        const int gsz = min(p.tiles_m - first, p.group_m);
+        const int in_g = tile - g * per_group;
+        tm = first + in_g % gsz;
+        tn = in_g / gsz;
+    }
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int k_begin = split * p.k_per_split;
+    const int k_end = min(p.K, k_begin + p.k_per_split);
+    const int nk = k_end > k_begin ? (k_end - k_begin + BK - 1) / BK : 0;
+
+    TileLoader<LA, BM, BK, NT> la;
+    TileLoader<LB, BN, BK, NT> lb;
+    la.init(p.A + (int64_t)bz * p.a_b, p.a_mn, p.a_k, p.M, m0, k_begin, t);
+    lb.init(p.B + (int64_t)bz * p.b_b, p.b_mn, p.b_k, p.N, n0, k_begin, t);
+
+    f32x16 acc[MB][NB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    float* const As0 = smem;
+    float* const Bs0 = smem + GA::lds_floats;
+    float* const As1 = Bs0 + GB::lds_floats;
+    float* const Bs1 = As1 + GA::lds_floats;
+
+    if (nk > 0) {
+        la.load(k_begin, k_end);
+        lb.load(k_begin, k_end);
+        la.store(As0);
+        lb.store(Bs0);
+        __syncthreads();
+
+        for (int kt = 0; kt < nk; ++kt) {
+            const bool more = kt + 1 < nk;
+            const float* Acur = (kt & 1) ? As1 : As0;
+            const float* Bcur = (kt & 1) ? Bs1 : Bs0;
+            if (more) {
+                la.load(k_begin + (kt + 1) * BK, k_end);
+                lb.load(k_begin + (kt + 1) * BK, k_end);
+            }
+#pragma unroll
+            for (int q = 0; q < BK / 16; ++q) {
+                float fa[MB][8], fb[NB][8];
+#pragma unroll
+                for (int i = 0; i < MB; ++i)
+                    read_frag<LA, BM, BK, NT>(Acur, wm * WM + i * 32, q, lane, fa[i]);
+#pragma unroll
+                for (int j = 0; j < NB; ++j)
+                    read_frag<LB, BN, BK, NT>(Bcur, wn * WN + j * 32, q, lane, fb[j]);
+#pragma unroll
+                for (int s = 0; s < 8; ++s)
+#pragma unroll
+                    for (int i = 0; i < MB; ++i)
+#pragma unroll
+                        for (int j = 0; j < NB; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                                fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
+            }
+            if (more) {
+                la.store((kt & 1) ? As0 : As1);
+                lb.store((kt & 1) ? Bs0 : Bs1);
+            }
+            __syncthreads();
+        }
+    }
+
+    // ---- epilogue ---------------------------------------------------------
+    const int h = lane >> 5, c = lane & 31;
+    if (p.splits > 1) {
+        float* W = p.ws + ((int64_t)split * p.batch + bz) * (int64_t)p.M * p.N;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int n = n0 + wn * WN + j * 32 + c;
+            if (n >= p.N) continue;
+#pragma unroll
+            for (int i = 0; i < MB; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                    if (m < p.M) W[(int64_t)m * p.N + n] = acc[i][j][r];
+                }
+        }
+        return;
+    }
+
+    float* Cb = p.C + (int64_t)bz * p.c_b;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        const int n = n0 + wn * WN + j * 32 + c;
+        if (n >= p.N) continue;
+        int64_t coff;
+        if (p.c_n_inner >= p.N) {
+            coff = (int64_t)n * p.c_n;
+        } else {
+            const int64_t no = n / p.c_n_inner, ni = n - no * p.c_n_inner;
+            coff = no * p.c_n_outer + ni * p.c_n;
+        }
+        const float bcol = (p.bias_axis == 2) ? p.bias[(int64_t)n * p.bias_stride] : 0.f;
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (m >= p.M) continue;
+                float v = acc[i][j][r] + bcol;
+                if (p.bias_axis == 1) v += p.bias[(int64_t)m * p.bias_stride];
+                float* dst = Cb + (int64_t)m * p.c_m + coff;
+                if (p.beta != 0.f) v += p.beta * *dst;
+                *dst = v;
+            }
+    }
+}
+
+}  // namespace mtk

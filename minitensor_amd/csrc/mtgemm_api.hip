@@ -1,0 +1,478 @@
+// mtgemm_api.hip -- the C ABI of include/mtgemm.h: argument checking, operand
+// layout classification, the tile / split-K plan, and the small companion
+// kernels (split-K reduction, column sums, im2col).
+//
+// Reference interfaces replaced (all reference citations are paths inside
+// dionkadi/miniTensor):
+//   mt_gemm_f32      <- matmul_gpu / matmul_gpu_v2 / matmul_gpu_bk16 /
+//                       matmul_gpu_strided (src/gpu_ops.cpp:1103-1144, 1167-1223)
+//                       and bmm's per-batch loop (include/TensorOps.hpp:933-991)
+//   mt_colsum_f32    <- sum_gpu over axis 0 used by unbroadcast for the Linear
+//                       bias gradient (src/gpu_ops.cpp:1306-1348)
+//   mt_linear_*      <- Linear::forward (include/Module.hpp:112-114) and
+//                       MatmulBackward (include/Autograd.hpp:117-147)
+//   mt_conv2d_fwd_f32 <- conv2d_gpu (src/gpu_ops.cpp:2237-2325)
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+
+#include "gemm_configs.hpp"
+#include "mtgemm.h"
+
+using namespace mtk;
+
+namespace {
+
+constexpr int64_t kMaxDim = (int64_t)1 << 31;  // M, N, K and batch are 32-bit inside kernels
+
+thread_local char g_last_config[160] = "none";
+
+hipError_t capture_safe_last_error() {
+    // A launch inside stream capture reports hipErrorStreamCaptureUnsupported
+    // from hipGetLastError even when it was recorded correctly (the reference
+    // treats it the same way, include/GpuUtils.hpp:69-73).
+    hipError_t e = hipGetLastError();
+    return e == hipErrorStreamCaptureUnsupported ? hipSuccess : e;
+}
+
+int device_cu_count() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int v = cache[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+        cus = 256;
+    cache[dev].store(cus, std::memory_order_relaxed);
+    return cus;
+}
+
+bool valid_mat(const mt_mat_f32* X) {
+    if (!X) return false;
+    if (X->rows < 0 || X->cols < 0 || X->batch < 1) return false;
+    if (X->row_stride < 0 || X->col_stride < 0 || X->batch_stride < 0 || X->offset < 0) return false;
+    if (X->rows >= kMaxDim || X->cols >= kMaxDim || X->batch >= kMaxDim) return false;
+    return true;
+}
+
+// Layout mode of one operand in (mn, k) coordinates; see gemm_kernel.hpp.
+int classify(const float* p, int64_t s_mn, int64_t s_k, int64_t MN, int64_t K, int64_t s_b,
+             bool batched) {
+    const bool aligned = ((uintptr_t)p & 15u) == 0 && (!batched || (s_b & 3) == 0);
+    const bool kc = (s_k == 1) || (K == 1);
+    const bool mc = (s_mn == 1) || (MN == 1);
+    if (kc && aligned && (K & 3) == 0 && (MN == 1 || (s_mn & 3) == 0)) return L_KV;
+    if (mc && aligned && (MN & 3) == 0 && (K == 1 || (s_k & 3) == 0)) return L_MV;
+    if (s_k == 1) return L_KS;
+    if (s_mn == 1) return L_MS;
+    return s_k <= s_mn ? L_KS : L_MS;
+}
+
+const char* layout_name(int l) {
+    switch (l) {
+        case L_KV: return "kv";
+        case L_MV: return "mv";
+        case L_KS: return "ks";
+        default: return "ms";
+    }
+}
+
+struct Plan {
+    int cfg = 0;
+    int splits = 1;
+    int kps = 0;
+    int tiles_m = 0, tiles_n = 0;
+    size_t ws_bytes = 0;
+};
+
+constexpr int kBM[kNumCfg] = {TileCfg<0>::BM, TileCfg<1>::BM, TileCfg<2>::BM};
+constexpr int kBN[kNumCfg] = {TileCfg<0>::BN, TileCfg<1>::BN, TileCfg<2>::BN};
+constexpr int kBK = 16;
+static_assert(TileCfg<0>::BK == kBK && TileCfg<1>::BK == kBK && TileCfg<2>::BK == kBK,
+              "split-K granularity assumes one BK for all configurations");
+
+// Cost model (in CU cycles) used to pick the tile configuration and split-K
+// factor.  Work per workgroup is priced at the CU's fp32 MFMA rate (256
+// flop/clk) with a per-configuration efficiency; each round of resident
+// workgroups pays a fixed latency; split-K pays for its partial traffic.
+struct CostModel {
+    double eff[kNumCfg] = {0.85, 0.75, 0.55};
+    int occ[kNumCfg] = {1, 2, 4};            // resident workgroups per CU
+    double round_latency = 3000.0;           // cycles of fill/drain per round
+    double bytes_per_cycle = 2500.0;         // device HBM bytes per CU-clock
+    double launch_cycles = 6000.0;           // second (reduce) launch
+};
+
+Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool allow_split) {
+    static const CostModel cm;
+    static const int kSplits[] = {1, 2, 3, 4, 6, 8, 12, 16};
+    Plan best;
+    double best_t = 1e300;
+    for (int cfg = 0; cfg < kNumCfg; ++cfg) {
+        const int64_t tm = (M + kBM[cfg] - 1) / kBM[cfg];
+        const int64_t tn = (N + kBN[cfg] - 1) / kBN[cfg];
+        const int64_t tiles = tm * tn * batch;
+        for (int s : kSplits) {
+            if (s > 1 && !allow_split) break;
+            int64_t kps = K > 0 ? ((K + s - 1) / s + kBK - 1) / kBK * kBK : kBK;
+            if (s > 1 && kps < 64) break;
+            const int64_t splits = K > 0 ? (K + kps - 1) / kps : 1;
+            if (splits != s) continue;
+            const int64_t wgs = tiles * splits;
+            if (wgs * 512 >= ((int64_t)1 << 32)) continue;
+            const double per_cu = std::ceil((double)wgs / cus);
+            const double rounds = std::ceil((double)wgs / ((double)cus * cm.occ[cfg]));
+            const double work = (double)kBM[cfg] * kBN[cfg] * (double)std::max<int64_t>(kps, kBK) * 2.0 /
+                                (256.0 * cm.eff[cfg]);
+            double t = per_cu * work + rounds * cm.round_latency;
+            if (splits > 1) {
+                const double bytes = (double)(2 * splits + 1) * M * N * batch * 4.0;
+                t += bytes / (cm.bytes_per_cycle) + cm.launch_cycles;
+            }
+            if (t < best_t) {
+                best_t = t;
+                best.cfg = cfg;
+                best.splits = (int)splits;
+                best.kps = (int)kps;
+                best.tiles_m = (int)tm;
+                best.tiles_n = (int)tn;
+                best.ws_bytes = splits > 1 ? (size_t)splits * batch * M * N * sizeof(float) : 0;
+            }
+        }
+    }
+    return best;
+}
+
+GemmLaunchFn pick_launcher(int cfg, int la, int lb) {
+    switch (cfg) {
+        case 0: return launcher_cfg0(la, lb);
+        case 1: return launcher_cfg1(la, lb);
+        default: return launcher_cfg2(la, lb);
+    }
+}
+
+// Checks the three operands and derives the problem sizes.
+int check_gemm(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C,
+               int64_t* M, int64_t* N, int64_t* K, int64_t* batch) {
+    if (!valid_mat(A) || !valid_mat(B) || !valid_mat(C)) return MT_ERR_INVALID;
+    if (A->cols != B->rows || C->rows != A->rows || C->cols != B->cols) return MT_ERR_INVALID;
+    *M = A->rows; *N = B->cols; *K = A->cols; *batch = C->batch;
+    if ((A->batch != 1 && A->batch != *batch) || (B->batch != 1 && B->batch != *batch))
+        return MT_ERR_INVALID;
+    // Two output elements must never share an address.
+    if ((*M > 1 && C->row_stride == 0) || (*N > 1 && C->col_stride == 0) ||
+        (*batch > 1 && C->batch_stride == 0))
+        return MT_ERR_INVALID;
+    const bool c_empty = (*M == 0 || *N == 0);
+    if (!c_empty && !C->base) return MT_ERR_INVALID;
+    if (!c_empty && *K > 0 && (!A->base || !B->base)) return MT_ERR_INVALID;
+    return MT_OK;
+}
+
+// Sum split-K partials in split order, then apply bias and beta: deterministic.
+__global__ void __launch_bounds__(256) splitk_reduce_f32(GemmParams p) {
+    const int64_t MN = (int64_t)p.M * p.N;
+    const int64_t total = MN * p.batch;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t bz = e / MN;
+        const int64_t mn = e - bz * MN;
+        const int m = (int)(mn / p.N);
+        const int n = (int)(mn - (int64_t)m * p.N);
+        float v = 0.f;
+        for (int s = 0; s < p.splits; ++s) v += p.ws[((int64_t)s * p.batch + bz) * MN + mn];
+        if (p.bias_axis == 1) v += p.bias[(int64_t)m * p.bias_stride];
+        else if (p.bias_axis == 2) v += p.bias[(int64_t)n * p.bias_stride];
+        int64_t coff;
+        if (p.c_n_inner >= p.N) {
+            coff = (int64_t)n * p.c_n;
+        } else {
+            const int64_t no = n / p.c_n_inner, ni = n - no * p.c_n_inner;
+            coff = no * p.c_n_outer + ni * p.c_n;
+        }
+        float* dst = p.C + bz * p.c_b + (int64_t)m * p.c_m + coff;
+        if (p.beta != 0.f) v += p.beta * *dst;
+        *dst = v;
+    }
+}
+
+int run_gemm(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C, int64_t c_n_inner,
+             int64_t c_n_outer, const mt_epilogue_f32* ep, void* workspace, size_t ws_bytes,
+             hipStream_t stream) {
+    int64_t M, N, K, batch;
+    int rc = check_gemm(A, B, C, &M, &N, &K, &batch);
+    if (rc != MT_OK) return rc;
+    if (ep && ep->bias_axis != MT_BIAS_NONE) {
+        if (ep->bias_axis != MT_BIAS_ROW && ep->bias_axis != MT_BIAS_COL) return MT_ERR_INVALID;
+        if (!ep->bias || ep->bias_stride < 0) return MT_ERR_INVALID;
+    }
+    if (M == 0 || N == 0) {
+        std::snprintf(g_last_config, sizeof g_last_config, "empty");
+        return MT_OK;
+    }
+
+    GemmParams p{};
+    p.A = A->base ? A->base + A->offset : nullptr;
+    p.a_mn = A->row_stride; p.a_k = A->col_stride; p.a_b = A->batch == 1 ? 0 : A->batch_stride;
+    p.B = B->base ? B->base + B->offset : nullptr;
+    p.b_mn = B->col_stride; p.b_k = B->row_stride; p.b_b = B->batch == 1 ? 0 : B->batch_stride;
+    p.C = const_cast<float*>(C->base) + C->offset;
+    p.c_m = C->row_stride; p.c_n = C->col_stride; p.c_b = C->batch_stride;
+    p.c_n_inner = c_n_inner > 0 ? c_n_inner : N;
+    p.c_n_outer = c_n_outer;
+    p.bias = ep ? ep->bias : nullptr;
+    p.bias_stride = ep ? ep->bias_stride : 0;
+    p.bias_axis = ep ? ep->bias_axis : MT_BIAS_NONE;
+    p.beta = ep ? ep->beta : 0.f;
+    p.M = (int)M; p.N = (int)N; p.K = (int)K; p.batch = (int)batch;
+
+    if (K == 0) {  // nothing to load: a K-free pass writes bias (+beta*C) or zeros
+        p.A = p.B = nullptr;
+    }
+    const int la = K == 0 ? L_KS : classify(p.A, p.a_mn, p.a_k, M, K, p.a_b, p.a_b != 0);
+    const int lb = K == 0 ? L_KS : classify(p.B, p.b_mn, p.b_k, N, K, p.b_b, p.b_b != 0);
+
+    Plan plan = make_plan(M, N, K, batch, device_cu_count(), true);
+    if (plan.splits > 1 && (workspace == nullptr || ws_bytes < plan.ws_bytes))
+        plan = make_plan(M, N, K, batch, device_cu_count(), false);
+    p.splits = plan.splits;
+    p.k_per_split = plan.splits > 1 ? plan.kps : (int)std::max<int64_t>(K, 1);
+    p.tiles_m = plan.tiles_m;
+    p.tiles_n = plan.tiles_n;
+    p.group_m = 4;
+    p.ws = plan.splits > 1 ? static_cast<float*>(workspace) : nullptr;
+
+    const int64_t nblocks = (int64_t)plan.tiles_m * plan.tiles_n * plan.splits * batch;
+    if (nblocks >= ((int64_t)1 << 31)) return MT_ERR_UNSUPPORTED;
+    std::snprintf(g_last_config, sizeof g_last_config, "%dx%d a=%s b=%s split=%d wgs=%lld",
+                  kBM[plan.cfg], kBN[plan.cfg], layout_name(la), layout_name(lb), plan.splits,
+                  (long long)nblocks);
+
+    hipError_t e = pick_launcher(plan.cfg, la, lb)(p, (unsigned)nblocks, stream);
+    if (e == hipErrorStreamCaptureUnsupported) e = hipSuccess;
+    if (e != hipSuccess) return MT_ERR_HIP;
+    if (plan.splits > 1) {
+        const int64_t total = M * N * batch;
+        const int64_t blocks = std::min<int64_t>((total + 255) / 256, 65536);
+        hipLaunchKernelGGL(splitk_reduce_f32, dim3((unsigned)blocks), dim3(256), 0, stream, p);
+        if (capture_safe_last_error() != hipSuccess) return MT_ERR_HIP;
+    }
+    return MT_OK;
+}
+
+size_t gemm_ws(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C) {
+    int64_t M, N, K, batch;
+    if (check_gemm(A, B, C, &M, &N, &K, &batch) != MT_OK || M == 0 || N == 0) return 0;
+    return make_plan(M, N, K, batch, device_cu_count(), true).ws_bytes;
+}
+
+// ---- column sums (Linear bias gradient) ------------------------------------
+// 64 columns per workgroup, 4 row groups summed in a fixed order.
+__global__ void __launch_bounds__(256)
+colsum_f32(const float* X, int64_t rs, int64_t cs, int R, int Cn, float* out, int64_t os,
+           float beta) {
+    __shared__ float part[4][64];
+    const int cl = threadIdx.x & 63, g = threadIdx.x >> 6;
+    const int c = blockIdx.x * 64 + cl;
+    float s = 0.f;
+    if (c < Cn)
+        for (int r = g; r < R; r += 4) s += X[(int64_t)r * rs + (int64_t)c * cs];
+    part[g][cl] = s;
+    __syncthreads();
+    if (g == 0 && c < Cn) {
+        const float v = ((part[0][cl] + part[1][cl]) + part[2][cl]) + part[3][cl];
+        float* d = out + (int64_t)c * os;
+        *d = (beta != 0.f ? beta * *d : 0.f) + v;
+    }
+}
+
+// ---- im2col: col[k][np], k = (c*kh + r)*kw + s, np = (img*Ho + oh)*Wo + ow --
+// Each thread owns one np column and walks KCHUNK consecutive k rows, so the
+// np decomposition is done once and the stores are coalesced along np.
+constexpr int kIm2colK = 32;
+__global__ void __launch_bounds__(256)
+im2col_f32(const float* in, float* col, int C, int H, int W, int kh, int kw, int st, int pad,
+           int Ho, int Wo, int64_t NP, int64_t Kg) {
+    const int64_t np = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (np >= NP) return;
+    const int64_t hw = (int64_t)Ho * Wo;
+    const int64_t img = np / hw;
+    const int rem = (int)(np - img * hw);
+    const int oh = rem / Wo, ow = rem - oh * Wo;
+    const int iy0 = oh * st - pad, ix0 = ow * st - pad;
+    const float* src = in + img * (int64_t)C * H * W;
+    int64_t k = (int64_t)blockIdx.y * kIm2colK;
+    const int64_t kend = std::min<int64_t>(Kg, k + kIm2colK);
+    int s = (int)(k % kw);
+    int r = (int)((k / kw) % kh);
+    int c = (int)(k / ((int64_t)kw * kh));
+    for (; k < kend; ++k) {
+        const int iy = iy0 + r, ix = ix0 + s;
+        float v = 0.f;
+        if (iy >= 0 && iy < H && ix >= 0 && ix < W) v = src[((int64_t)c * H + iy) * W + ix];
+        col[k * NP + np] = v;
+        if (++s == kw) { s = 0; if (++r == kh) { r = 0; ++c; } }
+    }
+}
+
+bool conv_dims(const mt_conv2d_desc* d, int64_t* Ho, int64_t* Wo) {
+    if (!d) return false;
+    if (d->n < 0 || d->c_in < 0 || d->h < 0 || d->w < 0 || d->c_out < 0 || d->kh < 1 ||
+        d->kw < 1 || d->stride < 1 || d->pad < 0)
+        return false;
+    *Ho = (d->h + 2 * d->pad < d->kh) ? 0 : (d->h + 2 * d->pad - d->kh) / d->stride + 1;
+    *Wo = (d->w + 2 * d->pad < d->kw) ? 0 : (d->w + 2 * d->pad - d->kw) / d->stride + 1;
+    const int64_t kg = d->c_in * d->kh * d->kw;
+    const int64_t np = d->n * *Ho * *Wo;
+    if (kg >= kMaxDim || np >= kMaxDim || d->c_out >= kMaxDim) return false;
+    if (d->h >= kMaxDim || d->w >= kMaxDim) return false;
+    return true;
+}
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+void conv_gemm_views(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, const float* weight,
+                     const float* col, float* output, mt_mat_f32* A, mt_mat_f32* B,
+                     mt_mat_f32* C) {
+    const int64_t kg = d->c_in * d->kh * d->kw, np = d->n * Ho * Wo;
+    *A = mt_mat_f32{weight, 0, d->c_out, kg, kg, 1, 1, 0};
+    *B = mt_mat_f32{col, 0, kg, np, np, 1, 1, 0};
+    // C(m = c_out, n = np) -> output[img][c_out][hw]; the column scatter is
+    // passed separately (inner extent Ho*Wo, outer stride c_out*Ho*Wo).
+    *C = mt_mat_f32{output, 0, d->c_out, np, Ho * Wo, 1, 1, 0};
+}
+
+}  // namespace
+
+extern "C" {
+
+int mt_gemm_f32(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C,
+                const mt_epilogue_f32* ep, void* workspace, size_t ws_bytes, void* stream) {
+    return run_gemm(A, B, C, 0, 0, ep, workspace, ws_bytes, static_cast<hipStream_t>(stream));
+}
+
+size_t mt_gemm_workspace_f32(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C) {
+    return gemm_ws(A, B, C);
+}
+
+int mt_colsum_f32(const mt_mat_f32* X, float* out, int64_t out_stride, float beta, void* stream) {
+    if (!valid_mat(X) || X->batch != 1 || out_stride < 0) return MT_ERR_INVALID;
+    if (X->cols == 0) return MT_OK;
+    if (!out || (X->cols > 1 && out_stride == 0)) return MT_ERR_INVALID;
+    if (X->rows > 0 && !X->base) return MT_ERR_INVALID;
+    const unsigned blocks = (unsigned)((X->cols + 63) / 64);
+    hipLaunchKernelGGL(colsum_f32, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       X->base ? X->base + X->offset : nullptr, X->row_stride, X->col_stride,
+                       (int)X->rows, (int)X->cols, out, out_stride, beta);
+    return capture_safe_last_error() == hipSuccess ? MT_OK : MT_ERR_HIP;
+}
+
+// Linear views: X [B,in], W [out,in].  Wᵀ is W with its strides swapped.
+static mt_mat_f32 transposed(const mt_mat_f32& X) {
+    mt_mat_f32 t = X;
+    t.rows = X.cols; t.cols = X.rows;
+    t.row_stride = X.col_stride; t.col_stride = X.row_stride;
+    return t;
+}
+
+int mt_linear_forward_f32(const mt_mat_f32* X, const mt_mat_f32* W, const float* bias,
+                          int64_t bias_stride, const mt_mat_f32* Y, void* workspace,
+                          size_t ws_bytes, void* stream) {
+    if (!valid_mat(X) || !valid_mat(W) || !valid_mat(Y)) return MT_ERR_INVALID;
+    const mt_mat_f32 Wt = transposed(*W);
+    mt_epilogue_f32 ep{bias, bias_stride, bias ? MT_BIAS_COL : MT_BIAS_NONE, 0.f};
+    return run_gemm(X, &Wt, Y, 0, 0, &ep, workspace, ws_bytes, static_cast<hipStream_t>(stream));
+}
+
+size_t mt_linear_workspace_f32(int64_t rows, int64_t in_f, int64_t out_f) {
+    if (rows < 0 || in_f < 0 || out_f < 0) return 0;
+    const int cus = device_cu_count();
+    size_t ws = 0;
+    if (rows > 0 && out_f > 0) ws = std::max(ws, make_plan(rows, out_f, in_f, 1, cus, true).ws_bytes);
+    if (rows > 0 && in_f > 0) ws = std::max(ws, make_plan(rows, in_f, out_f, 1, cus, true).ws_bytes);
+    if (out_f > 0 && in_f > 0) ws = std::max(ws, make_plan(out_f, in_f, rows, 1, cus, true).ws_bytes);
+    return ws;
+}
+
+int mt_linear_backward_f32(const mt_mat_f32* dY, const mt_mat_f32* X, const mt_mat_f32* W,
+                           const mt_mat_f32* dX, const mt_mat_f32* dW, float beta_w, float* db,
+                           int64_t db_stride, float beta_b, void* workspace, size_t ws_bytes,
+                           void* stream) {
+    if (!valid_mat(dY) || !valid_mat(X) || !valid_mat(W)) return MT_ERR_INVALID;
+    if (dY->rows != X->rows || dY->cols != W->rows || X->cols != W->cols) return MT_ERR_INVALID;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (dX) {  // dX[B,in] = dY[B,out] · W[out,in]
+        int rc = run_gemm(dY, W, dX, 0, 0, nullptr, workspace, ws_bytes, s);
+        if (rc != MT_OK) return rc;
+    }
+    if (dW) {  // dW[out,in] = dYᵀ[out,B] · X[B,in] (+ beta_w·dW)
+        const mt_mat_f32 dYt = transposed(*dY);
+        mt_epilogue_f32 ep{nullptr, 0, MT_BIAS_NONE, beta_w};
+        int rc = run_gemm(&dYt, X, dW, 0, 0, &ep, workspace, ws_bytes, s);
+        if (rc != MT_OK) return rc;
+    }
+    if (db) {
+        int rc = mt_colsum_f32(dY, db, db_stride, beta_b, stream);
+        if (rc != MT_OK) return rc;
+    }
+    return MT_OK;
+}
+
+size_t mt_conv2d_workspace_f32(const mt_conv2d_desc* d) {
+    int64_t Ho, Wo;
+    if (!conv_dims(d, &Ho, &Wo)) return 0;
+    const int64_t kg = d->c_in * d->kh * d->kw, np = d->n * Ho * Wo;
+    if (np == 0 || d->c_out == 0) return 0;
+    const size_t col = align_up((size_t)kg * np * sizeof(float), 256);
+    return col + make_plan(d->c_out, np, kg, 1, device_cu_count(), true).ws_bytes;
+}
+
+int mt_conv2d_fwd_f32(const mt_conv2d_desc* d, const float* input, const float* weight,
+                      const float* bias, float* output, void* workspace, size_t ws_bytes,
+                      void* stream) {
+    int64_t Ho, Wo;
+    if (!conv_dims(d, &Ho, &Wo)) return MT_ERR_INVALID;
+    const int64_t kg = d->c_in * d->kh * d->kw, np = d->n * Ho * Wo;
+    if (np == 0 || d->c_out == 0) return MT_OK;
+    if (!output || (kg > 0 && (!input || !weight))) return MT_ERR_INVALID;
+    const size_t col_bytes = align_up((size_t)kg * np * sizeof(float), 256);
+    if (kg > 0 && (!workspace || ws_bytes < col_bytes)) return MT_ERR_WORKSPACE;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    float* col = static_cast<float*>(workspace);
+    if (kg > 0) {
+        dim3 grid((unsigned)((np + 255) / 256), (unsigned)((kg + kIm2colK - 1) / kIm2colK));
+        hipLaunchKernelGGL(im2col_f32, grid, dim3(256), 0, s, input, col, (int)d->c_in, (int)d->h,
+                           (int)d->w, (int)d->kh, (int)d->kw, (int)d->stride, (int)d->pad, (int)Ho,
+                           (int)Wo, np, kg);
+        if (capture_safe_last_error() != hipSuccess) return MT_ERR_HIP;
+    }
+    mt_mat_f32 A, B, C;
+    conv_gemm_views(d, Ho, Wo, weight, col, output, &A, &B, &C);
+    mt_epilogue_f32 ep{bias, 1, bias ? MT_BIAS_ROW : MT_BIAS_NONE, 0.f};
+    char* gws = static_cast<char*>(workspace) + (kg > 0 ? col_bytes : 0);
+    const size_t gws_bytes = ws_bytes > col_bytes ? ws_bytes - col_bytes : 0;
+    return run_gemm(&A, &B, &C, Ho * Wo, d->c_out * Ho * Wo, &ep, gws, gws_bytes, s);
+}
+
+const char* mt_strerror(int status) {
+    switch (status) {
+        case MT_OK: return "success";
+        case MT_ERR_INVALID: return "invalid argument";
+        case MT_ERR_WORKSPACE: return "workspace missing or too small";
+        case MT_ERR_HIP: return "HIP runtime error";
+        case MT_ERR_UNSUPPORTED: return "unsupported request";
+        default: return "unknown status";
+    }
+}
+
+int mt_version(void) { return MTGEMM_VERSION; }
+
+const char* mt_last_config(void) { return g_last_config; }
+
+}  // extern "C"

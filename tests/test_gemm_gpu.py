@@ -1,0 +1,234 @@
+"""GPU parity of mt_gemm_f32 against the CPU oracle (the reference's matmul_cpu /
+matmul_cpu_strided restated in oracle/oracle.c) on identical seeded inputs.
+
+Bound: max|err| <= 1e-5·√K·max|A|·max|B| (tests/util_parity.py).
+"""
+import numpy as np
+import pytest
+import torch
+
+import minitensor_amd as mt
+import oracle
+from util_parity import amax, assert_close
+
+pytestmark = pytest.mark.gpu
+
+
+def to_gpu(a: np.ndarray, dev) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def run(A: torch.Tensor, B: torch.Tensor, **kw) -> np.ndarray:
+    C = mt.gemm(A, B, **kw)
+    torch.cuda.synchronize()
+    print(f"[config] {mt.last_config()}", flush=True)
+    return C.cpu().numpy()
+
+
+def test_known_answer_2x3x2(dev):
+    # reference test/tensor_test.cpp:258-316 (CPU and GPU matmul)
+    a = np.array([[1, 2, 3], [4, 5, 6]], np.float32)
+    b = np.array([[7, 8], [9, 10], [11, 12]], np.float32)
+    c = run(to_gpu(a, dev), to_gpu(b, dev))
+    np.testing.assert_array_equal(c, np.array([[58, 64], [139, 154]], np.float32))
+
+
+def test_fill_2_and_3(dev):
+    # reference test/engien_test.cpp:80-96: 2x3 of 2s times 3x2 of 3s = 18 everywhere
+    c = run(torch.full((2, 3), 2.0, device=dev), torch.full((3, 2), 3.0, device=dev))
+    np.testing.assert_array_equal(c, np.full((2, 2), 18.0, np.float32))
+
+
+def test_config1_mlp_linear_shape(dev):
+    # C[256,512] = A[256,512]·B[512,512], U(-1,1), seeds 42/43
+    a = oracle.uniform((256, 512), 42)
+    b = oracle.uniform((512, 512), 43)
+    c = run(to_gpu(a, dev), to_gpu(b, dev))
+    assert_close(c, oracle.matmul(a, b), 512, amax(a), amax(b), "C1 256x512x512")
+
+
+@pytest.mark.parametrize("M,N,K", [
+    (257, 511, 383),   # every tail at once (reference benchmark shape)
+    (1, 4096, 4096),   # GEMV row
+    (4096, 1, 4096),   # GEMV column
+    (4096, 4096, 1),   # outer product (K = 1)
+    (63, 4096, 64),
+    (130, 70, 33),
+    (5, 7, 3),
+    (256, 256, 4099),  # K tail with split-K
+    (64, 64, 8192),    # skinny output, deep K: split-K
+])
+def test_shapes_and_tails(dev, M, N, K):
+    a = oracle.uniform((M, K), 7 + M)
+    b = oracle.uniform((K, N), 11 + N)
+    c = run(to_gpu(a, dev), to_gpu(b, dev))
+    assert_close(c, oracle.matmul(a, b), K, amax(a), amax(b), f"{M}x{N}x{K}")
+
+
+def test_k_zero_gives_zeros_and_bias(dev):
+    # reference F6b: K = 0 must give zeros (the reference v2 kernel reads an
+    # uninitialised LDS buffer); with a fused bias it gives the bias.
+    A = torch.empty((33, 0), device=dev)
+    B = torch.empty((0, 17), device=dev)
+    c = run(A, B)
+    np.testing.assert_array_equal(c, np.zeros((33, 17), np.float32))
+    bias = torch.arange(17, dtype=torch.float32, device=dev)
+    c = run(A, B, bias=bias, bias_axis=mt.BIAS_COL)
+    np.testing.assert_array_equal(c, np.broadcast_to(np.arange(17, dtype=np.float32), (33, 17)))
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("M,N,K", [(300, 260, 200), (64, 96, 32), (512, 512, 512)])
+def test_transpose_views(dev, ta, tb, M, N, K):
+    # NN / NT / TN / TT through transpose views (strides swapped, not materialised),
+    # as MatmulBackward hands them over (reference include/Autograd.hpp:124-142).
+    a = oracle.normal((M, K), 42)
+    b = oracle.normal((K, N), 43)
+    A = to_gpu(a.T.copy(), dev).t() if ta else to_gpu(a, dev)
+    B = to_gpu(b.T.copy(), dev).t() if tb else to_gpu(b, dev)
+    assert A.is_contiguous() != ta and B.is_contiguous() != tb
+    c = run(A, B)
+    a_view = a.T.copy().T if ta else a
+    b_view = b.T.copy().T if tb else b
+    assert_close(c, oracle.matmul(a_view, b_view), K, amax(a), amax(b), f"ta={ta} tb={tb}")
+
+
+def test_row_slice_offset(dev):
+    # reference F1: a row slice is "contiguous" with offset != 0; the reference
+    # GPU path drops the offset, this backend honours it.
+    a = oracle.normal((300, 96), 42)
+    b = oracle.normal((96, 130), 43)
+    A = to_gpu(a, dev)[37:]
+    assert A.storage_offset() == 37 * 96
+    c = run(A, to_gpu(b, dev))
+    assert_close(c, oracle.matmul(a[37:], b), 96, amax(a), amax(b), "slice rows 37:")
+
+
+@pytest.mark.parametrize("off", [1, 2, 3])
+def test_unaligned_offsets_take_scalar_path(dev, off):
+    a = oracle.uniform((200 * 64 + 8,), 5)
+    b = oracle.uniform((64 * 72 + 8,), 6)
+    A = to_gpu(a, dev)[off:off + 200 * 64].view(200, 64)
+    B = to_gpu(b, dev)[off:off + 64 * 72].view(64, 72)
+    c = run(A, B)
+    assert "ks" in mt.last_config() or "ms" in mt.last_config()
+    av = a[off:off + 200 * 64].reshape(200, 64)
+    bv = b[off:off + 64 * 72].reshape(64, 72)
+    assert_close(c, oracle.matmul(av, bv), 64, amax(av), amax(bv), f"offset {off}")
+
+
+def test_expand_stride_zero(dev):
+    # expand views (stride 0, reference include/TensorImpl.hpp:204-228)
+    row = oracle.uniform((1, 128), 3)
+    col = oracle.uniform((96, 1), 4)
+    A = to_gpu(row, dev).expand(80, 128)           # [80,128] strides (0,1)
+    B = to_gpu(col, dev).expand(96, 128)           # [96,128] strides (1,0)
+    assert A.stride() == (0, 1) and B.stride() == (1, 0)
+    c = run(A[:, :96], B)
+    av = np.broadcast_to(row, (80, 128))[:, :96]
+    bv = np.broadcast_to(col, (96, 128))
+    assert_close(c, oracle.matmul(av, bv), 96, amax(av), amax(bv), "expand")
+
+
+def test_doubly_strided_views(dev):
+    # every-other-column and every-third-row views: no unit stride anywhere
+    a = oracle.normal((150, 200), 8)
+    b = oracle.normal((300, 90), 9)
+    A = to_gpu(a, dev)[::2, ::2]        # [75,100] strides (400,2)
+    B = to_gpu(b, dev)[::3]             # [100,90] strides (270,1)
+    Bs = B[:, ::2]                      # [100,45] strides (270,2)
+    c = run(A, Bs)
+    av, bv = a[::2, ::2], b[::3][:, ::2]
+    assert_close(c, oracle.matmul(av, bv), 100, amax(av), amax(bv), "doubly strided")
+
+
+@pytest.mark.parametrize("axis", [mt.BIAS_ROW, mt.BIAS_COL])
+def test_bias_epilogue(dev, axis):
+    a = oracle.uniform((200, 300), 1)
+    b = oracle.uniform((300, 170), 2)
+    bias = oracle.uniform((200 if axis == mt.BIAS_ROW else 170,), 3)
+    c = run(to_gpu(a, dev), to_gpu(b, dev), bias=to_gpu(bias, dev), bias_axis=axis)
+    want = oracle.matmul(a, b) + (bias[:, None] if axis == mt.BIAS_ROW else bias[None, :])
+    assert_close(c, want, 300, amax(a), amax(b), f"bias axis {axis}", extra=1e-6)
+
+
+def test_beta_accumulate(dev):
+    a = oracle.uniform((128, 256), 1)
+    b = oracle.uniform((256, 192), 2)
+    c0 = oracle.uniform((128, 192), 3)
+    C = to_gpu(c0, dev)
+    mt.gemm(to_gpu(a, dev), to_gpu(b, dev), out=C, beta=1.0)
+    torch.cuda.synchronize()
+    assert_close(C.cpu().numpy(), oracle.matmul(a, b) + c0, 256, amax(a), amax(b), "beta=1",
+                 extra=1e-6)
+
+
+def test_split_k_is_deterministic(dev):
+    a = oracle.uniform((64, 8192), 21)
+    b = oracle.uniform((8192, 64), 22)
+    A, B = to_gpu(a, dev), to_gpu(b, dev)
+    c1 = run(A, B)
+    assert "split=1 " not in mt.last_config() + " "
+    c2 = run(A, B)
+    np.testing.assert_array_equal(c1, c2)
+
+
+def test_batched_config5b(dev):
+    # BASELINE config 5b: [64]x[512,64]·[64,512], U(-1,1) seeds 42/43; one launch
+    a = oracle.uniform((64, 512, 64), 42)
+    b = oracle.uniform((64, 64, 512), 43)
+    c = mt.bmm(to_gpu(a, dev), to_gpu(b, dev))
+    torch.cuda.synchronize()
+    assert_close(c.cpu().numpy(), oracle.bmm(a, b), 64, amax(a), amax(b), "C5b bmm")
+
+
+def test_batched_shared_weight(dev):
+    # batch stride 0 on A: one weight for every batch entry (conv-style)
+    a = oracle.uniform((1, 96, 80), 1)
+    b = oracle.uniform((7, 80, 50), 2)
+    A = to_gpu(a, dev).expand(7, 96, 80)
+    c = mt.gemm(A, to_gpu(b, dev))
+    torch.cuda.synchronize()
+    assert_close(c.cpu().numpy(), oracle.bmm(np.broadcast_to(a, (7, 96, 80)), b), 80,
+                 amax(a), amax(b), "shared A")
+
+
+def test_config2_4096_properties(dev):
+    # BASELINE config 2 (4096^3): the full oracle would take minutes, so check
+    # (1) 24 sampled rows against the oracle's fp64 brute force over the full K,
+    # (2) the checksum identity C·1 = A·(B·1) in fp64 over all rows.
+    a = oracle.uniform((4096, 4096), 42)
+    b = oracle.uniform((4096, 4096), 43)
+    C = mt.gemm(to_gpu(a, dev), to_gpu(b, dev))
+    torch.cuda.synchronize()
+    print(f"[config] {mt.last_config()}", flush=True)
+    c = C.cpu().numpy()
+    rows = np.linspace(0, 4095, 24).astype(np.int64)
+    assert_close(c[rows], oracle.matmul_f64_rows(a, b, rows), 4096, amax(a), amax(b),
+                 "C2 sampled rows")
+    rowsum = c.astype(np.float64).sum(axis=1)
+    want = a.astype(np.float64) @ b.astype(np.float64).sum(axis=1)
+    err = np.max(np.abs(rowsum - want))
+    bound = 4096 * 1e-5 * 64
+    print(f"[parity] C2 checksum: max|err|={err:.3e} bound={bound:.3e}")
+    assert err <= bound
+
+
+def test_config3_transpose_and_slice_views(dev):
+    # C = A·Bᵀ with B [2048,1024] passed as a transpose view,
+    # and the slice A[128:] (offset 131072); N(0,1) seeds 42/43.  Sampled rows
+    # against the oracle (full K).
+    a = oracle.normal((2048, 1024), 42)
+    b = oracle.normal((2048, 1024), 43)
+    A, B = to_gpu(a, dev), to_gpu(b, dev)
+    rows = np.array([0, 1, 127, 128, 129, 1000, 2047 - 128, 2047], np.int64)
+    c = run(A, B.t())
+    assert_close(c[rows], oracle.matmul_f64_rows(a, b.T, rows), 1024, amax(a), amax(b), "C3a")
+    As = A[128:]
+    assert As.storage_offset() == 131072
+    c = run(As, B.t())
+    r2 = rows[rows < 1920]
+    assert_close(c[r2], oracle.matmul_f64_rows(a[128:], b.T, r2), 1024, amax(a), amax(b), "C3b")
+    # the view result equals the result on materialised copies
+    c_mat = run(As.contiguous(), B.t().contiguous())
+    assert_close(c, c_mat, 1024, amax(a), amax(b), "C3b view == copy")
