@@ -165,11 +165,11 @@ int check_gemm(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C,
     *M = A->rows; *N = B->cols; *K = A->cols; *batch = C->batch;
     if ((A->batch != 1 && A->batch != *batch) || (B->batch != 1 && B->batch != *batch))
         return MT_ERR_INVALID;
-    // Two output elements must never share an address.
-    if ((*M > 1 && C->row_stride == 0) || (*N > 1 && C->col_stride == 0) ||
-        (*batch > 1 && C->batch_stride == 0))
-        return MT_ERR_INVALID;
     const bool c_empty = (*M == 0 || *N == 0);
+    // Two output elements must never share an address.
+    if (!c_empty && ((*M > 1 && C->row_stride == 0) || (*N > 1 && C->col_stride == 0) ||
+                     (*batch > 1 && C->batch_stride == 0)))
+        return MT_ERR_INVALID;
     if (!c_empty && !C->base) return MT_ERR_INVALID;
     if (!c_empty && *K > 0 && (!A->base || !B->base)) return MT_ERR_INVALID;
     return MT_OK;

@@ -1,0 +1,119 @@
+"""CPU tests of the C ABI: the library loads, exports every entry point that
+include/mtgemm.h declares, and rejects invalid arguments before touching the
+GPU (error behaviour of the reference's matmul: include/TensorOps.hpp:995-1005)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+import minitensor_amd as mt
+
+HEADER_DIR = Path(__file__).resolve().parents[1] / "include"
+
+
+def declared_functions():
+    names = set()
+    for h in HEADER_DIR.glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b(mt_\w+)\s*\(", text, re.M))
+    return sorted(names)
+
+
+def test_header_declares_the_abi():
+    names = declared_functions()
+    for n in ["mt_gemm_f32", "mt_gemm_workspace_f32", "mt_conv2d_fwd_f32",
+              "mt_linear_forward_f32", "mt_linear_backward_f32", "mt_colsum_f32"]:
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = mt.lib()
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, f"not exported: {missing}"
+
+
+def test_version_and_strerror():
+    lib = mt.lib()
+    assert lib.mt_version() == 1
+    assert lib.mt_strerror(mt.MT_ERR_INVALID) == b"invalid argument"
+    assert lib.mt_strerror(mt.MT_ERR_WORKSPACE).startswith(b"workspace")
+    assert lib.mt_strerror(12345) == b"unknown status"
+
+
+def M(rows, cols, rs=None, cs=1, batch=1, bs=0, off=0, base=0x1000):
+    return mt.MatF32(base, off, rows, cols, cols if rs is None else rs, cs, batch, bs)
+
+
+BAD = {
+    "inner dimension mismatch": (M(4, 5), M(6, 3), M(4, 3)),
+    "C rows mismatch": (M(4, 5), M(5, 3), M(5, 3)),
+    "C cols mismatch": (M(4, 5), M(5, 3), M(4, 4)),
+    "negative stride": (M(4, 5, rs=-5), M(5, 3), M(4, 3)),
+    "negative offset": (M(4, 5, off=-1), M(5, 3), M(4, 3)),
+    "batch mismatch": (M(4, 5, batch=3, bs=20), M(5, 3, batch=2, bs=15), M(4, 3, batch=3, bs=12)),
+    "zero batch": (M(4, 5), M(5, 3), M(4, 3, batch=0)),
+    "C rows alias (stride 0)": (M(4, 5), M(5, 3), M(4, 3, rs=0)),
+    "C cols alias (stride 0)": (M(4, 5), M(5, 3), M(4, 3, cs=0)),
+    "null C": (M(4, 5), M(5, 3), M(4, 3, base=0)),
+    "null A with K > 0": (M(4, 5, base=0), M(5, 3), M(4, 3)),
+    "dimension too large": (M(1 << 31, 5), M(5, 3), M(1 << 31, 3)),
+}
+
+
+@pytest.mark.parametrize("case", sorted(BAD))
+def test_gemm_rejects_invalid_arguments(case):
+    a, b, c = BAD[case]
+    rc = mt.lib().mt_gemm_f32(a, b, c, None, None, 0, None)
+    assert rc == mt.MT_ERR_INVALID, case
+
+
+def test_gemm_rejects_bad_epilogue():
+    ep = mt.EpilogueF32(None, 1, mt.BIAS_COL, 0.0)
+    rc = mt.lib().mt_gemm_f32(M(4, 5), M(5, 3), M(4, 3), ctypes.byref(ep), None, 0, None)
+    assert rc == mt.MT_ERR_INVALID
+    ep = mt.EpilogueF32(0x2000, 1, 7, 0.0)
+    rc = mt.lib().mt_gemm_f32(M(4, 5), M(5, 3), M(4, 3), ctypes.byref(ep), None, 0, None)
+    assert rc == mt.MT_ERR_INVALID
+
+
+def test_empty_output_is_a_no_op():
+    # M == 0 or N == 0: nothing to launch, success (the reference skips the launch too)
+    assert mt.lib().mt_gemm_f32(M(0, 5), M(5, 3), M(0, 3), None, None, 0, None) == mt.MT_OK
+    assert mt.lib().mt_gemm_f32(M(4, 5), M(5, 0), M(4, 0), None, None, 0, None) == mt.MT_OK
+    assert mt.last_config() == "empty"
+
+
+def test_conv_rejects_invalid_descriptors():
+    lib = mt.lib()
+    for d in [mt.Conv2dDesc(1, 3, 8, 8, 4, 0, 3, 1, 0),    # kh = 0
+              mt.Conv2dDesc(1, 3, 8, 8, 4, 3, 3, 0, 0),    # stride 0
+              mt.Conv2dDesc(-1, 3, 8, 8, 4, 3, 3, 1, 0),   # negative batch
+              mt.Conv2dDesc(1, 3, 8, 8, 4, 3, 3, 1, -1)]:  # negative padding
+        rc = lib.mt_conv2d_fwd_f32(ctypes.byref(d), 0x1000, 0x1000, None, 0x1000, None, 0, None)
+        assert rc == mt.MT_ERR_INVALID
+    # kernel larger than the padded input: the reference's safe_out_size gives 0 -> no work
+    d = mt.Conv2dDesc(1, 3, 2, 2, 4, 5, 5, 1, 0)
+    assert lib.mt_conv2d_workspace_f32(ctypes.byref(d)) == 0
+    assert lib.mt_conv2d_fwd_f32(ctypes.byref(d), 0x1000, 0x1000, None, 0x1000, None, 0,
+                                 None) == mt.MT_OK
+    # a real conv without the im2col workspace is refused
+    d = mt.Conv2dDesc(2, 3, 8, 8, 4, 3, 3, 1, 1)
+    assert lib.mt_conv2d_workspace_f32(ctypes.byref(d)) >= 2 * 27 * 64 * 4
+    assert lib.mt_conv2d_fwd_f32(ctypes.byref(d), 0x1000, 0x1000, None, 0x1000, None, 0,
+                                 None) == mt.MT_ERR_WORKSPACE
+
+
+def test_linear_rejects_mismatched_shapes():
+    lib = mt.lib()
+    rc = lib.mt_linear_backward_f32(M(8, 10), M(8, 6), M(11, 6), None, None, 0.0, None, 0, 0.0,
+                                    None, 0, None)
+    assert rc == mt.MT_ERR_INVALID
+
+
+def test_python_front_end_errors():
+    import torch
+    with pytest.raises(ValueError):
+        mt.matmul(torch.zeros(2, 3), torch.zeros(3, 2))          # CPU tensors: GPU only
+    with pytest.raises(ValueError):
+        mt.conv2d(torch.zeros(1, 1, 3, 3), torch.zeros(1, 1, 2, 2))

@@ -1,0 +1,165 @@
+"""GPU parity of the Linear GEMMs (fused bias, backward, bias gradient) and of
+the conv-as-GEMM path against the CPU oracle and the reference's own vectors."""
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import minitensor_amd as mt
+import oracle
+from util_parity import amax, assert_close
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden" / "reference_vectors.npz"
+
+
+def g(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def sync_np(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def test_config4_linear_forward_backward(dev):
+    # BASELINE config 4 (ResNet50-fc): X[256,2048] ~ N(0,1), W[1000,2048] He-init,
+    # b = 0, dY[256,1000] ~ N(0, 0.01); Y = X·Wᵀ + b, dX = dY·W, dW = dYᵀ·X, db = Σ dY.
+    x = oracle.normal((256, 2048), 42)
+    w = oracle.normal((1000, 2048), 43, std=(2.0 / 2048) ** 0.5)
+    b = np.zeros(1000, np.float32)
+    dy = oracle.normal((256, 1000), 44, std=0.01)
+    X, W, B, dY = g(x, dev), g(w, dev), g(b, dev), g(dy, dev)
+    y = sync_np(mt.linear(X, W, B))
+    print(f"[config] fwd {mt.last_config()}")
+    dx, dw, db = mt.linear_backward(dY, X, W)
+    dx, dw, db = sync_np(dx), sync_np(dw), sync_np(db)
+    assert_close(y, oracle.linear(x, w, b), 2048, amax(x), amax(w), "C4 Y")
+    wdx, wdw, wdb = oracle.linear_backward(dy, x, w)
+    assert_close(dx, wdx, 1000, amax(dy), amax(w), "C4 dX")
+    assert_close(dw, wdw, 256, amax(dy), amax(x), "C4 dW")
+    assert_close(db, wdb, 256, amax(dy), 1.0, "C4 db")
+
+
+def test_linear_nonzero_bias_and_grad_accumulation(dev):
+    x = oracle.normal((100, 300), 1)
+    w = oracle.normal((70, 300), 2, std=0.08)
+    b = oracle.normal((70,), 3, std=0.5)
+    dy = oracle.normal((100, 70), 4, std=0.1)
+    X, W, B, dY = g(x, dev), g(w, dev), g(b, dev), g(dy, dev)
+    y = sync_np(mt.linear(X, W, B))
+    assert_close(y, oracle.linear(x, w, b), 300, amax(x), amax(w), "Y with bias", extra=1e-6)
+    # accumulate_grad: a second backward adds into the first (beta = 1 epilogue)
+    wdx, wdw, wdb = oracle.linear_backward(dy, x, w)
+    dx, dw, db = mt.linear_backward(dY, X, W)
+    mt.linear_backward(dY, X, W, need_dx=False, dw=dw, db=db, beta_w=1.0, beta_b=1.0)
+    assert_close(sync_np(dw), 2 * wdw, 100, amax(dy), amax(x), "dW accumulated", extra=1e-6)
+    assert_close(sync_np(db), 2 * wdb, 100, amax(dy), 1.0, "db accumulated", extra=1e-6)
+
+
+def test_reference_layout_linear_via_views(dev):
+    # The reference's Linear keeps W_ref [in,out] and computes matmul(x, W_ref) + b,
+    # then dX = dY·W_refᵀ (view) and dW_ref = xᵀ (view)·dY (include/Module.hpp:92-114,
+    # include/Autograd.hpp:117-147).  Same GEMMs through mt_gemm_f32 views.
+    with np.load(GOLDEN, allow_pickle=False) as d:
+        v = {k: d[k] for k in d.files}
+    x, w_ref, b, dy = v["lin_x"], v["lin_w_ref"], v["lin_b"], v["lin_dy"]
+    X, W, B, dY = g(x, dev), g(w_ref, dev), g(b, dev), g(dy, dev)
+    y = sync_np(mt.gemm(X, W, bias=B, bias_axis=mt.BIAS_COL))
+    dx = sync_np(mt.gemm(dY, W.t()))
+    dw = sync_np(mt.gemm(X.t(), dY))
+    db = sync_np(mt.colsum(dY))
+    K = x.shape[1]
+    assert_close(y, v["lin_y"], K, amax(x), amax(w_ref), "ref Linear Y", extra=1e-6)
+    assert_close(dx, v["lin_dx"], w_ref.shape[1], amax(dy), amax(w_ref), "ref Linear dX")
+    assert_close(dw, v["lin_dw_ref"], x.shape[0], amax(dy), amax(x), "ref Linear dW_ref")
+    assert_close(db, v["lin_db"], x.shape[0], amax(dy), 1.0, "ref Linear db")
+
+
+def test_golden_matmul_vectors(dev):
+    with np.load(GOLDEN, allow_pickle=False) as d:
+        v = {k: d[k] for k in d.files}
+    # offset views: A = rows 2..4 of a [5,5] storage, B at offset 3
+    As = g(v["offset_a_store"], dev)
+    Bs = g(v["offset_b_store"], dev)
+    A = torch.as_strided(As, (3, 5), (5, 1), 10)
+    B = torch.as_strided(Bs, (5, 4), (4, 1), 3)
+    assert_close(sync_np(mt.gemm(A, B)), v["offset_c"], 5, 1.0, 1.0, "golden offset views")
+    bt = g(v["bT_bt"], dev)
+    assert_close(sync_np(mt.gemm(g(v["bT_a"], dev), bt.t())), v["bT_c"], 47, 1.0, 1.0, "golden Bᵀ")
+    row = g(v["expand_row"], dev)[None, :].expand(17, 40)
+    assert_close(sync_np(mt.gemm(row, g(v["expand_b"], dev))), v["expand_c"], 40,
+                 amax(v["expand_row"]), amax(v["expand_b"]), "golden expand")
+    assert_close(sync_np(mt.gemm(g(v["dense_a"], dev), g(v["dense_b"], dev))), v["dense_c"], 96,
+                 1.0, 1.0, "golden dense")
+    out = mt.conv2d(g(v["conv_x"], dev), g(v["conv_w"], dev), g(v["conv_b"], dev), 2, 1)
+    assert_close(sync_np(out), v["conv_out"], 27, amax(v["conv_x"]), amax(v["conv_w"]),
+                 "golden conv", extra=1e-6)
+
+
+def test_colsum_shapes(dev):
+    for R, C in [(1, 1), (256, 1000), (1000, 3), (7, 130), (0, 5)]:
+        x = oracle.normal((R, C), R + C)
+        got = sync_np(mt.colsum(g(x, dev)))
+        assert_close(got, oracle.colsum(x) if R else np.zeros(C, np.float32), R, amax(x) if R else 0,
+                     1.0, f"colsum {R}x{C}")
+    x = oracle.normal((64, 48), 1)
+    X = g(x, dev).t()  # transposed view [48,64]
+    assert_close(sync_np(mt.colsum(X)), oracle.colsum(x.T), 48, amax(x), 1.0, "colsum view")
+
+
+def seq(shape, start, step):
+    return (start + step * np.arange(int(np.prod(shape)), dtype=np.float32)).reshape(shape)
+
+
+def test_conv_reference_device_equivalence(dev):
+    # reference test/spatial_test.cpp:209-230: [4,3,32,32] ⊛ [16,3,3,3], stride 2, pad 1,
+    # sequential fills, bias 0.1; the reference allows rtol 1e-3 / atol 1e-4.
+    x = seq((4, 3, 32, 32), 0.1, 0.01)
+    w = seq((16, 3, 3, 3), -0.5, 0.02)
+    b = np.full(16, 0.1, np.float32)
+    out = sync_np(mt.conv2d(g(x, dev), g(w, dev), g(b, dev), 2, 1))
+    want = oracle.conv2d(x, w, b, 2, 1)
+    np.testing.assert_allclose(out, want, rtol=1e-3, atol=1e-4)
+    assert_close(out, want, 27, amax(x), amax(w), "spatial_test conv", extra=1e-5)
+
+
+@pytest.mark.parametrize("n,c,h,wd,co,kh,kw,stride,pad", [
+    (1, 1, 3, 3, 1, 2, 2, 1, 0),
+    (2, 5, 9, 7, 6, 3, 3, 1, 1),
+    (3, 4, 11, 10, 6, 3, 2, 2, 2),
+    (2, 16, 8, 8, 32, 1, 1, 1, 0),
+    (1, 3, 17, 13, 8, 5, 5, 3, 1),
+    (2, 8, 5, 5, 4, 7, 7, 1, 3),
+    (1, 2, 2, 2, 3, 5, 5, 1, 0),   # kernel larger than the input: empty output
+])
+def test_conv_shapes(dev, n, c, h, wd, co, kh, kw, stride, pad):
+    x = oracle.normal((n, c, h, wd), n + c)
+    w = oracle.normal((co, c, kh, kw), co + kh)
+    b = oracle.normal((co,), 5)
+    out = sync_np(mt.conv2d(g(x, dev), g(w, dev), g(b, dev), stride, pad))
+    want = oracle.conv2d(x, w, b, stride, pad)
+    assert out.shape == want.shape
+    if want.size:
+        assert_close(out, want, c * kh * kw, amax(x), amax(w), "conv", extra=1e-5)
+
+
+def test_config5a_conv(dev):
+    # BASELINE config 5a: N=32, C=256, 14x14 -> 256, 3x3 s1 p1 (GEMM M=6272, K=2304, N=256).
+    # 16 sampled output channels against the oracle's direct conv, plus the
+    # channel-sum identity Σ_co out = conv(x, Σ_co w) + Σ b over every position.
+    x = oracle.normal((32, 256, 14, 14), 42)
+    w = oracle.normal((256, 256, 3, 3), 43, std=(2.0 / 2304) ** 0.5)
+    b = np.zeros(256, np.float32)
+    out = sync_np(mt.conv2d(g(x, dev), g(w, dev), g(b, dev), 1, 1))
+    print(f"[config] {mt.last_config()}")
+    ch = np.arange(0, 256, 16)
+    want = oracle.conv2d(x, w[ch], b[ch], 1, 1)
+    assert_close(out[:, ch], want, 2304, amax(x), amax(w), "C5a sampled channels")
+    wsum = w.astype(np.float64).sum(axis=0, keepdims=True).astype(np.float32)
+    total = oracle.conv2d(x, wsum, None, 1, 1)[:, 0]
+    err = np.max(np.abs(out.astype(np.float64).sum(axis=1) - total))
+    bound = 256 * 1e-5 * 48 * amax(x) * amax(w) + 1e-3
+    print(f"[parity] C5a channel-sum: max|err|={err:.3e} bound={bound:.3e}")
+    assert err <= bound
