@@ -126,6 +126,39 @@ int mt_conv2d_fwd_f32(const mt_conv2d_desc* d, const float* input, const float* 
                       void* stream);
 size_t mt_conv2d_workspace_f32(const mt_conv2d_desc* d);
 
+/* Conv2D backward as GEMMs (dense NCHW tensors, same descriptor as forward):
+ *   weight: dW[c_out, c_in*kh*kw] = dY[c_out, n*h_out*w_out] · colᵀ (+ beta·dW)
+ *           replaces conv2d_backward_weight_gpu (reference src/gpu_ops.cpp:2623-2713)
+ *   input:  dcol = Wᵀ · dY, then a deterministic col2im gather into dX
+ *           replaces conv2d_backward_input_gpu + fused_backward_input_kernel
+ *           (reference src/gpu_ops.cpp:2499-2550, 861-907)
+ *   bias:   db[c] = Σ_{n,y,x} dY[n,c,y,x] (+ beta·db)
+ *           replaces conv2d_backward_bias_gpu (reference src/gpu_ops.cpp:2483-2497)
+ * One workspace query covers weight and input. */
+int mt_conv2d_bwd_weight_f32(const mt_conv2d_desc* d, const float* input, const float* grad_out,
+                             float* grad_weight, float beta, void* workspace, size_t ws_bytes,
+                             void* stream);
+int mt_conv2d_bwd_input_f32(const mt_conv2d_desc* d, const float* grad_out, const float* weight,
+                            float* grad_input, void* workspace, size_t ws_bytes, void* stream);
+int mt_conv2d_bwd_bias_f32(const mt_conv2d_desc* d, const float* grad_out, float* grad_bias,
+                           float beta, void* stream);
+size_t mt_conv2d_bwd_workspace_f32(const mt_conv2d_desc* d);
+
+/* ---- support kernels the Tensor layer needs around the GEMMs --------------- */
+/* p[i] = value for i in [0, n).  Replaces fill_gpu (reference
+ * src/gpu_ops.cpp:1149-1161; declared include/TensorOps.hpp:721), which the
+ * reference's Tensor::fill and backward()'s ones_like seed call. */
+int mt_fill_f32(float* p, int64_t n, float value, void* stream);
+
+/* Y = alpha·X + beta·Y elementwise over matching (batch, rows, cols) views.
+ * X may broadcast (stride 0); beta == 0 never reads Y; Y must not alias X
+ * unless X and Y are the same view.  Replaces copy_gpu_strided behind
+ * Tensor::contiguous() (reference src/gpu_ops.cpp:2940-2972), the add_ of
+ * accumulate_grad (include/Tensor.hpp:96-102) and the unfused broadcast bias
+ * add (binary_gpu_strided with AddOp, src/gpu_ops.cpp:192-213). */
+int mt_axpby_f32(const mt_mat_f32* X, float alpha, const mt_mat_f32* Y, float beta,
+                 void* stream);
+
 /* ---- diagnostics ---------------------------------------------------------- */
 const char* mt_strerror(int status);
 int mt_version(void);

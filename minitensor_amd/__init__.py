@@ -82,6 +82,19 @@ _SIGS = {
                                          ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                          ctypes.c_size_t, ctypes.c_void_p]),
     "mt_conv2d_workspace_f32": (ctypes.c_size_t, [_P(Conv2dDesc)]),
+    "mt_conv2d_bwd_weight_f32": (ctypes.c_int, [_P(Conv2dDesc), ctypes.c_void_p, ctypes.c_void_p,
+                                                ctypes.c_void_p, ctypes.c_float, ctypes.c_void_p,
+                                                ctypes.c_size_t, ctypes.c_void_p]),
+    "mt_conv2d_bwd_input_f32": (ctypes.c_int, [_P(Conv2dDesc), ctypes.c_void_p, ctypes.c_void_p,
+                                               ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                               ctypes.c_void_p]),
+    "mt_conv2d_bwd_bias_f32": (ctypes.c_int, [_P(Conv2dDesc), ctypes.c_void_p, ctypes.c_void_p,
+                                              ctypes.c_float, ctypes.c_void_p]),
+    "mt_conv2d_bwd_workspace_f32": (ctypes.c_size_t, [_P(Conv2dDesc)]),
+    "mt_fill_f32": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64, ctypes.c_float,
+                                   ctypes.c_void_p]),
+    "mt_axpby_f32": (ctypes.c_int, [_P(MatF32), ctypes.c_float, _P(MatF32), ctypes.c_float,
+                                    ctypes.c_void_p]),
     "mt_strerror": (ctypes.c_char_p, [ctypes.c_int]),
     "mt_version": (ctypes.c_int, []),
     "mt_last_config": (ctypes.c_char_p, []),
@@ -295,6 +308,39 @@ def conv2d(x: torch.Tensor, w: torch.Tensor, b: Optional[torch.Tensor] = None, s
                                  _stream(stream))
     _check(rc, "mt_conv2d_fwd_f32")
     return out
+
+
+def conv2d_backward(x: torch.Tensor, w: torch.Tensor, dy: torch.Tensor, stride: int = 1,
+                    padding: int = 0, need_dx: bool = True, need_dw: bool = True,
+                    need_db: bool = True, ws: Optional[torch.Tensor] = None, stream=None):
+    """Conv2D backward on dense NCHW tensors: returns (dX, dW, db), None where not asked."""
+    _require_gpu(x, w, dy)
+    x, w, dy = x.contiguous(), w.contiguous(), dy.contiguous()
+    n, c, h, wd = x.shape
+    co, _, kh, kw = w.shape
+    d = Conv2dDesc(n, c, h, wd, co, kh, kw, stride, padding)
+    if tuple(dy.shape) != (n, co, conv_out_size(h, padding, kh, stride),
+                           conv_out_size(wd, padding, kw, stride)):
+        raise ValueError("conv2d_backward: grad_output has the wrong shape")
+    if ws is None:
+        ws = workspace(lib().mt_conv2d_bwd_workspace_f32(ctypes.byref(d)), x.device)
+    wp, wn = _ptr(ws), (ws.numel() if ws is not None else 0)
+    dx = dw = db = None
+    s = _stream(stream)
+    if need_dx:
+        dx = torch.empty_like(x)
+        _check(lib().mt_conv2d_bwd_input_f32(ctypes.byref(d), dy.data_ptr(), w.data_ptr(),
+                                             dx.data_ptr(), wp, wn, s), "mt_conv2d_bwd_input_f32")
+    if need_dw:
+        dw = torch.empty_like(w)
+        _check(lib().mt_conv2d_bwd_weight_f32(ctypes.byref(d), x.data_ptr(), dy.data_ptr(),
+                                              dw.data_ptr(), 0.0, wp, wn, s),
+               "mt_conv2d_bwd_weight_f32")
+    if need_db:
+        db = torch.empty((co,), dtype=torch.float32, device=x.device)
+        _check(lib().mt_conv2d_bwd_bias_f32(ctypes.byref(d), dy.data_ptr(), db.data_ptr(), 0.0, s),
+               "mt_conv2d_bwd_bias_f32")
+    return dx, dw, db
 
 
 def last_config() -> str:

@@ -22,7 +22,8 @@ OBJDIR = PKG / "_build"
 LIB = LIBDIR / "libmtgemm.so"
 
 ARCH = "gfx950"
-HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+HIPCC = os.environ.get("HIPCC", str(ROCM / "bin" / "hipcc"))
 
 # -packed-fp32-ops: keep the compiler from emitting v_pk_{add,mul,fma}_f32.
 COMMON = [
@@ -79,5 +80,25 @@ def build(verbose: bool = False) -> Path:
     return LIB
 
 
+HOST_TESTS = LIBDIR / "mt_host_tests"
+
+
+def build_host_tests(verbose: bool = False) -> Path:
+    """Compile the C++ host-layer test program against libmtgemm.so (rpath $ORIGIN)."""
+    src = PKG / "cpp" / "tests" / "host_tests.cpp"
+    # Host-only C++ (no device code): g++ against the HIP runtime headers.
+    cmd = [os.environ.get("CXX", "g++"), "-std=c++20", "-O2", "-Wall", "-D__HIP_PLATFORM_AMD__",
+           f"-I{ROCM / 'include'}", f"-I{ROOT / 'include'}", f"-I{PKG / 'cpp'}", str(src),
+           "-o", str(HOST_TESTS), f"-L{LIBDIR}", "-lmtgemm", f"-L{ROCM / 'lib'}", "-lamdhip64",
+           "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{ROCM / 'lib'}"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"host test build failed:\n{r.stdout}")
+    return HOST_TESTS
+
+
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))
+    print(build_host_tests(verbose="-v" in sys.argv))

@@ -1,0 +1,116 @@
+// MemoryPool.hpp -- caching allocator for tensor storage and GEMM workspaces.
+//
+// Same contract as the reference's MemoryPool (include/MemoryPool.hpp:24-127):
+// allocate/free by (bytes, device), power-of-two size bins, blocks cached
+// until empty_cache(), mutex-protected.  Device blocks come from hipMalloc on
+// the tensor's device; host blocks are 64-byte aligned heap memory (so CPU
+// tensors work on machines without a GPU).  Split-K partials and im2col
+// buffers are taken from here, so once warm no GEMM call allocates.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdlib>
+#include <mutex>
+#include <new>
+#include <unordered_map>
+#include <vector>
+
+#include "Defines.hpp"
+#include "GpuUtils.hpp"
+
+class MemoryPool {
+public:
+    static MemoryPool& get() {
+        static MemoryPool pool;
+        return pool;
+    }
+
+    void* allocate(size_t bytes, Device device) {
+        if (bytes == 0) return nullptr;
+        const size_t b = bin(bytes);
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            auto& fl = cache(device)[b];
+            if (!fl.empty()) {
+                void* p = fl.back();
+                fl.pop_back();
+                return p;
+            }
+        }
+        if (device.is_gpu()) {
+            int prev = 0;
+            GPU_CHECK(hipGetDevice(&prev));
+            if (prev != device.index) GPU_CHECK(hipSetDevice(device.index));
+            void* p = nullptr;
+            hipError_t e = hipMalloc(&p, b);
+            if (e != hipSuccess) {  // release cached blocks once and retry
+                release(device);
+                e = hipMalloc(&p, b);
+            }
+            if (prev != device.index) (void)hipSetDevice(prev);
+            if (e != hipSuccess) mt_detail::hip_fail(e, __FILE__, __LINE__);
+            return p;
+        }
+        void* p = std::aligned_alloc(64, b);
+        if (!p) throw std::bad_alloc();
+        return p;
+    }
+
+    void free(void* p, size_t bytes, Device device) {
+        if (!p || bytes == 0) return;
+        std::lock_guard<std::mutex> lk(mu_);
+        cache(device)[bin(bytes)].push_back(p);
+    }
+
+    // Returns every cached block to the system (device memory: hipFree).
+    void empty_cache() {
+        release(Device(DeviceType::CPU));
+        for (int i = 0; i < kMaxGpus; ++i) release(Device(DeviceType::CUDA, (uint8_t)i));
+    }
+
+    size_t cached_blocks(Device device) {
+        std::lock_guard<std::mutex> lk(mu_);
+        size_t n = 0;
+        for (auto& kv : cache(device)) n += kv.second.size();
+        return n;
+    }
+
+    static size_t bin(size_t bytes) {
+        size_t b = 256;
+        while (b < bytes) b <<= 1;
+        return b;
+    }
+
+private:
+    static constexpr int kMaxGpus = 16;
+    using Bins = std::unordered_map<size_t, std::vector<void*>>;
+
+    MemoryPool() = default;
+    ~MemoryPool() = default;  // blocks are kept until process exit, as the reference does
+
+    Bins& cache(Device d) {
+        if (!d.is_gpu()) return host_;
+        if (d.index >= kMaxGpus) throw std::invalid_argument("MemoryPool: device index out of range");
+        return gpu_[d.index];
+    }
+
+    void release(Device d) {
+        std::vector<void*> blocks;
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            for (auto& kv : cache(d)) {
+                blocks.insert(blocks.end(), kv.second.begin(), kv.second.end());
+                kv.second.clear();
+            }
+        }
+        for (void* p : blocks) {
+            if (d.is_gpu()) (void)hipFree(p);
+            else std::free(p);
+        }
+    }
+
+    std::mutex mu_;
+    Bins host_;
+    Bins gpu_[kMaxGpus];
+};

@@ -1,0 +1,463 @@
+// host_tests.cpp -- tests of the C++ host layer (Tensor / matmul / bmm / conv2d /
+// F::linear / Linear / Conv2D / Dispatch) on the CPU device and on the GPU.
+//
+//   mt_host_tests --cpu    CPU-device tests (no GPU needed)
+//   mt_host_tests --gpu    GPU tests: known answers and CPU-vs-GPU equivalence
+//
+// Known answers are the reference's own tests: test/tensor_test.cpp:258-510,
+// test/engien_test.cpp:80-96, test/spatial_test.cpp:155-230, test/view_test.cpp.
+// Equivalence uses the GEMM parity bound 1e-5·√K·max|A|·max|B|.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <random>
+#include <string>
+#include <vector>
+
+#include "minitensor/minitensor.hpp"
+
+namespace {
+
+struct Case {
+    const char* name;
+    bool gpu;
+    void (*fn)();
+};
+std::vector<Case>& cases() {
+    static std::vector<Case> c;
+    return c;
+}
+struct Reg {
+    Reg(const char* n, bool g, void (*f)()) { cases().push_back({n, g, f}); }
+};
+int g_fail = 0;
+const char* g_cur = "";
+
+#define TEST_CPU(name) static void name(); static Reg reg_##name(#name, false, name); static void name()
+#define TEST_GPU(name) static void name(); static Reg reg_##name(#name, true, name); static void name()
+#define CHECK(cond)                                                                   \
+    do {                                                                              \
+        if (!(cond)) {                                                                \
+            std::printf("  FAIL %s: %s (line %d)\n", g_cur, #cond, __LINE__);         \
+            ++g_fail;                                                                 \
+        }                                                                             \
+    } while (0)
+#define CHECK_EQ_F(a, b) CHECK(std::fabs((double)(a) - (double)(b)) <= 1e-6 * (1 + std::fabs((double)(b))))
+#define CHECK_THROWS(expr, Exc)                     \
+    do {                                            \
+        bool thrown_ = false;                       \
+        try { expr; } catch (const Exc&) { thrown_ = true; } \
+        CHECK(thrown_ && #Exc);                     \
+    } while (0)
+
+const Device CPU{DeviceType::CPU};
+const Device GPU{DeviceType::CUDA, 0};
+
+Tensor<float> host(const Tensor<float>& t) { return t.to(CPU).contiguous(); }
+
+float val(const Tensor<float>& t, size_t i) {
+    Tensor<float> h = t.to(CPU);
+    return h.data()[h.offset() + i];
+}
+
+// Seeded U(lo,hi) from std::mt19937 with an explicit transform.
+Tensor<float> uniform(std::vector<size_t> shape, unsigned seed, float lo = -1.f, float hi = 1.f) {
+    Tensor<float> t(shape);
+    std::mt19937 g(seed);
+    for (size_t i = 0; i < t.total_elements(); ++i)
+        t.data()[i] = lo + (hi - lo) * (float)((g() >> 8) * (1.0 / 16777216.0));
+    return t;
+}
+
+float amax(const Tensor<float>& t) {
+    Tensor<float> h = host(t);
+    float m = 0;
+    for (size_t i = 0; i < h.total_elements(); ++i) m = std::max(m, std::fabs(h.data()[i]));
+    return m;
+}
+
+// max |a - b| over two same-shape tensors (any device / strides).
+double max_err(const Tensor<float>& a, const Tensor<float>& b) {
+    Tensor<float> x = host(a), y = host(b);
+    CHECK(x.shape() == y.shape());
+    double e = 0;
+    for (size_t i = 0; i < x.total_elements(); ++i)
+        e = std::max(e, (double)std::fabs(x.data()[i] - y.data()[i]));
+    return e;
+}
+
+void check_close(const Tensor<float>& got, const Tensor<float>& want, size_t K, float am, float bm,
+                 double extra = 0.0) {
+    const double bound = 1e-5 * std::sqrt((double)std::max<size_t>(K, 1)) * am * bm + extra;
+    const double e = max_err(got, want);
+    if (!(e <= bound)) std::printf("  %s: max|err| %.3e > bound %.3e\n", g_cur, e, bound);
+    CHECK(e <= bound);
+}
+
+Tensor<float> mat23() {
+    Tensor<float> A({2, 3});
+    for (int i = 0; i < 6; ++i) A.data()[i] = (float)(i + 1);
+    return A;
+}
+Tensor<float> mat32() {
+    Tensor<float> B({3, 2});
+    for (int i = 0; i < 6; ++i) B.data()[i] = (float)(i + 7);
+    return B;
+}
+
+// =====================================================================
+// CPU device
+// =====================================================================
+TEST_CPU(cpu_matmul_known_answer) {  // tensor_test.cpp:258-283
+    Tensor<float> C = matmul(mat23(), mat32());
+    CHECK(C.shape() == (std::vector<size_t>{2, 2}));
+    CHECK_EQ_F(C.data()[0], 58); CHECK_EQ_F(C.data()[1], 64);
+    CHECK_EQ_F(C.data()[2], 139); CHECK_EQ_F(C.data()[3], 154);
+}
+
+TEST_CPU(cpu_autograd_matmul) {  // tensor_test.cpp:368-419
+    Tensor<float> A = mat23(), B = mat32();
+    A.set_requires_grad(true);
+    B.set_requires_grad(true);
+    Tensor<float> C = matmul(A, B);
+    C.backward();
+    const float dA[] = {15, 19, 23, 15, 19, 23}, dB[] = {5, 5, 7, 7, 9, 9};
+    for (int i = 0; i < 6; ++i) {
+        CHECK_EQ_F(A.grad().data()[i], dA[i]);
+        CHECK_EQ_F(B.grad().data()[i], dB[i]);
+    }
+}
+
+TEST_CPU(cpu_chained_matmul_plus_bias) {  // tensor_test.cpp:448-488
+    Tensor<float> A = mat23(), B = mat32(), C({2});
+    C.data()[0] = 10; C.data()[1] = 20;
+    A.set_requires_grad(true); B.set_requires_grad(true); C.set_requires_grad(true);
+    Tensor<float> D = matmul(A, B) + C;
+    CHECK_EQ_F(D.data()[0], 68); CHECK_EQ_F(D.data()[3], 174);
+    D.backward();
+    CHECK_EQ_F(A.grad().data()[0], 15); CHECK_EQ_F(A.grad().data()[2], 23);
+    CHECK_EQ_F(B.grad().data()[0], 5); CHECK_EQ_F(B.grad().data()[4], 9);
+    CHECK_EQ_F(C.grad().data()[0], 2); CHECK_EQ_F(C.grad().data()[1], 2);
+}
+
+TEST_CPU(cpu_broadcast_add_grads) {  // tensor_test.cpp AutogradTest.BroadcastingAddition
+    Tensor<float> A({2, 3}), B({3});
+    A.fill(1); B.fill(2);
+    A.set_requires_grad(true); B.set_requires_grad(true);
+    Tensor<float> C = A + B;
+    C.backward();
+    CHECK_EQ_F(A.grad().data()[5], 1);
+    CHECK(B.grad().shape() == (std::vector<size_t>{3}));
+    for (int i = 0; i < 3; ++i) CHECK_EQ_F(B.grad().data()[i], 2);
+}
+
+TEST_CPU(cpu_matmul_backward_fills) {  // engien_test.cpp:80-96
+    Tensor<float> a({2, 3}), b({3, 2});
+    a.fill(2); b.fill(3);
+    a.set_requires_grad(true); b.set_requires_grad(true);
+    Tensor<float> c = matmul(a, b);
+    CHECK_EQ_F(val(c, 0), 18);
+    c.backward();
+    CHECK_EQ_F(val(a.grad(), 0), 6);
+    CHECK_EQ_F(val(b.grad(), 0), 4);
+}
+
+TEST_CPU(cpu_views_slice_transpose_expand) {
+    Tensor<float> big = uniform({10, 6}, 1);
+    Tensor<float> s = big.slice(0, 3, 8);  // offset view, strides unchanged
+    CHECK(s.offset() == 18 && s.is_contiguous());
+    Tensor<float> B = uniform({6, 4}, 2);
+    check_close(matmul(s, B), matmul(s.contiguous(), B), 6, 1, 1);
+    Tensor<float> bt = uniform({4, 6}, 3).transpose(0, 1);  // [6,4] strides (1,6)
+    CHECK(!bt.is_contiguous());
+    check_close(matmul(s, bt), matmul(s, bt.contiguous()), 6, 1, 1);
+    Tensor<float> row = uniform({1, 6}, 4).expand({5, 6});  // stride 0
+    CHECK(row.strides()[0] == 0);
+    check_close(matmul(row, B), matmul(row.contiguous(), B), 6, 1, 1);
+    CHECK_THROWS(big.slice(0, 5, 3), std::out_of_range);
+    CHECK_THROWS(big.slice(2, 0, 1), std::out_of_range);
+}
+
+TEST_CPU(cpu_matmul_errors) {  // include/TensorOps.hpp:995-1005 error behaviour
+    CHECK_THROWS(matmul(Tensor<float>({2, 3}), Tensor<float>({2, 3})), std::invalid_argument);
+    CHECK_THROWS(matmul(Tensor<float>({2, 3, 1}), Tensor<float>({3, 2})), std::invalid_argument);
+    CHECK_THROWS(bmm(Tensor<float>({2, 3, 4}), Tensor<float>({3, 4, 2})), std::invalid_argument);
+    CHECK_THROWS(bmm(Tensor<float>({2, 3, 4}), Tensor<float>({2, 5, 2})), std::invalid_argument);
+    CHECK_THROWS(F::linear(Tensor<float>({2, 3}), Tensor<float>({4, 5})), std::invalid_argument);
+}
+
+TEST_CPU(cpu_saved_tensor_version_check) {
+    Tensor<float> A = mat23(), B = mat32();
+    A.set_requires_grad(true);
+    Tensor<float> C = matmul(A, B);
+    add_(B, mat32());  // in-place change of a saved input
+    CHECK_THROWS(C.backward(), std::runtime_error);
+}
+
+TEST_CPU(cpu_bmm_and_backward) {
+    Tensor<float> A = uniform({3, 4, 5}, 1), B = uniform({3, 5, 2}, 2);
+    A.set_requires_grad(true); B.set_requires_grad(true);
+    Tensor<float> C = bmm(A, B);
+    for (size_t z = 0; z < 3; ++z) {
+        auto a = A.as_strided({4, 5}, {5, 1}, z * 20);
+        auto b = B.as_strided({5, 2}, {2, 1}, z * 10);
+        auto c = C.as_strided({4, 2}, {2, 1}, z * 8);
+        NoGradGuard g;
+        check_close(c, matmul(a, b), 5, 1, 1);
+    }
+    C.backward();  // dA = ones·Bᵀ, dB = Aᵀ·ones per batch
+    for (size_t z = 0; z < 3; ++z)
+        for (size_t i = 0; i < 4; ++i)
+            for (size_t k = 0; k < 5; ++k) {
+                float want = B.data()[z * 10 + k * 2] + B.data()[z * 10 + k * 2 + 1];
+                CHECK(std::fabs(A.grad().data()[z * 20 + i * 5 + k] - want) < 1e-6);
+            }
+}
+
+TEST_CPU(cpu_conv_known_answer) {  // spatial_test.cpp:155-185
+    Tensor<float> x({1, 1, 3, 3}), w({1, 1, 2, 2}), b({1});
+    for (int i = 0; i < 9; ++i) x.data()[i] = (float)(i + 1);
+    w.fill(1);
+    Tensor<float> y = conv2d(x, w, b, 1, 0);
+    CHECK(y.shape() == (std::vector<size_t>{1, 1, 2, 2}));
+    const float want[] = {12, 16, 24, 28};
+    for (int i = 0; i < 4; ++i) CHECK_EQ_F(y.data()[i], want[i]);
+}
+
+// L = Σ dY ⊙ f(params); analytic gradients vs central differences.
+void gradcheck(Tensor<float>& p, const std::function<Tensor<float>()>& f, const Tensor<float>& dy,
+               double tol) {
+    auto loss = [&]() {
+        NoGradGuard g;
+        Tensor<float> y = host(f());
+        double s = 0;
+        for (size_t i = 0; i < y.total_elements(); ++i) s += (double)y.data()[i] * dy.data()[i];
+        return s;
+    };
+    Tensor<float> g = host(p.grad());
+    const float eps = 1e-2f;
+    for (size_t i = 0; i < p.total_elements(); i += std::max<size_t>(1, p.total_elements() / 13)) {
+        const float old = p.data()[i];
+        p.data()[i] = old + eps; const double hi = loss();
+        p.data()[i] = old - eps; const double lo = loss();
+        p.data()[i] = old;
+        const double fd = (hi - lo) / (2 * eps);
+        if (std::fabs(fd - g.data()[i]) > tol * (1 + std::fabs(fd)))
+            std::printf("  %s: grad[%zu] %.6f vs fd %.6f\n", g_cur, i, g.data()[i], fd);
+        CHECK(std::fabs(fd - g.data()[i]) <= tol * (1 + std::fabs(fd)));
+    }
+}
+
+TEST_CPU(cpu_linear_module_and_F_linear) {
+    Linear<float> lin(7, 5);
+    CHECK(lin.weight_.shape() == (std::vector<size_t>{7, 5}));
+    CHECK(lin.bias_.shape() == (std::vector<size_t>{1, 5}));
+    Tensor<float> x = uniform({4, 7}, 9);
+    Tensor<float> y = lin.forward(x);
+    Tensor<float> ref = matmul(x, lin.weight_) + lin.bias_;
+    check_close(y, ref, 7, amax(x), amax(lin.weight_), 1e-6);
+    // F::linear with the PyTorch layout gives the same result from wᵀ
+    Tensor<float> w = lin.weight_.transpose(0, 1).contiguous();
+    check_close(F::linear(x, w, lin.bias_.reshape({5})), y, 7, amax(x), amax(w), 1e-6);
+    // backward vs finite differences (the reference's gradcheck recipe)
+    Tensor<float> dy = uniform({4, 5}, 10);
+    Tensor<float> xs = uniform({4, 7}, 11);
+    xs.set_requires_grad(true);
+    Tensor<float> out = lin.forward(xs);
+    out.grad() = dy;
+    out.backward();
+    gradcheck(lin.weight_, [&]() { return lin.forward(xs); }, dy, 2e-3);
+    gradcheck(lin.bias_, [&]() { return lin.forward(xs); }, dy, 2e-3);
+    gradcheck(xs, [&]() { return lin.forward(xs); }, dy, 2e-3);
+}
+
+TEST_CPU(cpu_conv_module_backward_gradcheck) {
+    Conv2D<float> conv(3, 4, 3, 2, 1);
+    Tensor<float> x = uniform({2, 3, 7, 6}, 5);
+    x.set_requires_grad(true);
+    conv.bias_.fill(0.1f);
+    Tensor<float> y = conv.forward(x);
+    Tensor<float> dy = uniform(y.shape(), 6);
+    y.grad() = dy;
+    y.backward();
+    gradcheck(conv.weight_, [&]() { return conv.forward(x); }, dy, 2e-3);
+    gradcheck(conv.bias_, [&]() { return conv.forward(x); }, dy, 2e-3);
+    gradcheck(x, [&]() { return conv.forward(x); }, dy, 2e-3);
+}
+
+TEST_CPU(cpu_dispatch_registry) {
+    auto* fn = OpRegistry<float>::instance().lookup_binary(OpType::Matmul);
+    CHECK(fn != nullptr);
+    Tensor<float> out({2, 2});
+    dispatch_binary_op(OpType::Matmul, mat23(), mat32(), out);
+    CHECK_EQ_F(out.data()[0], 58); CHECK_EQ_F(out.data()[3], 154);
+    CHECK(OpRegistry<float>::instance().lookup_binary(OpType::Conv2D) != nullptr);
+    Tensor<float> x({1, 1, 3, 3}), w({1, 1, 2, 2}), y({1, 1, 2, 2});
+    for (int i = 0; i < 9; ++i) x.data()[i] = (float)(i + 1);
+    w.fill(1);
+    dispatch_binary_op(OpType::Conv2D, x, w, y);
+    CHECK_EQ_F(y.data()[0], 12); CHECK_EQ_F(y.data()[3], 28);
+}
+
+// =====================================================================
+// GPU device
+// =====================================================================
+TEST_GPU(gpu_matmul_known_answer) {  // tensor_test.cpp:285-316
+    Tensor<float> C = host(matmul(mat23().to(GPU), mat32().to(GPU)));
+    CHECK_EQ_F(C.data()[0], 58); CHECK_EQ_F(C.data()[1], 64);
+    CHECK_EQ_F(C.data()[2], 139); CHECK_EQ_F(C.data()[3], 154);
+}
+
+TEST_GPU(gpu_gradients_fills) {  // tensor_test.cpp:490-510
+    Tensor<float> A({2, 3}, GPU), B({3, 2}, GPU);
+    A.fill(2); B.fill(3);
+    A.set_requires_grad(true); B.set_requires_grad(true);
+    Tensor<float> C = matmul(A, B);
+    C.backward();
+    CHECK_EQ_F(val(A.grad(), 0), 6);
+    CHECK_EQ_F(val(B.grad(), 0), 4);
+}
+
+TEST_GPU(gpu_chained_matmul_plus_bias) {
+    Tensor<float> A = mat23().to(GPU), B = mat32().to(GPU), C({2});
+    C.data()[0] = 10; C.data()[1] = 20;
+    Tensor<float> Cg = C.to(GPU);
+    A.set_requires_grad(true); B.set_requires_grad(true); Cg.set_requires_grad(true);
+    Tensor<float> D = matmul(A, B) + Cg;
+    CHECK_EQ_F(val(D, 0), 68); CHECK_EQ_F(val(D, 3), 174);
+    D.backward();
+    CHECK_EQ_F(val(A.grad(), 2), 23);
+    CHECK_EQ_F(val(B.grad(), 4), 9);
+    CHECK_EQ_F(val(Cg.grad(), 0), 2); CHECK_EQ_F(val(Cg.grad(), 1), 2);
+}
+
+TEST_GPU(gpu_cpu_equivalence_views) {
+    // a row/column slice with an offset (the reference's GPU path drops it), a
+    // transpose view and an expand view, each against the CPU device
+    Tensor<float> big = uniform({400, 300}, 1), b = uniform({250, 200}, 2);
+    Tensor<float> a = big.slice(0, 37, 337).slice(1, 100, 300);            // [300,200]
+    Tensor<float> Ag = big.to(GPU).slice(0, 37, 337).slice(1, 100, 300);
+    Tensor<float> B = b.transpose(0, 1), Bg = b.to(GPU).transpose(0, 1);   // [200,250]
+    check_close(matmul(Ag, Bg), matmul(a, B), 200, 1, 1);
+    check_close(matmul(Ag.transpose(0, 1), Ag), matmul(a.transpose(0, 1), a), 300, 1, 1);
+    Tensor<float> row = uniform({1, 300}, 3);
+    check_close(matmul(row.to(GPU).expand({50, 300}), Ag), matmul(row.expand({50, 300}), a), 300,
+                1, 1);
+}
+
+TEST_GPU(gpu_bmm_forward_backward) {
+    Tensor<float> A = uniform({8, 33, 40}, 1), B = uniform({8, 40, 21}, 2);
+    Tensor<float> Ag = A.to(GPU), Bg = B.to(GPU);
+    A.set_requires_grad(true); B.set_requires_grad(true);
+    Ag.set_requires_grad(true); Bg.set_requires_grad(true);
+    Tensor<float> C = bmm(A, B), Cg = bmm(Ag, Bg);
+    check_close(Cg, C, 40, 1, 1);
+    Tensor<float> dy = uniform({8, 33, 21}, 3);
+    C.grad() = dy;
+    Cg.grad() = dy.to(GPU);
+    C.backward();
+    Cg.backward();
+    check_close(Ag.grad(), A.grad(), 21, 1, 1);
+    check_close(Bg.grad(), B.grad(), 33, 1, 1);
+}
+
+TEST_GPU(gpu_linear_config4_equivalence) {
+    // BASELINE config 4 shape through the Linear module (W_ref [2048,1000]) and F::linear.
+    Linear<float> lin(2048, 1000);
+    Tensor<float> x = uniform({256, 2048}, 42), dy = uniform({256, 1000}, 44, -0.01f, 0.01f);
+    Linear<float> lg = lin;  // same parameters, moved to the GPU below
+    lg.weight_ = lin.weight_.to(GPU);
+    lg.bias_ = lin.bias_.to(GPU);
+    lg.weight_.set_requires_grad(true);
+    lg.bias_.set_requires_grad(true);
+    Tensor<float> xg = x.to(GPU);
+    x.set_requires_grad(true);
+    xg.set_requires_grad(true);
+    Tensor<float> y = lin.forward(x), yg = lg.forward(xg);
+    check_close(yg, y, 2048, amax(x), amax(lin.weight_), 1e-6);
+    y.grad() = dy;
+    yg.grad() = dy.to(GPU);
+    y.backward();
+    yg.backward();
+    check_close(xg.grad(), x.grad(), 1000, amax(dy), amax(lin.weight_));
+    check_close(lg.weight_.grad(), lin.weight_.grad(), 256, amax(dy), amax(x));
+    check_close(lg.bias_.grad(), lin.bias_.grad(), 256, amax(dy), 1);
+    // F::linear (PyTorch layout) on the GPU equals the module
+    Tensor<float> w = lg.weight_.transpose(0, 1);
+    check_close(F::linear(xg, w, lg.bias_.reshape({1000})), yg, 2048, amax(x), amax(lin.weight_), 1e-6);
+}
+
+TEST_GPU(gpu_grad_accumulation_in_epilogue) {
+    // A weight used twice: the second gradient is accumulated by the GEMM epilogue.
+    Tensor<float> W = uniform({64, 48}, 1).to(GPU), x1 = uniform({32, 64}, 2).to(GPU),
+                  x2 = uniform({32, 64}, 3).to(GPU);
+    W.set_requires_grad(true);
+    Tensor<float> y = matmul(x1, W) + matmul(x2, W);
+    y.backward();
+    Tensor<float> Wc = host(W);
+    Wc.set_requires_grad(true);
+    Tensor<float> yc = matmul(host(x1), Wc) + matmul(host(x2), Wc);
+    yc.backward();
+    check_close(W.grad(), Wc.grad(), 64, 2, 1, 1e-5);
+}
+
+TEST_GPU(gpu_conv_equivalence_and_backward) {
+    // reference spatial_test.cpp:209-230 shape, plus a full backward
+    Tensor<float> x = uniform({4, 3, 32, 32}, 1), w = uniform({16, 3, 3, 3}, 2), b({16});
+    b.fill(0.1f);
+    Tensor<float> xg = x.to(GPU), wg = w.to(GPU), bg = b.to(GPU);
+    for (auto* t : {&x, &w, &b, &xg, &wg, &bg}) t->set_requires_grad(true);
+    Tensor<float> y = conv2d(x, w, b, 2, 1), yg = conv2d(xg, wg, bg, 2, 1);
+    check_close(yg, y, 27, 1, 1, 1e-5);
+    Tensor<float> dy = uniform(y.shape(), 3);
+    y.grad() = dy;
+    yg.grad() = dy.to(GPU);
+    y.backward();
+    yg.backward();
+    check_close(xg.grad(), x.grad(), 16 * 9, 1, 1);
+    check_close(wg.grad(), w.grad(), 4 * 16 * 16, 1, 1);
+    check_close(bg.grad(), b.grad(), 4 * 16 * 16, 1, 1);
+}
+
+TEST_GPU(gpu_contiguous_and_dispatch) {
+    Tensor<float> a = uniform({37, 53}, 1);
+    Tensor<float> t = a.to(GPU).transpose(0, 1);
+    Tensor<float> c = t.contiguous();
+    CHECK(c.is_contiguous() && c.offset() == 0);
+    check_close(c, a.transpose(0, 1).contiguous(), 1, 0, 0);
+    Tensor<float> out({2, 2}, GPU);
+    dispatch_binary_op(OpType::Matmul, mat23().to(GPU), mat32().to(GPU), out);
+    CHECK_EQ_F(val(out, 0), 58); CHECK_EQ_F(val(out, 3), 154);
+    CHECK_THROWS(matmul(mat23().to(GPU), mat32()), std::invalid_argument);
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    const bool want_gpu = argc > 1 && std::strcmp(argv[1], "--gpu") == 0;
+    const bool want_cpu = argc > 1 && std::strcmp(argv[1], "--cpu") == 0;
+    if (!want_gpu && !want_cpu) {
+        std::printf("usage: %s --cpu | --gpu\n", argv[0]);
+        return 2;
+    }
+    int ran = 0;
+    for (auto& c : cases()) {
+        if (c.gpu != want_gpu) continue;
+        g_cur = c.name;
+        const int before = g_fail;
+        std::printf("[ RUN  ] %s\n", c.name);
+        std::fflush(stdout);
+        try {
+            c.fn();
+        } catch (const std::exception& e) {
+            std::printf("  FAIL %s: exception %s\n", c.name, e.what());
+            ++g_fail;
+        }
+        std::printf("[ %s ] %s\n", g_fail == before ? " OK " : "FAIL", c.name);
+        std::fflush(stdout);
+        ++ran;
+    }
+    std::printf("%d tests, %d failures\n", ran, g_fail);
+    return g_fail ? 1 : 0;
+}

@@ -348,6 +348,110 @@ void conv_gemm_views(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, const floa
     *C = mt_mat_f32{output, 0, d->c_out, np, Ho * Wo, 1, 1, 0};
 }
 
+
+// ---- support kernels ---------------------------------------------------------
+__global__ void __launch_bounds__(256) fill_f32(float* p, int64_t n, float v) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+// Y = alpha*X + beta*Y over (batch, rows, cols) views; grid-stride over the
+// elements in row-major (batch, row, col) order.
+__global__ void __launch_bounds__(256)
+axpby_f32(const float* X, int64_t xb, int64_t xr, int64_t xc, float alpha, float* Y, int64_t yb,
+          int64_t yr, int64_t yc, float beta, int64_t rows, int64_t cols, int64_t total) {
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t rc = rows * cols;
+        const int64_t b = e / rc;
+        const int64_t rem = e - b * rc;
+        const int64_t r = rem / cols, c = rem - r * cols;
+        float* y = Y + b * yb + r * yr + c * yc;
+        const float v = alpha * X[b * xb + r * xr + c * xc];
+        *y = beta != 0.f ? v + beta * *y : v;
+    }
+}
+
+unsigned grid_for(int64_t total) {
+    return (unsigned)std::max<int64_t>(1, std::min<int64_t>((total + 255) / 256, 8192));
+}
+
+// dX[img][c][y][x] = Σ_{r,s} dcol[(c*kh + r)*kw + s][(img*Ho + oh)*Wo + ow] over the
+// (r, s) whose window position (oh, ow) covers (y, x): a gather, so every input
+// element is written once, in a fixed (r, s) order -- no atomics.
+__global__ void __launch_bounds__(256)
+col2im_gather_f32(const float* dcol, float* dx, int C, int H, int W, int kh, int kw, int st,
+                  int pad, int Ho, int Wo, int64_t NP, int64_t total) {
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int x = (int)(e % W);
+        const int64_t t1 = e / W;
+        const int y = (int)(t1 % H);
+        const int64_t t2 = t1 / H;
+        const int c = (int)(t2 % C);
+        const int64_t img = t2 / C;
+        float acc = 0.f;
+        for (int r = 0; r < kh; ++r) {
+            const int ty = y + pad - r;
+            if (ty < 0 || ty % st) continue;
+            const int oh = ty / st;
+            if (oh >= Ho) continue;
+            for (int s = 0; s < kw; ++s) {
+                const int tx = x + pad - s;
+                if (tx < 0 || tx % st) continue;
+                const int ow = tx / st;
+                if (ow >= Wo) continue;
+                const int64_t k = ((int64_t)c * kh + r) * kw + s;
+                acc += dcol[k * NP + (img * Ho + oh) * Wo + ow];
+            }
+        }
+        dx[e] = acc;
+    }
+}
+
+// db[c] = beta*db[c] + Σ_{img, hw} dY[img][c][hw]; one workgroup per channel,
+// fixed-order tree reduction.
+__global__ void __launch_bounds__(256)
+conv_bias_grad_f32(const float* dy, float* db, int N, int C, int64_t HW, float beta) {
+    __shared__ float red[256];
+    const int c = blockIdx.x;
+    const int t = threadIdx.x;
+    float s = 0.f;
+    const int64_t total = (int64_t)N * HW;
+    for (int64_t i = t; i < total; i += 256) {
+        const int64_t img = i / HW, hw = i - img * HW;
+        s += dy[(img * C + c) * HW + hw];
+    }
+    red[t] = s;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (t < w) red[t] += red[t + w];
+        __syncthreads();
+    }
+    if (t == 0) db[c] = (beta != 0.f ? beta * db[c] : 0.f) + red[0];
+}
+
+// dY [n][c_out][hw] -> dYt [c_out][n][hw] (contiguous), through the axpby kernel.
+hipError_t transpose_dy(const mt_conv2d_desc* d, int64_t hw, const float* dy, float* dyt,
+                        hipStream_t s) {
+    const int64_t total = d->c_out * d->n * hw;
+    hipLaunchKernelGGL(axpby_f32, dim3(grid_for(total)), dim3(256), 0, s, dy, hw,
+                       d->c_out * hw, (int64_t)1, 1.0f, dyt, d->n * hw, hw, (int64_t)1, 0.0f,
+                       d->n, hw, total);
+    return capture_safe_last_error();
+}
+
+hipError_t launch_im2col(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, const float* input,
+                         float* col, hipStream_t s) {
+    const int64_t kg = d->c_in * d->kh * d->kw, np = d->n * Ho * Wo;
+    dim3 grid((unsigned)((np + 255) / 256), (unsigned)((kg + kIm2colK - 1) / kIm2colK));
+    hipLaunchKernelGGL(im2col_f32, grid, dim3(256), 0, s, input, col, (int)d->c_in, (int)d->h,
+                       (int)d->w, (int)d->kh, (int)d->kw, (int)d->stride, (int)d->pad, (int)Ho,
+                       (int)Wo, np, kg);
+    return capture_safe_last_error();
+}
+
 }  // namespace
 
 extern "C" {
@@ -445,19 +549,129 @@ int mt_conv2d_fwd_f32(const mt_conv2d_desc* d, const float* input, const float* 
     if (kg > 0 && (!workspace || ws_bytes < col_bytes)) return MT_ERR_WORKSPACE;
     hipStream_t s = static_cast<hipStream_t>(stream);
     float* col = static_cast<float*>(workspace);
-    if (kg > 0) {
-        dim3 grid((unsigned)((np + 255) / 256), (unsigned)((kg + kIm2colK - 1) / kIm2colK));
-        hipLaunchKernelGGL(im2col_f32, grid, dim3(256), 0, s, input, col, (int)d->c_in, (int)d->h,
-                           (int)d->w, (int)d->kh, (int)d->kw, (int)d->stride, (int)d->pad, (int)Ho,
-                           (int)Wo, np, kg);
-        if (capture_safe_last_error() != hipSuccess) return MT_ERR_HIP;
-    }
+    if (kg > 0 && launch_im2col(d, Ho, Wo, input, col, s) != hipSuccess) return MT_ERR_HIP;
     mt_mat_f32 A, B, C;
     conv_gemm_views(d, Ho, Wo, weight, col, output, &A, &B, &C);
     mt_epilogue_f32 ep{bias, 1, bias ? MT_BIAS_ROW : MT_BIAS_NONE, 0.f};
     char* gws = static_cast<char*>(workspace) + (kg > 0 ? col_bytes : 0);
     const size_t gws_bytes = ws_bytes > col_bytes ? ws_bytes - col_bytes : 0;
     return run_gemm(&A, &B, &C, Ho * Wo, d->c_out * Ho * Wo, &ep, gws, gws_bytes, s);
+}
+
+size_t mt_conv2d_bwd_workspace_f32(const mt_conv2d_desc* d) {
+    int64_t Ho, Wo;
+    if (!conv_dims(d, &Ho, &Wo)) return 0;
+    const int64_t kg = d->c_in * d->kh * d->kw, np = d->n * Ho * Wo;
+    if (np == 0 || d->c_out == 0 || kg == 0) return 0;
+    const int cus = device_cu_count();
+    const size_t bufs = align_up((size_t)kg * np * sizeof(float), 256) +
+                        align_up((size_t)d->c_out * np * sizeof(float), 256);
+    const size_t g = std::max(make_plan(d->c_out, kg, np, 1, cus, true).ws_bytes,
+                              make_plan(kg, np, d->c_out, 1, cus, true).ws_bytes);
+    return bufs + g;
+}
+
+int mt_conv2d_bwd_weight_f32(const mt_conv2d_desc* d, const float* input, const float* grad_out,
+                             float* grad_weight, float beta, void* workspace, size_t ws_bytes,
+                             void* stream) {
+    int64_t Ho, Wo;
+    if (!conv_dims(d, &Ho, &Wo)) return MT_ERR_INVALID;
+    const int64_t kg = d->c_in * d->kh * d->kw, np = d->n * Ho * Wo, hw = Ho * Wo;
+    if (kg == 0 || d->c_out == 0) return MT_OK;
+    if (!grad_weight) return MT_ERR_INVALID;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const size_t col_b = align_up((size_t)kg * np * sizeof(float), 256);
+    const size_t dyt_b = align_up((size_t)d->c_out * np * sizeof(float), 256);
+    if (np > 0) {
+        if (!input || !grad_out) return MT_ERR_INVALID;
+        if (!workspace || ws_bytes < col_b + dyt_b) return MT_ERR_WORKSPACE;
+    }
+    float* col = static_cast<float*>(workspace);
+    float* dyt = reinterpret_cast<float*>(static_cast<char*>(workspace) + col_b);
+    if (np > 0) {
+        if (launch_im2col(d, Ho, Wo, input, col, s) != hipSuccess) return MT_ERR_HIP;
+        if (transpose_dy(d, hw, grad_out, dyt, s) != hipSuccess) return MT_ERR_HIP;
+    }
+    // dW[c_out, kg] = dYt[c_out, np] · colᵀ[np, kg]
+    const mt_mat_f32 A{dyt, 0, d->c_out, np, np, 1, 1, 0};
+    const mt_mat_f32 B{col, 0, np, kg, 1, np, 1, 0};
+    const mt_mat_f32 C{grad_weight, 0, d->c_out, kg, kg, 1, 1, 0};
+    const mt_epilogue_f32 ep{nullptr, 0, MT_BIAS_NONE, beta};
+    char* gws = static_cast<char*>(workspace) + col_b + dyt_b;
+    const size_t gws_b = ws_bytes > col_b + dyt_b ? ws_bytes - col_b - dyt_b : 0;
+    return run_gemm(&A, &B, &C, 0, 0, &ep, np > 0 ? gws : nullptr, np > 0 ? gws_b : 0, s);
+}
+
+int mt_conv2d_bwd_input_f32(const mt_conv2d_desc* d, const float* grad_out, const float* weight,
+                            float* grad_input, void* workspace, size_t ws_bytes, void* stream) {
+    int64_t Ho, Wo;
+    if (!conv_dims(d, &Ho, &Wo)) return MT_ERR_INVALID;
+    const int64_t kg = d->c_in * d->kh * d->kw, np = d->n * Ho * Wo, hw = Ho * Wo;
+    const int64_t total = d->n * d->c_in * d->h * d->w;
+    if (total == 0) return MT_OK;
+    if (!grad_input) return MT_ERR_INVALID;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (np == 0 || d->c_out == 0) {  // no output position touches the input
+        hipLaunchKernelGGL(fill_f32, dim3(grid_for(total)), dim3(256), 0, s, grad_input, total, 0.f);
+        return capture_safe_last_error() == hipSuccess ? MT_OK : MT_ERR_HIP;
+    }
+    if (!grad_out || !weight) return MT_ERR_INVALID;
+    const size_t col_b = align_up((size_t)kg * np * sizeof(float), 256);
+    const size_t dyt_b = align_up((size_t)d->c_out * np * sizeof(float), 256);
+    if (!workspace || ws_bytes < col_b + dyt_b) return MT_ERR_WORKSPACE;
+    float* dcol = static_cast<float*>(workspace);
+    float* dyt = reinterpret_cast<float*>(static_cast<char*>(workspace) + col_b);
+    if (transpose_dy(d, hw, grad_out, dyt, s) != hipSuccess) return MT_ERR_HIP;
+    // dcol[kg, np] = Wᵀ[kg, c_out] · dYt[c_out, np]
+    const mt_mat_f32 A{weight, 0, kg, d->c_out, 1, kg, 1, 0};
+    const mt_mat_f32 B{dyt, 0, d->c_out, np, np, 1, 1, 0};
+    const mt_mat_f32 C{dcol, 0, kg, np, np, 1, 1, 0};
+    char* gws = static_cast<char*>(workspace) + col_b + dyt_b;
+    const size_t gws_b = ws_bytes - col_b - dyt_b;
+    int rc = run_gemm(&A, &B, &C, 0, 0, nullptr, gws, gws_b, s);
+    if (rc != MT_OK) return rc;
+    hipLaunchKernelGGL(col2im_gather_f32, dim3(grid_for(total)), dim3(256), 0, s, dcol, grad_input,
+                       (int)d->c_in, (int)d->h, (int)d->w, (int)d->kh, (int)d->kw, (int)d->stride,
+                       (int)d->pad, (int)Ho, (int)Wo, np, total);
+    return capture_safe_last_error() == hipSuccess ? MT_OK : MT_ERR_HIP;
+}
+
+int mt_conv2d_bwd_bias_f32(const mt_conv2d_desc* d, const float* grad_out, float* grad_bias,
+                           float beta, void* stream) {
+    int64_t Ho, Wo;
+    if (!conv_dims(d, &Ho, &Wo)) return MT_ERR_INVALID;
+    if (d->c_out == 0) return MT_OK;
+    if (!grad_bias || (d->n * Ho * Wo > 0 && !grad_out)) return MT_ERR_INVALID;
+    hipLaunchKernelGGL(conv_bias_grad_f32, dim3((unsigned)d->c_out), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), grad_out, grad_bias, (int)d->n,
+                       (int)d->c_out, Ho * Wo, beta);
+    return capture_safe_last_error() == hipSuccess ? MT_OK : MT_ERR_HIP;
+}
+
+int mt_fill_f32(float* p, int64_t n, float value, void* stream) {
+    if (n < 0 || (n > 0 && !p)) return MT_ERR_INVALID;
+    if (n == 0) return MT_OK;
+    hipLaunchKernelGGL(fill_f32, dim3(grid_for(n)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       p, n, value);
+    return capture_safe_last_error() == hipSuccess ? MT_OK : MT_ERR_HIP;
+}
+
+int mt_axpby_f32(const mt_mat_f32* X, float alpha, const mt_mat_f32* Y, float beta, void* stream) {
+    if (!valid_mat(X) || !valid_mat(Y)) return MT_ERR_INVALID;
+    if (X->rows != Y->rows || X->cols != Y->cols || (X->batch != 1 && X->batch != Y->batch))
+        return MT_ERR_INVALID;
+    const int64_t total = Y->batch * Y->rows * Y->cols;
+    if (total == 0) return MT_OK;
+    if (!X->base || !Y->base) return MT_ERR_INVALID;
+    if ((Y->rows > 1 && Y->row_stride == 0) || (Y->cols > 1 && Y->col_stride == 0) ||
+        (Y->batch > 1 && Y->batch_stride == 0))
+        return MT_ERR_INVALID;
+    hipLaunchKernelGGL(axpby_f32, dim3(grid_for(total)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), X->base + X->offset,
+                       X->batch == 1 ? 0 : X->batch_stride, X->row_stride, X->col_stride, alpha,
+                       const_cast<float*>(Y->base) + Y->offset, Y->batch_stride, Y->row_stride,
+                       Y->col_stride, beta, Y->rows, Y->cols, total);
+    return capture_safe_last_error() == hipSuccess ? MT_OK : MT_ERR_HIP;
 }
 
 const char* mt_strerror(int status) {

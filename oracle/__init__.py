@@ -57,6 +57,9 @@ def lib() -> ctypes.CDLL:
         h.ora_bmm.argtypes = [_f, _f, _f, _sz, _sz, _sz, _sz]
         h.ora_conv2d.argtypes = [_f, _f, _f, _f] + [_sz] * 9
         h.ora_colsum.argtypes = [_f, _sz, _sz, _sz, _sz, _f]
+        h.ora_conv2d_bwd_input.argtypes = [_f, _f, _f] + [_sz] * 9
+        h.ora_conv2d_bwd_weight.argtypes = [_f, _f, _f] + [_sz] * 9
+        h.ora_conv2d_bwd_bias.argtypes = [_f, _f] + [_sz] * 4
         h.ora_matmul_f64_rows.argtypes = [_f, _sz, _sz, _f, _sz, _sz, _i64, _sz, _sz, _sz, _d]
         _lib = h
     return _lib
@@ -78,6 +81,7 @@ def ref() -> ctypes.CDLL:
                                           _sz, _sz, _sz, _f]
         h.ref_conv2d_f32.argtypes = [_f, _f, _f, _f] + [_sz] * 9
         h.ref_linear_f32.argtypes = [_f, _f, _f, _f, _sz, _sz, _sz, _f, _f, _f, _f]
+        h.ref_conv2d_bwd_f32.argtypes = [_f, _f, _f, _f, _f, _f] + [_sz] * 9
         _ref = h
     return _ref
 
@@ -157,6 +161,20 @@ def conv2d(x: np.ndarray, w: np.ndarray, b: Optional[np.ndarray], stride: int, p
     lib().ora_conv2d(_fp(x), _fp(w), _fp(np.ascontiguousarray(b)) if b is not None else None,
                      _fp(out), n, c, h, wd, co, kh, kw, stride, pad)
     return out
+
+
+def conv2d_backward(x: np.ndarray, w: np.ndarray, dy: np.ndarray, stride: int, pad: int):
+    """conv2d_backward_{input,weight,bias}_cpu: returns (dX, dW, db)."""
+    x, w, dy = (np.ascontiguousarray(t) for t in (x, w, dy))
+    n, c, h, wd = x.shape
+    co, _, kh, kw = w.shape
+    dx = np.empty_like(x)
+    dw = np.empty_like(w)
+    db = np.empty((co,), np.float32)
+    lib().ora_conv2d_bwd_input(_fp(dy), _fp(w), _fp(dx), n, c, h, wd, co, kh, kw, stride, pad)
+    lib().ora_conv2d_bwd_weight(_fp(dy), _fp(x), _fp(dw), n, c, h, wd, co, kh, kw, stride, pad)
+    lib().ora_conv2d_bwd_bias(_fp(dy), _fp(db), n, co, dy.shape[2], dy.shape[3])
+    return dx, dw, db
 
 
 def colsum(x: np.ndarray) -> np.ndarray:

@@ -14,6 +14,9 @@
  *   ora_matmul_strided  include/TensorOps.hpp:162-189  matmul_cpu_strided
  *   ora_bmm             include/TensorOps.hpp:933-991  bmm's intent: matmul_cpu per batch
  *   ora_conv2d          include/TensorOps.hpp:235-273  conv2d_cpu (bias first, c_in->r->s)
+ *   ora_conv2d_bwd_input  include/TensorOps.hpp:318-353  conv2d_backward_input_cpu (scatter order)
+ *   ora_conv2d_bwd_weight include/TensorOps.hpp:355-394  conv2d_backward_weight_cpu (per-image sums)
+ *   ora_conv2d_bwd_bias   include/TensorOps.hpp:396-415  conv2d_backward_bias_cpu (per-image sums)
  *   ora_colsum          include/TensorOps.hpp:190-233  sum_cpu over axis 0 (sequential)
  *   ora_matmul_f64_rows (checker) fp64 brute force of selected rows
  *   ora_mt19937_*, ora_fill_*  deterministic seeded inputs (std::mt19937 + own transforms)
@@ -128,6 +131,65 @@ void ora_conv2d(const float* in, const float* w, const float* bias, float* out, 
                             }
                     out[n * (C_out * H_out * W_out) + co * (H_out * W_out) + y * W_out + x] = val;
                 }
+}
+
+static size_t out_dim(size_t in, size_t pad, size_t k, size_t stride) {
+    return (in + 2 * pad < k) ? 0 : (in + 2 * pad - k) / stride + 1;
+}
+
+void ora_conv2d_bwd_input(const float* go, const float* w, float* gi, size_t N, size_t C_in,
+                          size_t H, size_t W, size_t C_out, size_t kH, size_t kW, size_t stride,
+                          size_t pad) {
+    const size_t Ho = out_dim(H, pad, kH, stride), Wo = out_dim(W, pad, kW, stride);
+    memset(gi, 0, N * C_in * H * W * sizeof(float));
+    for (size_t n = 0; n < N; ++n)
+        for (size_t co = 0; co < C_out; ++co)
+            for (size_t y = 0; y < Ho; ++y)
+                for (size_t x = 0; x < Wo; ++x) {
+                    const float g = go[n * (C_out * Ho * Wo) + co * (Ho * Wo) + y * Wo + x];
+                    for (size_t ci = 0; ci < C_in; ++ci)
+                        for (size_t r = 0; r < kH; ++r)
+                            for (size_t s = 0; s < kW; ++s) {
+                                const long iy = (long)(y * stride + r) - (long)pad;
+                                const long ix = (long)(x * stride + s) - (long)pad;
+                                if (iy >= 0 && iy < (long)H && ix >= 0 && ix < (long)W)
+                                    gi[n * (C_in * H * W) + ci * (H * W) + (size_t)iy * W + (size_t)ix] +=
+                                        g * w[co * (C_in * kH * kW) + ci * (kH * kW) + r * kW + s];
+                            }
+                }
+}
+
+void ora_conv2d_bwd_weight(const float* go, const float* in, float* gw, size_t N, size_t C_in,
+                           size_t H, size_t W, size_t C_out, size_t kH, size_t kW, size_t stride,
+                           size_t pad) {
+    const size_t Ho = out_dim(H, pad, kH, stride), Wo = out_dim(W, pad, kW, stride);
+    memset(gw, 0, C_out * C_in * kH * kW * sizeof(float));
+    for (size_t n = 0; n < N; ++n)
+        for (size_t co = 0; co < C_out; ++co)
+            for (size_t ci = 0; ci < C_in; ++ci)
+                for (size_t r = 0; r < kH; ++r)
+                    for (size_t s = 0; s < kW; ++s) {
+                        float sum = 0.0f;
+                        for (size_t y = 0; y < Ho; ++y)
+                            for (size_t x = 0; x < Wo; ++x) {
+                                const long iy = (long)(y * stride + r) - (long)pad;
+                                const long ix = (long)(x * stride + s) - (long)pad;
+                                if (iy >= 0 && iy < (long)H && ix >= 0 && ix < (long)W)
+                                    sum += in[n * (C_in * H * W) + ci * (H * W) + (size_t)iy * W + (size_t)ix] *
+                                           go[n * (C_out * Ho * Wo) + co * (Ho * Wo) + y * Wo + x];
+                            }
+                        gw[co * (C_in * kH * kW) + ci * (kH * kW) + r * kW + s] += sum;
+                    }
+}
+
+void ora_conv2d_bwd_bias(const float* go, float* gb, size_t N, size_t C_out, size_t Ho, size_t Wo) {
+    memset(gb, 0, C_out * sizeof(float));
+    for (size_t n = 0; n < N; ++n)
+        for (size_t c = 0; c < C_out; ++c) {
+            float sum = 0.0f;
+            for (size_t i = 0; i < Ho * Wo; ++i) sum += go[n * (C_out * Ho * Wo) + c * (Ho * Wo) + i];
+            gb[c] += sum;
+        }
 }
 
 void ora_colsum(const float* x, size_t rs, size_t cs, size_t R, size_t Cn, float* out) {

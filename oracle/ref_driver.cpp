@@ -77,6 +77,26 @@ int ref_conv2d_f32(const float* in, const float* w, const float* bias, float* ou
     return 0;
 }
 
+// conv2d backward through the reference's autograd (Conv2DBackward ->
+// conv2d_backward_{input,weight,bias}_cpu), with dY installed as the output gradient.
+int ref_conv2d_bwd_f32(const float* in, const float* w, const float* dy, float* dx, float* dw,
+                       float* db, size_t N, size_t C, size_t H, size_t W, size_t Cout, size_t kh,
+                       size_t kw, size_t stride, size_t pad) {
+    Tensor<float> I = dense(in, {N, C, H, W});
+    Tensor<float> Wt = dense(w, {Cout, C, kh, kw});
+    Tensor<float> Bt({Cout});
+    I.set_requires_grad(true);
+    Wt.set_requires_grad(true);
+    Bt.set_requires_grad(true);
+    Tensor<float> Y = conv2d(I, Wt, Bt, stride, pad);
+    Y.grad() = dense(dy, Y.shape());
+    Y.backward();
+    copy_out(I.grad().contiguous(), dx);
+    copy_out(Wt.grad().contiguous(), dw);
+    copy_out(Bt.grad().contiguous(), db);
+    return 0;
+}
+
 // The reference Linear: W_ref [in,out], bias [1,out]; Y = matmul(X, W_ref) + bias.
 // The upstream gradient dY is installed as Y's gradient before backward().
 int ref_linear_f32(const float* x, const float* w_ref, const float* bias, const float* dy,

@@ -163,3 +163,47 @@ def test_config5a_conv(dev):
     bound = 256 * 1e-5 * 48 * amax(x) * amax(w) + 1e-3
     print(f"[parity] C5a channel-sum: max|err|={err:.3e} bound={bound:.3e}")
     assert err <= bound
+
+
+@pytest.mark.parametrize("n,c,h,wd,co,kh,kw,stride,pad", [
+    (2, 3, 9, 7, 4, 3, 3, 1, 1),
+    (1, 2, 8, 8, 3, 3, 2, 2, 0),
+    (3, 4, 5, 6, 2, 1, 1, 1, 0),
+    (2, 2, 7, 7, 3, 5, 5, 3, 2),
+    (4, 3, 32, 32, 16, 3, 3, 2, 1),   # the reference's device-equivalence conv shape
+])
+def test_conv_backward_shapes(dev, n, c, h, wd, co, kh, kw, stride, pad):
+    x = oracle.normal((n, c, h, wd), 1)
+    w = oracle.normal((co, c, kh, kw), 2)
+    ho, wo = oracle.conv_out(h, pad, kh, stride), oracle.conv_out(wd, pad, kw, stride)
+    dy = oracle.normal((n, co, ho, wo), 3)
+    dx, dw, db = mt.conv2d_backward(g(x, dev), g(w, dev), g(dy, dev), stride, pad)
+    dx, dw, db = sync_np(dx), sync_np(dw), sync_np(db)
+    wdx, wdw, wdb = oracle.conv2d_backward(x, w, dy, stride, pad)
+    assert_close(dx, wdx, co * kh * kw, amax(dy), amax(w), "conv dX")
+    assert_close(dw, wdw, n * ho * wo, amax(dy), amax(x), "conv dW")
+    assert_close(db, wdb, n * ho * wo, amax(dy), 1.0, "conv db")
+
+
+def test_config5a_conv_backward_adjoint(dev):
+    # BASELINE config 5a shape: dX and dW through the GEMM path, checked by the
+    # size-independent adjoint identities <dY, conv(x,w)> = <dX, x> = <dW, w>
+    # (fp64 sums over every element), plus 8 sampled dW output channels against
+    # the oracle's conv2d_backward_weight_cpu.
+    x = oracle.normal((32, 256, 14, 14), 42)
+    w = oracle.normal((256, 256, 3, 3), 43, std=(2.0 / 2304) ** 0.5)
+    dy = oracle.normal((32, 256, 14, 14), 44, std=0.01)
+    X, W, dY = g(x, dev), g(w, dev), g(dy, dev)
+    y = mt.conv2d(X, W, None, 1, 1)
+    dx, dw, db = mt.conv2d_backward(X, W, dY, 1, 1)
+    y, dx, dw, db = sync_np(y), sync_np(dx), sync_np(dw), sync_np(db)
+    ip = float(np.sum(dy.astype(np.float64) * y))
+    ipx = float(np.sum(dx.astype(np.float64) * x))
+    ipw = float(np.sum(dw.astype(np.float64) * w))
+    scale = float(np.sum(np.abs(dy.astype(np.float64) * y))) + 1.0
+    print(f"[parity] C5a adjoint: <dY,y>={ip:.6f} <dX,x>={ipx:.6f} <dW,w>={ipw:.6f}")
+    assert abs(ipx - ip) <= 1e-5 * scale and abs(ipw - ip) <= 1e-5 * scale
+    ch = np.arange(0, 256, 32)
+    _, wdw, wdb = oracle.conv2d_backward(x, w[ch], dy[:, ch], 1, 1)
+    assert_close(dw[ch], wdw, 32 * 196, amax(dy), amax(x), "C5a dW sampled channels")
+    assert_close(db, dy.astype(np.float64).sum(axis=(0, 2, 3)), 32 * 196, amax(dy), 1.0, "C5a db")

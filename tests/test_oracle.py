@@ -267,3 +267,35 @@ def test_planted_transpose_mistake_is_caught():
     # and a dropped last k term as well
     dropped = oracle.matmul(a[:, :-1], b[:-1])
     assert np.max(np.abs(dropped - oracle.matmul_f64_rows(a, b, range(24)))) > tol(24, 1, 1)
+
+
+@needs_ref
+@pytest.mark.parametrize("n,c,h,w,co,kh,kw,stride,pad", [
+    (2, 3, 9, 7, 4, 3, 3, 1, 1), (1, 2, 8, 8, 3, 3, 2, 2, 0), (3, 4, 5, 6, 2, 1, 1, 1, 0),
+    (2, 2, 7, 7, 3, 5, 5, 3, 2)])
+def test_conv_backward_matches_reference_build(n, c, h, w, co, kh, kw, stride, pad):
+    x = oracle.normal((n, c, h, w), 1)
+    wt = oracle.normal((co, c, kh, kw), 2)
+    ho, wo = oracle.conv_out(h, pad, kh, stride), oracle.conv_out(w, pad, kw, stride)
+    dy = oracle.normal((n, co, ho, wo), 3)
+    dx, dw, db = oracle.conv2d_backward(x, wt, dy, stride, pad)
+    rdx, rdw, rdb = np.empty_like(dx), np.empty_like(dw), np.empty_like(db)
+    oracle.ref().ref_conv2d_bwd_f32(*[oracle._fp(t) for t in (x, wt, dy, rdx, rdw, rdb)],
+                                    n, c, h, w, co, kh, kw, stride, pad)
+    np.testing.assert_array_equal(dx, rdx)
+    np.testing.assert_array_equal(dw, rdw)
+    np.testing.assert_array_equal(db, rdb)
+
+
+def test_conv_backward_adjoint_identities():
+    # conv is bilinear: <dY, conv(x, w)> = <dX(dY, w), x> = <dW(dY, x), w>  (bias 0)
+    x = oracle.normal((2, 3, 8, 9), 1)
+    w = oracle.normal((4, 3, 3, 3), 2)
+    for stride, pad in [(1, 1), (2, 0), (2, 2)]:
+        y = oracle.conv2d(x, w, None, stride, pad)
+        dy = oracle.normal(y.shape, 3)
+        dx, dw, db = oracle.conv2d_backward(x, w, dy, stride, pad)
+        ip = float(np.sum(dy.astype(np.float64) * y))
+        assert abs(float(np.sum(dx.astype(np.float64) * x)) - ip) <= 1e-4 * (1 + abs(ip))
+        assert abs(float(np.sum(dw.astype(np.float64) * w)) - ip) <= 1e-4 * (1 + abs(ip))
+        np.testing.assert_allclose(db, dy.astype(np.float64).sum(axis=(0, 2, 3)), atol=1e-4)
