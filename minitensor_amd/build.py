@@ -40,6 +40,8 @@ def _units():
     units = []
     for cfg in range(N_CFG):
         units.append((CSRC / "gemm_instances.hip", OBJDIR / f"gemm_cfg{cfg}.o", [f"-DMT_CFG={cfg}"]))
+        units.append((CSRC / "gemm_dl_instances.hip", OBJDIR / f"gemm_dl_cfg{cfg}.o",
+                      [f"-DMT_CFG={cfg}"]))
     units.append((CSRC / "mtgemm_api.hip", OBJDIR / "mtgemm_api.o", []))
     return units
 

@@ -33,4 +33,25 @@ GemmLaunchFn launcher_cfg0(int la, int lb);
 GemmLaunchFn launcher_cfg1(int la, int lb);
 GemmLaunchFn launcher_cfg2(int la, int lb);
 
+// Direct-to-LDS kernel (gemm_dl_kernel.hpp) for operands whose layouts are both
+// L_KV or L_MV: block tile BM x BN, wave tile WM x WN, STAGES-deep LDS ring of
+// 16-deep K-chunks.  Same tile sizes, in the same order, as TileCfg.
+template <int CFG> struct DlCfg;
+// 8 waves of 128x64; 2 x 32 KB ring.
+template <> struct DlCfg<0> { static constexpr int BM = 256, BN = 256, WM = 128, WN = 64, STAGES = 2; };
+// 8 waves of 64x32; 4 x 16 KB ring, two workgroups per CU.
+template <> struct DlCfg<1> { static constexpr int BM = 128, BN = 128, WM = 64, WN = 32, STAGES = 4; };
+// 4 waves of 32x32; 4 x 8 KB ring.
+template <> struct DlCfg<2> { static constexpr int BM = 64, BN = 64, WM = 32, WN = 32, STAGES = 4; };
+
+template <int CFG>
+constexpr int dl_threads() {
+    return (DlCfg<CFG>::BM / DlCfg<CFG>::WM) * (DlCfg<CFG>::BN / DlCfg<CFG>::WN) * 64;
+}
+
+// la, lb in {L_KV, L_MV}.
+GemmLaunchFn dl_launcher_cfg0(int la, int lb);
+GemmLaunchFn dl_launcher_cfg1(int la, int lb);
+GemmLaunchFn dl_launcher_cfg2(int la, int lb);
+
 }  // namespace mtk

@@ -1,0 +1,47 @@
+// gemm_dl_instances.hip -- instantiates gemm_f32_dl for one tile
+// configuration (selected with -DMT_CFG=<n>) and the 2x2 vector operand
+// layouts (k-contiguous / mn-contiguous for A and for B).
+#include "gemm_configs.hpp"
+#include "gemm_dl_kernel.hpp"
+
+#ifndef MT_CFG
+#error "build with -DMT_CFG=<tile configuration index>"
+#endif
+
+namespace mtk {
+namespace {
+
+template <int CFG, int LA, int LB>
+hipError_t launch_dl(const GemmParams& p, unsigned nblocks, hipStream_t s) {
+    using C = DlCfg<CFG>;
+    hipLaunchKernelGGL((gemm_f32_dl<C::BM, C::BN, C::WM, C::WN, LA, LB, C::STAGES>),
+                       dim3(nblocks), dim3(dl_threads<CFG>()), 0, s, p);
+    return hipGetLastError();
+}
+
+#define MT_DL_TABLE(CFG) \
+    { { launch_dl<CFG, L_KV, L_KV>, launch_dl<CFG, L_KV, L_MV> }, \
+      { launch_dl<CFG, L_MV, L_KV>, launch_dl<CFG, L_MV, L_MV> } }
+
+}  // namespace
+
+#if MT_CFG == 0
+GemmLaunchFn dl_launcher_cfg0(int la, int lb) {
+    static const GemmLaunchFn table[2][2] = MT_DL_TABLE(0);
+    return table[la][lb];
+}
+#elif MT_CFG == 1
+GemmLaunchFn dl_launcher_cfg1(int la, int lb) {
+    static const GemmLaunchFn table[2][2] = MT_DL_TABLE(1);
+    return table[la][lb];
+}
+#elif MT_CFG == 2
+GemmLaunchFn dl_launcher_cfg2(int la, int lb) {
+    static const GemmLaunchFn table[2][2] = MT_DL_TABLE(2);
+    return table[la][lb];
+}
+#else
+#error "unknown MT_CFG"
+#endif
+
+}  // namespace mtk

@@ -1,0 +1,262 @@
+// gemm_dl_kernel.hpp -- fp32 MFMA GEMM whose operand tiles travel from HBM
+// straight into LDS (gfx950 global_load_lds_dwordx4), for operands with a
+// 16-byte vector layout (L_KV or L_MV).
+//
+// Same mathematics, tile mapping and epilogue as gemm_f32_mfma; the difference
+// is the data path:
+//   * No VGPR staging.  Each wave instruction moves 64 lanes x 16 B = 1 KB of
+//     one operand tile into LDS asynchronously, so the loads cost neither
+//     registers nor the issue slots of a register -> ds_write round trip, and
+//     the number of K-chunks in flight is limited only by LDS.
+//   * K advances in chunks of 16 through a ring of STAGES LDS slots: while
+//     chunk kt is multiplied, chunks kt+1 .. kt+STAGES-1 are in flight.  One
+//     s_barrier per chunk; each wave first waits (vmcnt) only for its own
+//     instructions of chunk kt, since the later ones may still be landing.
+//   * LDS tiles are unpadded (the DMA writes 1 KB contiguous per
+//     instruction):  k-contiguous operands -> [BMN][16], with the four 16-B
+//     k-groups of row r stored at position g ^ ((r >> 1) & 3), so that the
+//     fragment reads (two ds_read_b128 per lane, 32 rows at stride 64 B) hit
+//     every bank group once;  mn-contiguous operands -> [16][BMN].
+//   * Rows beyond M (or N) read a clamped, valid row: their products only
+//     reach output rows/columns that the epilogue never writes.
+//   * A K range that is not a multiple of 16 ends in a partial chunk.  It is
+//     fetched first, with bounds-checked scalar loads that write zeros past
+//     k_end, into the last ring slot (which the prologue leaves free), and
+//     multiplied before the pipelined loop starts; the prologue's DMA
+//     overlaps it.
+// K permutation, MFMA operand layouts and the accumulator layout are the ones
+// documented in gemm_kernel.hpp.
+#pragma once
+
+#include "gemm_kernel.hpp"
+
+namespace mtk {
+
+// Geometry of one 16-deep K-chunk of an operand tile with BMN rows, moved by
+// NW waves.
+template <int L, int BMN, int NW>
+struct DlTile {
+    static_assert(L == L_KV || L == L_MV, "direct-to-LDS needs a 16-byte vector layout");
+    static constexpr bool kc = (L == L_KV);
+    static constexpr int floats = BMN * 16;
+    static constexpr int insts = floats / 256;            // 256 floats per wave instruction
+    static_assert(insts % NW == 0, "tile must split evenly over the waves");
+    static constexpr int per_wave = insts / NW;
+};
+
+// Position (in 16-B groups) of k-group g of row r inside a k-contiguous tile.
+__device__ __forceinline__ int kswz(int r) { return (r >> 1) & 3; }
+
+template <int L, int BMN, int NW>
+struct DlLoader {
+    using T = DlTile<L, BMN, NW>;
+    const float* src[T::per_wave];   // this lane's source for each instruction, chunk 0
+    int64_t kstep;                    // elements between consecutive K-chunks
+
+    // X points at element (0, 0) of the operand (batch applied); mn0/k0 are the
+    // tile's first row and first k.  MN % 4 == 0 for L_MV (checked on the host).
+    __device__ __forceinline__ void init(const float* X, int64_t s_mn, int64_t s_k, int MN,
+                                         int mn0, int k0, int wave, int lane) {
+        kstep = 16 * s_k;
+#pragma unroll
+        for (int j = 0; j < T::per_wave; ++j) {
+            const int q = j * NW + wave;                  // instruction index within the chunk
+            if constexpr (T::kc) {
+                // 16 rows x 4 groups of 4 k per instruction; lane -> (row, slot).
+                const int r = q * 16 + (lane >> 2);
+                const int g = (lane & 3) ^ kswz(r);       // k-group that lands in slot lane&3
+                const int64_t row = min((int64_t)mn0 + r, (int64_t)MN - 1);
+                src[j] = X + row * s_mn + (int64_t)(k0 + g * 4) * s_k;
+            } else {
+                const int e = q * 256 + lane * 4;         // float index within [16][BMN]
+                const int kr = e / BMN, mn = e - kr * BMN;
+                const int64_t col = min((int64_t)mn0 + mn, (int64_t)MN - 4);
+                src[j] = X + (int64_t)(k0 + kr) * s_k + col;
+            }
+        }
+    }
+
+    // Issue the DMA of K-chunk `chunk` into the LDS tile at `tile`.
+    __device__ __forceinline__ void issue(float* tile, int chunk, int wave) const {
+#pragma unroll
+        for (int j = 0; j < T::per_wave; ++j) {
+            const int q = j * NW + wave;
+            __builtin_amdgcn_global_load_lds(
+                (const void __attribute__((address_space(1)))*)(src[j] + chunk * kstep),
+                (void __attribute__((address_space(3)))*)(tile + q * 256), 16, 0, 0);
+        }
+    }
+};
+
+// Bounds-checked fetch of the partial chunk [kt0, k_end) of one operand tile,
+// zero past k_end, in the same LDS layout as the DMA path.
+template <int L, int BMN, int NT>
+struct DlTail {
+    static constexpr int NI = BMN * 16 / NT;
+    static_assert(NI * NT == BMN * 16, "tail must split evenly over the threads");
+    float v[NI];
+
+    __device__ __forceinline__ void load(const float* X, int64_t s_mn, int64_t s_k, int MN,
+                                         int mn0, int kt0, int k_end, int t) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int e = t + i * NT;
+            int r, kk;
+            if constexpr (L == L_KV) { r = e >> 4; kk = e & 15; }
+            else { kk = e / BMN; r = e - kk * BMN; }
+            const int64_t row = min((int64_t)mn0 + r, (int64_t)MN - 1);
+            v[i] = (kt0 + kk < k_end) ? X[row * s_mn + (int64_t)(kt0 + kk) * s_k] : 0.f;
+        }
+    }
+
+    __device__ __forceinline__ void store(float* tile, int t) const {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int e = t + i * NT;
+            if constexpr (L == L_KV) {
+                const int r = e >> 4, kk = e & 15;
+                tile[r * 16 + ((((kk >> 2) ^ kswz(r))) << 2) + (kk & 3)] = v[i];
+            } else {
+                tile[e] = v[i];
+            }
+        }
+    }
+};
+
+// The 8 k-values (permuted order) of one 32-row MFMA block from a chunk tile.
+template <int L, int BMN>
+__device__ __forceinline__ void dl_frag(const float* tile, int row0, int lane, float (&f)[8]) {
+    const int h = lane >> 5, c = lane & 31;
+    if constexpr (L == L_KV) {
+        const int r = row0 + c;
+        const float* rp = tile + r * 16;
+        const f32x4 x = *reinterpret_cast<const f32x4*>(rp + (((2 * h) ^ kswz(r)) * 4));
+        const f32x4 y = *reinterpret_cast<const f32x4*>(rp + (((2 * h + 1) ^ kswz(r)) * 4));
+        f[0] = x[0]; f[1] = x[1]; f[2] = x[2]; f[3] = x[3];
+        f[4] = y[0]; f[5] = y[1]; f[6] = y[2]; f[7] = y[3];
+    } else {
+        const float* q = tile + (h * 8) * BMN + row0 + c;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) f[s] = q[s * BMN];
+    }
+}
+
+// s_waitcnt immediate (gfx9 encoding): vmcnt(n), lgkmcnt(0), expcnt unconstrained.
+constexpr int waitcnt_vm_lgkm0(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4); }
+
+template <int MB, int NB>
+__device__ __forceinline__ void mfma_chunk(f32x16 (&acc)[MB][NB], const float (&fa)[MB][8],
+                                           const float (&fb)[NB][8]) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+            for (int j = 0; j < NB; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j],
+                                                                 0, 0, 0);
+}
+
+template <int L, int BMN, int MB>
+__device__ __forceinline__ void dl_frags(const float* tile, int row0, int lane, float (&f)[MB][8]) {
+#pragma unroll
+    for (int i = 0; i < MB; ++i) dl_frag<L, BMN>(tile, row0 + i * 32, lane, f[i]);
+}
+
+template <int BM, int BN, int WM, int WN, int LA, int LB, int STAGES>
+__global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64)
+gemm_f32_dl(GemmParams p) {
+    constexpr int WAVES_N = BN / WN;
+    constexpr int NW = (BM / WM) * WAVES_N;
+    constexpr int NT = NW * 64;
+    constexpr int MB = WM / 32, NB = WN / 32;
+    static_assert(STAGES >= 2, "the ring needs at least two slots");
+    static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be 32-aligned");
+    using TA = DlTile<LA, BM, NW>;
+    using TB = DlTile<LB, BN, NW>;
+    constexpr int STAGE = TA::floats + TB::floats;
+    constexpr int LOADS = TA::per_wave + TB::per_wave;   // wave instructions per chunk
+    static_assert(LOADS * (STAGES - 2) < 64, "vmcnt holds at most 63");
+    __shared__ __attribute__((aligned(1024))) float smem[STAGES * STAGE];
+
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    const int ra = wm * WM, rb = wn * WN;     // this wave's first row in the A / B tile
+
+    const TileId id = tile_id(p);
+    const int m0 = id.tm * BM, n0 = id.tn * BN;
+    const int k_begin = id.split * p.k_per_split;
+    const int k_end = min(p.K, k_begin + p.k_per_split);
+    const int klen = k_end > k_begin ? k_end - k_begin : 0;
+    const int nk = klen >> 4;                 // full chunks
+    const bool tail = (klen & 15) != 0;
+    const float* Ab = p.A + (int64_t)id.bz * p.a_b;
+    const float* Bb = p.B + (int64_t)id.bz * p.b_b;
+
+    f32x16 acc[MB][NB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    DlTail<LA, BM, NT> ta;
+    DlTail<LB, BN, NT> tb;
+    if (tail) {
+        const int kt0 = k_begin + nk * 16;
+        ta.load(Ab, p.a_mn, p.a_k, p.M, m0, kt0, k_end, t);
+        tb.load(Bb, p.b_mn, p.b_k, p.N, n0, kt0, k_end, t);
+    }
+
+    DlLoader<LA, BM, NW> la;
+    DlLoader<LB, BN, NW> lb;
+    la.init(Ab, p.a_mn, p.a_k, p.M, m0, k_begin, wave, lane);
+    lb.init(Bb, p.b_mn, p.b_k, p.N, n0, k_begin, wave, lane);
+
+#pragma unroll
+    for (int c = 0; c < STAGES - 1; ++c)
+        if (c < nk) {
+            la.issue(smem + c * STAGE, c, wave);
+            lb.issue(smem + c * STAGE + TA::floats, c, wave);
+        }
+
+    if (tail) {
+        // Slot STAGES-1 is free until the first loop iteration's barrier.
+        float* const st = smem + (STAGES - 1) * STAGE;
+        ta.store(st, t);
+        tb.store(st + TA::floats, t);
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));
+        __builtin_amdgcn_s_barrier();
+        float fa[MB][8], fb[NB][8];
+        dl_frags<LA, BM, MB>(st, ra, lane, fa);
+        dl_frags<LB, BN, NB>(st + TA::floats, rb, lane, fb);
+        mfma_chunk<MB, NB>(acc, fa, fb);
+    }
+
+    for (int kt = 0; kt < nk; ++kt) {
+        // Chunk kt must have landed (own instructions, then everyone's).
+        // The barrier also retires every wave's reads of the slot refilled
+        // below.
+        if (kt + STAGES - 1 <= nk) __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(LOADS * (STAGES - 2)));
+        else __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+        __builtin_amdgcn_s_barrier();
+        const int cn = kt + STAGES - 1;
+        if (cn < nk) {
+            float* st = smem + (cn % STAGES) * STAGE;
+            la.issue(st, cn, wave);
+            lb.issue(st + TA::floats, cn, wave);
+        }
+        const float* At = smem + (kt % STAGES) * STAGE;
+        float fa[MB][8], fb[NB][8];
+        dl_frags<LA, BM, MB>(At, ra, lane, fa);
+        dl_frags<LB, BN, NB>(At + TA::floats, rb, lane, fb);
+        mfma_chunk<MB, NB>(acc, fa, fb);
+    }
+
+    store_tile<MB, NB>(p, acc, m0 + ra, n0 + rb, lane, id.split, id.bz);
+}
+
+}  // namespace mtk

@@ -182,8 +182,86 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblk) {
     return bid;
 }
 
-template <int BM, int BN, int BK, int WM, int WN, int LA, int LB>
-__global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64)
+// Workgroup -> (tile row, tile column, K split, batch) of a 1-D grid laid out
+// as [batch][split][tile].  Tiles are visited in groups of group_m tile rows so
+// that concurrently running workgroups share A and B panels in L2.
+struct TileId { int tm, tn, split, bz; };
+
+__device__ __forceinline__ TileId tile_id(const GemmParams& p) {
+    const int bid = xcd_remap(blockIdx.x, gridDim.x);
+    const int ntiles = p.tiles_m * p.tiles_n;
+    const int tile = bid % ntiles;
+    const int rest = bid / ntiles;
+    TileId id;
+    id.split = rest % p.splits;
+    id.bz = rest / p.splits;
+    const int per_group = p.group_m * p.tiles_n;
+    const int g = tile / per_group;
+    const int first = g * p.group_m;
+    const int gsz = min(p.tiles_m - first, p.group_m);
+    const int in_g = tile - g * per_group;
+    id.tm = first + in_g % gsz;
+    id.tn = in_g / gsz;
+    return id;
+}
+
+// Epilogue of one wave: (MB x NB) 32x32 accumulators whose first element is
+// C(mw0, nw0).  With split-K the raw partial goes to the workspace; otherwise
+// bias and beta*C are applied and the column index is scattered through
+// col(n) (see GemmParams).
+template <int MB, int NB>
+__device__ __forceinline__ void store_tile(const GemmParams& p, const f32x16 (&acc)[MB][NB],
+                                           int mw0, int nw0, int lane, int split, int bz) {
+    const int h = lane >> 5, c = lane & 31;
+    if (p.splits > 1) {
+        float* W = p.ws + ((int64_t)split * p.batch + bz) * (int64_t)p.M * p.N;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int n = nw0 + j * 32 + c;
+            if (n >= p.N) continue;
+#pragma unroll
+            for (int i = 0; i < MB; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = mw0 + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                    if (m < p.M) W[(int64_t)m * p.N + n] = acc[i][j][r];
+                }
+        }
+        return;
+    }
+
+    float* Cb = p.C + (int64_t)bz * p.c_b;
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        const int n = nw0 + j * 32 + c;
+        if (n >= p.N) continue;
+        int64_t coff;
+        if (p.c_n_inner >= p.N) {
+            coff = (int64_t)n * p.c_n;
+        } else {
+            const int64_t no = n / p.c_n_inner, ni = n - no * p.c_n_inner;
+            coff = no * p.c_n_outer + ni * p.c_n;
+        }
+        const float bcol = (p.bias_axis == 2) ? p.bias[(int64_t)n * p.bias_stride] : 0.f;
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = mw0 + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (m >= p.M) continue;
+                float v = acc[i][j][r] + bcol;
+                if (p.bias_axis == 1) v += p.bias[(int64_t)m * p.bias_stride];
+                float* dst = Cb + (int64_t)m * p.c_m + coff;
+                if (p.beta != 0.f) v += p.beta * *dst;
+                *dst = v;
+            }
+    }
+}
+
+// MINW: minimum resident waves per SIMD the register allocation must allow
+// (2 lets two 4-wave workgroups share a CU and hide each other's barriers).
+template <int BM, int BN, int BK, int WM, int WN, int LA, int LB, int MINW = 1>
+__global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64, MINW)
 gemm_f32_mfma(GemmParams p) {
     constexpr int WAVES_N = BN / WN;
     constexpr int NT = (BM / WM) * WAVES_N * 64;
@@ -200,23 +278,8 @@ gemm_f32_mfma(GemmParams p) {
     const int wave = t >> 6;
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
-    // ---- workgroup -> (tile, split, batch) ------------------------------
-    const int bid = xcd_remap(blockIdx.x, gridDim.x);
-    const int ntiles = p.tiles_m * p.tiles_n;
-    const int tile = bid % ntiles;
-    const int rest = bid / ntiles;
-    const int split = rest % p.splits;
-    const int bz = rest / p.splits;
-    int tm, tn;
-    {
-        const int per_group = p.group_m * p.tiles_n;
-        const int g = tile / per_group;
-        const int first = g * p.group_m;
-        const int gsz = min(p.tiles_m - first, p.group_m);
-        const int in_g = tile - g * per_group;
-        tm = first + in_g % gsz;
-        tn = in_g / gsz;
-    }
+    const TileId id = tile_id(p);
+    const int tm = id.tm, tn = id.tn, split = id.split, bz = id.bz;
     const int m0 = tm * BM, n0 = tn * BN;
     const int k_begin = split * p.k_per_split;
     const int k_end = min(p.K, k_begin + p.k_per_split);
@@ -281,51 +344,7 @@ gemm_f32_mfma(GemmParams p) {
         }
     }
 
-    // ---- epilogue ---------------------------------------------------------
-    const int h = lane >> 5, c = lane & 31;
-    if (p.splits > 1) {
-        float* W = p.ws + ((int64_t)split * p.batch + bz) * (int64_t)p.M * p.N;
-#pragma unroll
-        for (int j = 0; j < NB; ++j) {
-            const int n = n0 + wn * WN + j * 32 + c;
-            if (n >= p.N) continue;
-#pragma unroll
-            for (int i = 0; i < MB; ++i)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int m = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                    if (m < p.M) W[(int64_t)m * p.N + n] = acc[i][j][r];
-                }
-        }
-        return;
-    }
-
-    float* Cb = p.C + (int64_t)bz * p.c_b;
-#pragma unroll
-    for (int j = 0; j < NB; ++j) {
-        const int n = n0 + wn * WN + j * 32 + c;
-        if (n >= p.N) continue;
-        int64_t coff;
-        if (p.c_n_inner >= p.N) {
-            coff = (int64_t)n * p.c_n;
-        } else {
-            const int64_t no = n / p.c_n_inner, ni = n - no * p.c_n_inner;
-            coff = no * p.c_n_outer + ni * p.c_n;
-        }
-        const float bcol = (p.bias_axis == 2) ? p.bias[(int64_t)n * p.bias_stride] : 0.f;
-#pragma unroll
-        for (int i = 0; i < MB; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (m >= p.M) continue;
-                float v = acc[i][j][r] + bcol;
-                if (p.bias_axis == 1) v += p.bias[(int64_t)m * p.bias_stride];
-                float* dst = Cb + (int64_t)m * p.c_m + coff;
-                if (p.beta != 0.f) v += p.beta * *dst;
-                *dst = v;
-            }
-    }
+    store_tile<MB, NB>(p, acc, m0 + wm * WM, n0 + wn * WN, lane, split, bz);
 }
 
 }  // namespace mtk

@@ -84,6 +84,7 @@ const char* layout_name(int l) {
 }
 
 struct Plan {
+    bool dl = false;   // direct-to-LDS kernel (both operands in a vector layout)
     int cfg = 0;
     int splits = 1;
     int kps = 0;
@@ -101,18 +102,23 @@ static_assert(TileCfg<0>::BK == kBK && TileCfg<1>::BK == kBK && TileCfg<2>::BK =
 // factor.  Work per workgroup is priced at the CU's fp32 MFMA rate (256
 // flop/clk) with a per-configuration efficiency; each round of resident
 // workgroups pays a fixed latency; split-K pays for its partial traffic.
+// Row 0: register-staged kernel (any layout); row 1: direct-to-LDS kernel
+// (both operands in a vector layout).
 struct CostModel {
-    double eff[kNumCfg] = {0.85, 0.75, 0.55};
-    int occ[kNumCfg] = {1, 2, 4};            // resident workgroups per CU
+    double eff[2][kNumCfg] = {{0.85, 0.75, 0.55}, {0.88, 0.80, 0.60}};
+    int occ[2][kNumCfg] = {{1, 2, 4}, {1, 2, 4}};   // resident workgroups per CU
     double round_latency = 3000.0;           // cycles of fill/drain per round
     double bytes_per_cycle = 2500.0;         // device HBM bytes per CU-clock
     double launch_cycles = 6000.0;           // second (reduce) launch
 };
 
-Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool allow_split) {
+Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool allow_split,
+               bool dl) {
     static const CostModel cm;
     static const int kSplits[] = {1, 2, 3, 4, 6, 8, 12, 16};
+    const int fam = dl ? 1 : 0;
     Plan best;
+    best.dl = dl;
     double best_t = 1e300;
     for (int cfg = 0; cfg < kNumCfg; ++cfg) {
         const int64_t tm = (M + kBM[cfg] - 1) / kBM[cfg];
@@ -127,9 +133,9 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool all
             const int64_t wgs = tiles * splits;
             if (wgs * 512 >= ((int64_t)1 << 32)) continue;
             const double per_cu = std::ceil((double)wgs / cus);
-            const double rounds = std::ceil((double)wgs / ((double)cus * cm.occ[cfg]));
-            const double work = (double)kBM[cfg] * kBN[cfg] * (double)std::max<int64_t>(kps, kBK) * 2.0 /
-                                (256.0 * cm.eff[cfg]);
+            const double rounds = std::ceil((double)wgs / ((double)cus * cm.occ[fam][cfg]));
+            const double work = (double)kBM[cfg] * kBN[cfg] * (double)std::max<int64_t>(kps, kBK) *
+                                2.0 / (256.0 * cm.eff[fam][cfg]);
             double t = per_cu * work + rounds * cm.round_latency;
             if (splits > 1) {
                 const double bytes = (double)(2 * splits + 1) * M * N * batch * 4.0;
@@ -149,8 +155,22 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool all
     return best;
 }
 
-GemmLaunchFn pick_launcher(int cfg, int la, int lb) {
-    switch (cfg) {
+// Workspace that covers the plan of either kernel family (for sizes queried
+// before the operand pointers, and hence the layouts, are known).
+size_t plan_ws(int64_t M, int64_t N, int64_t K, int64_t batch, int cus) {
+    return std::max(make_plan(M, N, K, batch, cus, true, false).ws_bytes,
+                    make_plan(M, N, K, batch, cus, true, true).ws_bytes);
+}
+
+GemmLaunchFn pick_launcher(const Plan& plan, int la, int lb) {
+    if (plan.dl) {
+        switch (plan.cfg) {
+            case 0: return dl_launcher_cfg0(la, lb);
+            case 1: return dl_launcher_cfg1(la, lb);
+            default: return dl_launcher_cfg2(la, lb);
+        }
+    }
+    switch (plan.cfg) {
         case 0: return launcher_cfg0(la, lb);
         case 1: return launcher_cfg1(la, lb);
         default: return launcher_cfg2(la, lb);
@@ -238,9 +258,10 @@ int run_gemm(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C, int6
     const int la = K == 0 ? L_KS : classify(p.A, p.a_mn, p.a_k, M, K, p.a_b, p.a_b != 0);
     const int lb = K == 0 ? L_KS : classify(p.B, p.b_mn, p.b_k, N, K, p.b_b, p.b_b != 0);
 
-    Plan plan = make_plan(M, N, K, batch, device_cu_count(), true);
+    const bool dl = (la == L_KV || la == L_MV) && (lb == L_KV || lb == L_MV);
+    Plan plan = make_plan(M, N, K, batch, device_cu_count(), true, dl);
     if (plan.splits > 1 && (workspace == nullptr || ws_bytes < plan.ws_bytes))
-        plan = make_plan(M, N, K, batch, device_cu_count(), false);
+        plan = make_plan(M, N, K, batch, device_cu_count(), false, dl);
     p.splits = plan.splits;
     p.k_per_split = plan.splits > 1 ? plan.kps : (int)std::max<int64_t>(K, 1);
     p.tiles_m = plan.tiles_m;
@@ -250,11 +271,11 @@ int run_gemm(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C, int6
 
     const int64_t nblocks = (int64_t)plan.tiles_m * plan.tiles_n * plan.splits * batch;
     if (nblocks >= ((int64_t)1 << 31)) return MT_ERR_UNSUPPORTED;
-    std::snprintf(g_last_config, sizeof g_last_config, "%dx%d a=%s b=%s split=%d wgs=%lld",
-                  kBM[plan.cfg], kBN[plan.cfg], layout_name(la), layout_name(lb), plan.splits,
+    std::snprintf(g_last_config, sizeof g_last_config, "%s %dx%d a=%s b=%s split=%d wgs=%lld",
+                  plan.dl ? "dl" : "rs", kBM[plan.cfg], kBN[plan.cfg], layout_name(la), layout_name(lb), plan.splits,
                   (long long)nblocks);
 
-    hipError_t e = pick_launcher(plan.cfg, la, lb)(p, (unsigned)nblocks, stream);
+    hipError_t e = pick_launcher(plan, la, lb)(p, (unsigned)nblocks, stream);
     if (e == hipErrorStreamCaptureUnsupported) e = hipSuccess;
     if (e != hipSuccess) return MT_ERR_HIP;
     if (plan.splits > 1) {
@@ -269,7 +290,7 @@ int run_gemm(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C, int6
 size_t gemm_ws(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C) {
     int64_t M, N, K, batch;
     if (check_gemm(A, B, C, &M, &N, &K, &batch) != MT_OK || M == 0 || N == 0) return 0;
-    return make_plan(M, N, K, batch, device_cu_count(), true).ws_bytes;
+    return plan_ws(M, N, K, batch, device_cu_count());
 }
 
 // ---- column sums (Linear bias gradient) ------------------------------------
@@ -498,9 +519,9 @@ size_t mt_linear_workspace_f32(int64_t rows, int64_t in_f, int64_t out_f) {
     if (rows < 0 || in_f < 0 || out_f < 0) return 0;
     const int cus = device_cu_count();
     size_t ws = 0;
-    if (rows > 0 && out_f > 0) ws = std::max(ws, make_plan(rows, out_f, in_f, 1, cus, true).ws_bytes);
-    if (rows > 0 && in_f > 0) ws = std::max(ws, make_plan(rows, in_f, out_f, 1, cus, true).ws_bytes);
-    if (out_f > 0 && in_f > 0) ws = std::max(ws, make_plan(out_f, in_f, rows, 1, cus, true).ws_bytes);
+    if (rows > 0 && out_f > 0) ws = std::max(ws, plan_ws(rows, out_f, in_f, 1, cus));
+    if (rows > 0 && in_f > 0) ws = std::max(ws, plan_ws(rows, in_f, out_f, 1, cus));
+    if (out_f > 0 && in_f > 0) ws = std::max(ws, plan_ws(out_f, in_f, rows, 1, cus));
     return ws;
 }
 
@@ -534,7 +555,7 @@ size_t mt_conv2d_workspace_f32(const mt_conv2d_desc* d) {
     const int64_t kg = d->c_in * d->kh * d->kw, np = d->n * Ho * Wo;
     if (np == 0 || d->c_out == 0) return 0;
     const size_t col = align_up((size_t)kg * np * sizeof(float), 256);
-    return col + make_plan(d->c_out, np, kg, 1, device_cu_count(), true).ws_bytes;
+    return col + plan_ws(d->c_out, np, kg, 1, device_cu_count());
 }
 
 int mt_conv2d_fwd_f32(const mt_conv2d_desc* d, const float* input, const float* weight,
@@ -566,8 +587,8 @@ size_t mt_conv2d_bwd_workspace_f32(const mt_conv2d_desc* d) {
     const int cus = device_cu_count();
     const size_t bufs = align_up((size_t)kg * np * sizeof(float), 256) +
                         align_up((size_t)d->c_out * np * sizeof(float), 256);
-    const size_t g = std::max(make_plan(d->c_out, kg, np, 1, cus, true).ws_bytes,
-                              make_plan(kg, np, d->c_out, 1, cus, true).ws_bytes);
+    const size_t g = std::max(plan_ws(d->c_out, kg, np, 1, cus),
+                              plan_ws(kg, np, d->c_out, 1, cus));
     return bufs + g;
 }
 

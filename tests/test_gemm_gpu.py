@@ -232,3 +232,65 @@ def test_config3_transpose_and_slice_views(dev):
     # the view result equals the result on materialised copies
     c_mat = run(As.contiguous(), B.t().contiguous())
     assert_close(c, c_mat, 1024, amax(a), amax(b), "C3b view == copy")
+
+
+# ---- direct-to-LDS kernel (both operands in a 16-byte vector layout) ---------
+# Tails in M and N (clamped rows), K not a multiple of 16 (bounds-checked last
+# chunk), split-K over such a K, one-row/one-column operands, batch and the
+# bias/beta epilogue, for all four (k- / mn-contiguous) layout pairs.
+
+def _views(a, b, ta, tb, dev):
+    A = to_gpu(a.T.copy(), dev).t() if ta else to_gpu(a, dev)
+    B = to_gpu(b.T.copy(), dev).t() if tb else to_gpu(b, dev)
+    return A, B
+
+
+@pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("M,N,K", [(260, 132, 1000), (64, 64, 20), (516, 4, 36), (8, 1028, 4)])
+def test_dl_layouts_and_tails(dev, ta, tb, M, N, K):
+    a = oracle.uniform((M, K), 100 + M)
+    b = oracle.uniform((K, N), 200 + N)
+    A, B = _views(a, b, ta, tb, dev)
+    c = run(A, B)
+    assert mt.last_config().startswith("dl "), mt.last_config()
+    assert_close(c, oracle.matmul(a, b), K, amax(a), amax(b), f"dl {M}x{N}x{K} ta={ta} tb={tb}")
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 128, 4100), (96, 64, 6004), (1, 256, 64), (256, 1, 64),
+                                   (1000, 1000, 256)])
+def test_dl_split_k_and_edges(dev, M, N, K):
+    a = oracle.uniform((M, K), 300 + K)
+    b = oracle.uniform((K, N), 400 + K)
+    A, B = to_gpu(a, dev), to_gpu(b, dev)
+    c = run(A, B)
+    assert mt.last_config().startswith("dl "), mt.last_config()
+    assert_close(c, oracle.matmul(a, b), K, amax(a), amax(b), f"dl {M}x{N}x{K}")
+    np.testing.assert_array_equal(c, run(A, B))   # deterministic, also under split-K
+
+
+def test_dl_batched_transposed(dev):
+    a = oracle.uniform((5, 72, 100), 1)
+    b = oracle.uniform((5, 132, 100), 2)              # used as bᵀ: [5,100,132] view
+    A = to_gpu(a, dev)
+    B = to_gpu(b, dev).transpose(1, 2)
+    c = mt.gemm(A, B)
+    torch.cuda.synchronize()
+    assert mt.last_config().startswith("dl "), mt.last_config()
+    want = oracle.bmm(a, np.ascontiguousarray(b.transpose(0, 2, 1)))
+    assert_close(c.cpu().numpy(), want, 100, amax(a), amax(b), "dl batched Bᵀ")
+
+
+@pytest.mark.parametrize("axis", [mt.BIAS_ROW, mt.BIAS_COL])
+def test_dl_bias_and_beta(dev, axis):
+    a = oracle.uniform((200, 300), 5)
+    b = oracle.uniform((300, 172), 6)
+    bias = oracle.uniform((200 if axis == mt.BIAS_ROW else 172,), 7)
+    c0 = oracle.uniform((200, 172), 8)
+    C = to_gpu(c0, dev)
+    mt.gemm(to_gpu(a, dev), to_gpu(b, dev), out=C, beta=1.0, bias=to_gpu(bias, dev),
+            bias_axis=axis)
+    torch.cuda.synchronize()
+    assert mt.last_config().startswith("dl "), mt.last_config()
+    want = oracle.matmul(a, b) + c0 + (bias[:, None] if axis == mt.BIAS_ROW else bias[None, :])
+    assert_close(C.cpu().numpy(), want, 300, amax(a), amax(b), f"dl bias {axis} + beta",
+                 extra=1e-6)
