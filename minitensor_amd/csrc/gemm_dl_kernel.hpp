@@ -153,8 +153,7 @@ __device__ __forceinline__ void mfma_chunk(f32x16 (&acc)[MB][NB], const float (&
         for (int i = 0; i < MB; ++i)
 #pragma unroll
             for (int j = 0; j < NB; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j],
-                                                                 0, 0, 0);
+                acc[i][j] = mfma_32x32x2(fa[i][s], fb[j][s], acc[i][j]);
 }
 
 template <int L, int BMN, int MB>

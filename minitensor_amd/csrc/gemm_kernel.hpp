@@ -27,8 +27,11 @@
 //     k-values of one row are contiguous, one pair of ds_read_b128 for
 //     k-contiguous LDS tiles.
 //   * MFMA operand layout (v_mfma_f32_32x32x2_f32, CDNA3/CDNA4 ISA):
-//        A: lane l holds A[i = l%32][k = l/32];  B: lane l holds B[k = l/32][j = l%32]
+//        src0: lane l holds X[i = l%32][k = l/32];  src1: lane l holds Y[k = l/32][j = l%32]
 //        D: lane l, register r holds D[8*(r/4) + 4*(l/32) + r%4][l%32].
+//     The kernels pass B's fragment as src0 and A's as src1, i.e. they
+//     accumulate the transposed block, so each lane owns four consecutive
+//     columns of one output row per register quad (16-byte stores).
 //   * Work decomposition: one workgroup per (tile, split, batch) in a 1-D grid.
 //     Consecutive workgroup ids are dealt round-robin to the 8 XCDs, so ids
 //     are remapped to give each XCD a contiguous range of tiles, which are
@@ -65,6 +68,8 @@ struct GemmParams {
     float* ws;                                // split-K partials [splits][batch][M][N]
     int M, N, K, batch;
     int splits, k_per_split;                  // k_per_split is a multiple of BK
+    int c_vec;    // C takes 16-byte stores of 4 consecutive columns (c_n == 1, aligned)
+    int ws_vec;   // the split-K workspace takes 16-byte stores (N % 4 == 0, aligned)
     int tiles_m, tiles_n, group_m;
 };
 
@@ -205,10 +210,31 @@ __device__ __forceinline__ TileId tile_id(const GemmParams& p) {
     return id;
 }
 
+// One 32x32 accumulator of a wave: the MFMA is issued with B's fragment as
+// its first operand and A's as its second, so it computes the transposed
+// block and lane l, register r holds C(m, n) with
+//     m = m_blk + l%32,   n = n_blk + 8*(r/4) + 4*(l/32) + r%4.
+// Registers 4q..4q+3 of a lane are four consecutive columns of one row: the
+// epilogue stores them as one 16-byte vector when the output allows it.
+__device__ __forceinline__ f32x16 mfma_32x32x2(float a, float b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(b, a, c, 0, 0, 0);
+}
+
+// Column offset col(n) of the output (see GemmParams).
+__device__ __forceinline__ int64_t col_offset(const GemmParams& p, int n) {
+    if (p.c_n_inner >= p.N) return (int64_t)n * p.c_n;
+    const int64_t no = n / p.c_n_inner, ni = n - no * p.c_n_inner;
+    return no * p.c_n_outer + ni * p.c_n;
+}
+
 // Epilogue of one wave: (MB x NB) 32x32 accumulators whose first element is
 // C(mw0, nw0).  With split-K the raw partial goes to the workspace; otherwise
 // bias and beta*C are applied and the column index is scattered through
-// col(n) (see GemmParams).
+// col(n).  Each lane holds groups of four consecutive columns of one row.
+// When the host has established that every group is a whole, aligned,
+// contiguous 16-byte run (ws_vec / c_vec, which imply N % 4 == 0) a group is
+// one vector store; otherwise every element is stored on its own.  The two
+// variants are separate loops so the compiler never keeps both live.
 template <int MB, int NB>
 __device__ __forceinline__ void store_tile(const GemmParams& p, const f32x16 (&acc)[MB][NB],
                                            int mw0, int nw0, int lane, int split, int bz) {
@@ -216,44 +242,75 @@ __device__ __forceinline__ void store_tile(const GemmParams& p, const f32x16 (&a
     if (p.splits > 1) {
         float* W = p.ws + ((int64_t)split * p.batch + bz) * (int64_t)p.M * p.N;
 #pragma unroll
-        for (int j = 0; j < NB; ++j) {
-            const int n = nw0 + j * 32 + c;
-            if (n >= p.N) continue;
+        for (int i = 0; i < MB; ++i) {
+            const int m = mw0 + i * 32 + c;
+            if (m >= p.M) continue;
+            float* Wr = W + (int64_t)m * p.N;
 #pragma unroll
-            for (int i = 0; i < MB; ++i)
+            for (int j = 0; j < NB; ++j)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int m = mw0 + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                    if (m < p.M) W[(int64_t)m * p.N + n] = acc[i][j][r];
+                for (int q = 0; q < 4; ++q) {
+                    const int n = nw0 + j * 32 + 8 * q + 4 * h;
+                    if (p.ws_vec) {
+                        if (n < p.N) {
+                            const f32x4 v = {acc[i][j][4 * q], acc[i][j][4 * q + 1],
+                                             acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                            *reinterpret_cast<f32x4*>(Wr + n) = v;
+                        }
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (n + e < p.N) Wr[n + e] = acc[i][j][4 * q + e];
+                    }
                 }
         }
         return;
     }
 
     float* Cb = p.C + (int64_t)bz * p.c_b;
+    if (p.c_vec) {
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
-        const int n = nw0 + j * 32 + c;
-        if (n >= p.N) continue;
-        int64_t coff;
-        if (p.c_n_inner >= p.N) {
-            coff = (int64_t)n * p.c_n;
-        } else {
-            const int64_t no = n / p.c_n_inner, ni = n - no * p.c_n_inner;
-            coff = no * p.c_n_outer + ni * p.c_n;
+        for (int i = 0; i < MB; ++i) {
+            const int m = mw0 + i * 32 + c;
+            if (m >= p.M) continue;
+            float* Cr = Cb + (int64_t)m * p.c_m;
+            const float brow = (p.bias_axis == 1) ? p.bias[(int64_t)m * p.bias_stride] : 0.f;
+#pragma unroll
+            for (int j = 0; j < NB; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int n = nw0 + j * 32 + 8 * q + 4 * h;
+                    if (n >= p.N) continue;
+                    f32x4 o;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        o[e] = acc[i][j][4 * q + e] + brow;
+                        if (p.bias_axis == 2) o[e] += p.bias[(int64_t)(n + e) * p.bias_stride];
+                    }
+                    f32x4* dst = reinterpret_cast<f32x4*>(Cr + col_offset(p, n));
+                    if (p.beta != 0.f) o += p.beta * *dst;
+                    *dst = o;
+                }
         }
-        const float bcol = (p.bias_axis == 2) ? p.bias[(int64_t)n * p.bias_stride] : 0.f;
+        return;
+    }
 #pragma unroll
-        for (int i = 0; i < MB; ++i)
+    for (int i = 0; i < MB; ++i) {
+        const int m = mw0 + i * 32 + c;
+        if (m >= p.M) continue;
+        float* Cr = Cb + (int64_t)m * p.c_m;
+        const float brow = (p.bias_axis == 1) ? p.bias[(int64_t)m * p.bias_stride] : 0.f;
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int m = mw0 + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (m >= p.M) continue;
-                float v = acc[i][j][r] + bcol;
-                if (p.bias_axis == 1) v += p.bias[(int64_t)m * p.bias_stride];
-                float* dst = Cb + (int64_t)m * p.c_m + coff;
-                if (p.beta != 0.f) v += p.beta * *dst;
-                *dst = v;
+                const int n = nw0 + j * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                if (n >= p.N) continue;
+                float o = acc[i][j][r] + brow;
+                if (p.bias_axis == 2) o += p.bias[(int64_t)n * p.bias_stride];
+                float* dst = Cr + col_offset(p, n);
+                if (p.beta != 0.f) o += p.beta * *dst;
+                *dst = o;
             }
     }
 }
@@ -333,8 +390,7 @@ gemm_f32_mfma(GemmParams p) {
                     for (int i = 0; i < MB; ++i)
 #pragma unroll
                         for (int j = 0; j < NB; ++j)
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                                fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
+                            acc[i][j] = mfma_32x32x2(fa[i][s], fb[j][s], acc[i][j]);
             }
             if (more) {
                 la.store((kt & 1) ? As0 : As1);

@@ -268,6 +268,12 @@ int run_gemm(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C, int6
     p.tiles_n = plan.tiles_n;
     p.group_m = 4;
     p.ws = plan.splits > 1 ? static_cast<float*>(workspace) : nullptr;
+    // 16-byte epilogue stores: four consecutive columns must be contiguous,
+    // aligned, and (for a scattered output) never straddle a column group.
+    p.c_vec = p.c_n == 1 && (N & 3) == 0 && ((uintptr_t)p.C & 15u) == 0 && (p.c_m & 3) == 0 &&
+              (batch == 1 || (p.c_b & 3) == 0) &&
+              (p.c_n_inner >= N || ((p.c_n_inner & 3) == 0 && (p.c_n_outer & 3) == 0));
+    p.ws_vec = p.ws != nullptr && ((uintptr_t)p.ws & 15u) == 0 && (N & 3) == 0;
 
     const int64_t nblocks = (int64_t)plan.tiles_m * plan.tiles_n * plan.splits * batch;
     if (nblocks >= ((int64_t)1 << 31)) return MT_ERR_UNSUPPORTED;

@@ -294,3 +294,51 @@ def test_dl_bias_and_beta(dev, axis):
     want = oracle.matmul(a, b) + c0 + (bias[:, None] if axis == mt.BIAS_ROW else bias[None, :])
     assert_close(C.cpu().numpy(), want, 300, amax(a), amax(b), f"dl bias {axis} + beta",
                  extra=1e-6)
+
+
+# ---- epilogue paths -----------------------------------------------------------
+# Four consecutive output columns go out as one 16-byte store when C is
+# unit-stride, aligned and N % 4 == 0; every other output (strided, transposed,
+# misaligned, N % 4 != 0) takes the per-element path.  Same for split-K partials.
+
+@pytest.mark.parametrize("kind", ["transposed", "col_stride2", "offset1", "row_slice"])
+def test_output_views(dev, kind):
+    M, N, K = 96, 132, 80
+    a = oracle.uniform((M, K), 61)
+    b = oracle.uniform((K, N), 62)
+    if kind == "transposed":
+        buf = torch.full((N, M), 7.0, device=dev)
+        out = buf.t()                                  # strides (1, M)
+    elif kind == "col_stride2":
+        buf = torch.full((M, 2 * N), 7.0, device=dev)
+        out = buf[:, ::2]                              # strides (2N, 2)
+    elif kind == "offset1":
+        buf = torch.full((M * N + 1,), 7.0, device=dev)
+        out = buf[1:].view(M, N)                       # 4-byte aligned only
+    else:
+        buf = torch.full((M + 8, N), 7.0, device=dev)
+        out = buf[8:]                                  # aligned row slice
+    mt.gemm(to_gpu(a, dev), to_gpu(b, dev), out=out)
+    torch.cuda.synchronize()
+    print(f"[config] {mt.last_config()}", flush=True)
+    assert_close(out.cpu().numpy(), oracle.matmul(a, b), K, amax(a), amax(b), f"out {kind}")
+    # nothing outside the view was touched
+    mask = torch.ones_like(buf, dtype=torch.bool)
+    if kind == "transposed":
+        mask[:] = False
+    elif kind == "col_stride2":
+        mask[:, ::2] = False
+    elif kind == "offset1":
+        mask[1:] = False
+    else:
+        mask[8:] = False
+    assert torch.all(buf[mask] == 7.0)
+
+
+@pytest.mark.parametrize("N", [66, 68])
+def test_split_k_partials_ragged_n(dev, N):
+    a = oracle.uniform((64, 8192), 71)
+    b = oracle.uniform((8192, N), 72)
+    c = run(to_gpu(a, dev), to_gpu(b, dev))
+    assert "split=1 " not in mt.last_config() + " "
+    assert_close(c, oracle.matmul(a, b), 8192, amax(a), amax(b), f"split-K N={N}")
