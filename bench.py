@@ -9,7 +9,10 @@ exactly K steps bracketed by device synchronisation.  The GEMM is a single
 kernel launch per step, so the roofline figure uses the same events.
 
 Secondary lines (the other BASELINE configs: ms and TFLOPS, and HBM GB/s for
-the batched one) are timed the same way and reported under "secondary".
+the batched one) are reported under "secondary".  Their kernels take 10-100
+us, less than a Python/ctypes call, so `ms` is device time: 20 calls are
+captured into a HIP graph and the graph is replayed between HIP events.
+`ms_eager_python` is the same calls from a Python loop, for comparison.
 The CPU baseline times the reference's own matmul_cpu (oracle/_ref, built
 from the reference headers; the C restatement in oracle/ when that build is
 absent) on a 64-row sample of the same GEMM, single-threaded.
@@ -61,6 +64,36 @@ def time_events(fn, iters: int, warmup: int) -> float:
     return start.elapsed_time(stop) / iters
 
 
+def time_graph(fn, calls: int = 20, replays: int = 10) -> float:
+    """Mean device ms per call of fn: `calls` calls captured into one HIP graph,
+    replayed `replays` times between HIP events.  Removes the Python/ctypes
+    launch overhead, which exceeds the kernel time of the small configs."""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(calls):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / (replays * calls)
+    del graph
+    return ms
+
+
 def secondary(dev) -> dict:
     """BASELINE configs 1, 3, 4, 5 (ms, TFLOPS; GB/s for the HBM-near batched one)."""
     import torch
@@ -77,8 +110,15 @@ def secondary(dev) -> dict:
 
     out = {}
 
-    def rec(name, ms, flops, bytes_=None, cfg=None):
-        d = {"ms": round(ms, 5), "tflops": round(flops / ms / 1e9, 2),
+    def both(fn, iters, warmup):
+        """(device ms from graph replay, eager ms of the Python call loop)."""
+        eager = time_events(fn, iters, warmup)
+        return time_graph(fn), eager
+
+    def rec(name, times, flops, bytes_=None, cfg=None):
+        ms, eager = times
+        d = {"ms": round(ms, 5), "ms_eager_python": round(eager, 5),
+             "tflops": round(flops / ms / 1e9, 2),
              "frac_of_fp32_mfma_peak": round(flops / ms / 1e9 / PEAK_TFLOPS, 4)}
         if bytes_ is not None:
             d["hbm_gbs"] = round(bytes_ / ms / 1e6, 1)
@@ -91,18 +131,19 @@ def secondary(dev) -> dict:
     A, B = u(256, 512), u(512, 512)
     C = torch.empty(256, 512, device=dev)
     ws = mt.workspace(mt.lib().mt_gemm_workspace_f32(mt.mat(A), mt.mat(B), mt.mat(C)), dev)
-    ms = time_events(lambda: mt.gemm(A, B, out=C, ws=ws), 200, 20)
+    ms = both(lambda: mt.gemm(A, B, out=C, ws=ws), 200, 20)
     rec("c1_256x512x512", ms, 2 * 256 * 512 * 512, 4 * (256 * 512 + 512 * 512 + 256 * 512),
         mt.last_config())
 
     # C3: C = A·Bᵀ with B [2048,1024] as a transpose view; and the slice A[128:]
     A, B = n(2048, 1024), n(2048, 1024)
     C = torch.empty(2048, 2048, device=dev)
-    ms = time_events(lambda: mt.gemm(A, B.t(), out=C), 100, 10)
+    ws3 = mt.workspace(mt.lib().mt_gemm_workspace_f32(mt.mat(A), mt.mat(B.t()), mt.mat(C)), dev)
+    ms = both(lambda: mt.gemm(A, B.t(), out=C, ws=ws3), 100, 10)
     rec("c3a_2048x2048x1024_bT_view", ms, 2 * 2048 * 2048 * 1024, None, mt.last_config())
     As = A[128:]
     C2 = torch.empty(1920, 2048, device=dev)
-    ms = time_events(lambda: mt.gemm(As, B.t(), out=C2), 100, 10)
+    ms = both(lambda: mt.gemm(As, B.t(), out=C2, ws=ws3), 100, 10)
     rec("c3b_1920x2048x1024_slice_bT_view", ms, 2 * 1920 * 2048 * 1024, None, mt.last_config())
 
     # C4: Linear fwd + bwd, ResNet50-fc shape
@@ -116,15 +157,15 @@ def secondary(dev) -> dict:
     db = torch.empty(1000, device=dev)
     lws = mt.workspace(mt.lib().mt_linear_workspace_f32(256, 2048, 1000), dev)
     f = 2 * 256 * 1000 * 2048
-    ms_f = time_events(lambda: mt.linear(X, W, b, out=Y, ws=lws), 200, 20)
+    ms_f = both(lambda: mt.linear(X, W, b, out=Y, ws=lws), 200, 20)
     rec("c4_linear_fwd", ms_f, f, None, mt.last_config())
-    ms_dx = time_events(lambda: mt.linear_backward(dY, X, W, True, False, False, dx=dX, ws=lws),
+    ms_dx = both(lambda: mt.linear_backward(dY, X, W, True, False, False, dx=dX, ws=lws),
                         200, 20)
     rec("c4_linear_dx", ms_dx, f, None, mt.last_config())
-    ms_dw = time_events(lambda: mt.linear_backward(dY, X, W, False, True, True, dw=dW, db=db,
+    ms_dw = both(lambda: mt.linear_backward(dY, X, W, False, True, True, dw=dW, db=db,
                                                    ws=lws), 200, 20)
     rec("c4_linear_dw_db", ms_dw, f, None, mt.last_config())
-    ms_all = time_events(lambda: (mt.linear(X, W, b, out=Y, ws=lws),
+    ms_all = both(lambda: (mt.linear(X, W, b, out=Y, ws=lws),
                                   mt.linear_backward(dY, X, W, dx=dX, dw=dW, db=db, ws=lws)),
                          200, 20)
     rec("c4_linear_fwd_bwd_total", ms_all, 3 * f)
@@ -136,14 +177,15 @@ def secondary(dev) -> dict:
     d = mt.Conv2dDesc(32, 256, 14, 14, 256, 3, 3, 1, 1)
     import ctypes
     cws = mt.workspace(mt.lib().mt_conv2d_workspace_f32(ctypes.byref(d)), dev)
-    ms = time_events(lambda: mt.conv2d(x, w, cb, 1, 1, ws=cws), 100, 10)
+    ms = both(lambda: mt.conv2d(x, w, cb, 1, 1, ws=cws), 100, 10)
     rec("c5a_conv3x3_n32_c256_14x14", ms, 2 * 6272 * 256 * 2304,
         4 * (x.numel() + w.numel() + cb.numel() + 32 * 256 * 196), mt.last_config())
 
     # C5b: batched 64 x [512,64]·[64,512]
     A, B = u(64, 512, 64), u(64, 64, 512)
     C = torch.empty(64, 512, 512, device=dev)
-    ms = time_events(lambda: mt.gemm(A, B, out=C), 200, 20)
+    ws5 = mt.workspace(mt.lib().mt_gemm_workspace_f32(mt.mat(A), mt.mat(B), mt.mat(C)), dev)
+    ms = both(lambda: mt.gemm(A, B, out=C, ws=ws5), 200, 20)
     rec("c5b_bmm_64x512x512x64", ms, 2 * 64 * 512 * 512 * 64,
         4 * 64 * (512 * 64 + 64 * 512 + 512 * 512), mt.last_config())
     return out

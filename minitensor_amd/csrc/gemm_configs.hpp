@@ -39,10 +39,11 @@ GemmLaunchFn launcher_cfg2(int la, int lb);
 template <int CFG> struct DlCfg;
 // 8 waves of 128x64; 2 x 32 KB ring.
 template <> struct DlCfg<0> { static constexpr int BM = 256, BN = 256, WM = 128, WN = 64, STAGES = 2; };
-// 8 waves of 64x32; 4 x 16 KB ring, two workgroups per CU.
-template <> struct DlCfg<1> { static constexpr int BM = 128, BN = 128, WM = 64, WN = 32, STAGES = 4; };
-// 4 waves of 32x32; 4 x 8 KB ring.
-template <> struct DlCfg<2> { static constexpr int BM = 64, BN = 64, WM = 32, WN = 32, STAGES = 4; };
+// 8 waves of 64x32; 2 x 16 KB ring, up to four workgroups per CU.
+template <> struct DlCfg<1> { static constexpr int BM = 128, BN = 128, WM = 64, WN = 32, STAGES = 2; };
+// 4 waves of 32x32; 2 x 8 KB ring, up to eight workgroups per CU.  (Deeper
+// rings measured slower for these tiles: occupancy hides more latency.)
+template <> struct DlCfg<2> { static constexpr int BM = 64, BN = 64, WM = 32, WN = 32, STAGES = 2; };
 
 template <int CFG>
 constexpr int dl_threads() {

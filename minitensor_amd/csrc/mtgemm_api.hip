@@ -100,16 +100,19 @@ static_assert(TileCfg<0>::BK == kBK && TileCfg<1>::BK == kBK && TileCfg<2>::BK =
 
 // Cost model (in CU cycles) used to pick the tile configuration and split-K
 // factor.  Work per workgroup is priced at the CU's fp32 MFMA rate (256
-// flop/clk) with a per-configuration efficiency; each round of resident
-// workgroups pays a fixed latency; split-K pays for its partial traffic.
-// Row 0: register-staged kernel (any layout); row 1: direct-to-LDS kernel
-// (both operands in a vector layout).
+// flop/clk) with a per-configuration efficiency, plus the epilogue's store of
+// its tile; each round of resident workgroups pays a fixed latency; split-K
+// pays for its partial traffic and the reduction launch.  Row 0: register-
+// staged kernel (any layout); row 1: direct-to-LDS kernel (both operands in a
+// vector layout).  The constants are a least-squares fit to measured times of
+// every configuration and split factor on the benchmark shapes (MI355X).
 struct CostModel {
-    double eff[2][kNumCfg] = {{0.85, 0.75, 0.55}, {0.88, 0.80, 0.60}};
-    int occ[2][kNumCfg] = {{1, 2, 4}, {1, 2, 4}};   // resident workgroups per CU
-    double round_latency = 3000.0;           // cycles of fill/drain per round
-    double bytes_per_cycle = 2500.0;         // device HBM bytes per CU-clock
-    double launch_cycles = 6000.0;           // second (reduce) launch
+    double eff[2][kNumCfg] = {{0.84, 0.73, 0.63}, {0.88, 0.84, 0.71}};
+    int occ[2][kNumCfg] = {{1, 2, 4}, {1, 4, 8}};   // resident workgroups per CU
+    double round_latency = 9000.0;           // cycles of fill/drain per round
+    double epilogue_bytes_per_cycle = 10.7;  // one workgroup's tile store
+    double bytes_per_cycle = 4260.0;         // device HBM bytes per CU-clock
+    double launch_cycles = 8600.0;           // second (reduce) launch
 };
 
 Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool allow_split,
@@ -136,7 +139,8 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool all
             const double rounds = std::ceil((double)wgs / ((double)cus * cm.occ[fam][cfg]));
             const double work = (double)kBM[cfg] * kBN[cfg] * (double)std::max<int64_t>(kps, kBK) *
                                 2.0 / (256.0 * cm.eff[fam][cfg]);
-            double t = per_cu * work + rounds * cm.round_latency;
+            const double epi = (double)kBM[cfg] * kBN[cfg] * 4.0 / cm.epilogue_bytes_per_cycle;
+            double t = per_cu * (work + epi) + rounds * cm.round_latency;
             if (splits > 1) {
                 const double bytes = (double)(2 * splits + 1) * M * N * batch * 4.0;
                 t += bytes / (cm.bytes_per_cycle) + cm.launch_cycles;
