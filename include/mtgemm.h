@@ -109,10 +109,16 @@ int mt_linear_backward_f32(const mt_mat_f32* dY, const mt_mat_f32* X, const mt_m
  * NCHW input [n,c_in,h,w], OIHW weight [c_out,c_in,kh,kw], bias [c_out] or NULL,
  * output [n,c_out,h_out,w_out] with h_out = (h + 2*pad - kh)/stride + 1
  * (0 when h + 2*pad < kh), as the reference's safe_out_size
- * (include/TensorOps.hpp:17-20).  Tensors are dense NCHW (element offsets
- * applied by the caller).  The GEMM is C[c_out, n*h_out*w_out] =
+ * (include/TensorOps.hpp:17-20).  Weight and output are dense (element
+ * offsets applied by the caller).  The GEMM is C[c_out, n*h_out*w_out] =
  * W[c_out, c_in*kh*kw] · col[c_in*kh*kw, n*h_out*w_out] with the row bias fused
- * and the output scattered straight into NCHW.  Replaces conv2d_gpu +
+ * and the output scattered straight into NCHW.  When c_in*kh*kw % 4 == 0 and
+ * the weight is 16-byte aligned, col is never formed: the kernel gathers it
+ * from the input (implicit GEMM) and the workspace only holds split-K
+ * partials; otherwise an im2col pass fills a column buffer in the workspace
+ * first (mt_conv2d_workspace_f32 reports the size of whichever path the
+ * geometry takes; a misaligned weight then needs the column buffer too and
+ * the call returns MT_ERR_WORKSPACE if it is missing).  Replaces conv2d_gpu +
  * im2col_kernel + batched_sgemm_kernel_v2 (reference src/gpu_ops.cpp:2237-2325,
  * 1748-1825, 683-859; declared include/TensorOps.hpp:708). */
 typedef struct mt_conv2d_desc {
@@ -125,6 +131,16 @@ int mt_conv2d_fwd_f32(const mt_conv2d_desc* d, const float* input, const float* 
                       const float* bias, float* output, void* workspace, size_t ws_bytes,
                       void* stream);
 size_t mt_conv2d_workspace_f32(const mt_conv2d_desc* d);
+/* Same, for an input given as any NCHW view: in_strides = element strides of
+ * (n, c, h, w), e.g. a channel slice or an NHWC-stored tensor, read in place
+ * (weight and output stay dense).  Replaces conv2d_gpu_strided +
+ * conv2d_forward_kernel_strided (reference src/gpu_ops.cpp:2328-2399;
+ * declared include/TensorOps.hpp:709), which conv2d() takes for
+ * non-contiguous operands (include/TensorOps.hpp:1088-1097). */
+int mt_conv2d_fwd_strided_f32(const mt_conv2d_desc* d, const float* input,
+                              const int64_t in_strides[4], const float* weight,
+                              const float* bias, float* output, void* workspace,
+                              size_t ws_bytes, void* stream);
 
 /* Conv2D backward as GEMMs (dense NCHW tensors, same descriptor as forward):
  *   weight: dW[c_out, c_in*kh*kw] = dY[c_out, n*h_out*w_out] · colᵀ (+ beta·dW)

@@ -81,6 +81,11 @@ _SIGS = {
     "mt_conv2d_fwd_f32": (ctypes.c_int, [_P(Conv2dDesc), ctypes.c_void_p, ctypes.c_void_p,
                                          ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                          ctypes.c_size_t, ctypes.c_void_p]),
+    "mt_conv2d_fwd_strided_f32": (ctypes.c_int, [_P(Conv2dDesc), ctypes.c_void_p,
+                                                  _P(ctypes.c_int64), ctypes.c_void_p,
+                                                  ctypes.c_void_p, ctypes.c_void_p,
+                                                  ctypes.c_void_p, ctypes.c_size_t,
+                                                  ctypes.c_void_p]),
     "mt_conv2d_workspace_f32": (ctypes.c_size_t, [_P(Conv2dDesc)]),
     "mt_conv2d_bwd_weight_f32": (ctypes.c_int, [_P(Conv2dDesc), ctypes.c_void_p, ctypes.c_void_p,
                                                 ctypes.c_void_p, ctypes.c_float, ctypes.c_void_p,
@@ -287,13 +292,15 @@ def conv_out_size(inp: int, pad: int, k: int, stride: int) -> int:
 
 def conv2d(x: torch.Tensor, w: torch.Tensor, b: Optional[torch.Tensor] = None, stride: int = 1,
            padding: int = 0, ws: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
-    """The reference's conv2d forward on NCHW tensors as one fused GEMM."""
+    """The reference's conv2d forward on NCHW tensors as one fused GEMM.
+
+    x may be any NCHW view (read in place through its strides); the weight
+    and bias are made dense."""
     _require_gpu(x, w, b)
     if x.dim() != 4 or w.dim() != 4 or x.shape[1] != w.shape[1]:
         raise ValueError("conv2d: expected input [N,C,H,W] and weight [Cout,C,kh,kw]")
     if b is not None and (b.dim() != 1 or b.shape[0] != w.shape[0]):
         raise ValueError("conv2d: bias must be [Cout]")
-    x = x.contiguous()
     w = w.contiguous()
     b = b.contiguous() if b is not None else None
     n, c, h, wd = x.shape
@@ -303,10 +310,11 @@ def conv2d(x: torch.Tensor, w: torch.Tensor, b: Optional[torch.Tensor] = None, s
     out = torch.empty((n, co, ho, wo), dtype=torch.float32, device=x.device)
     if ws is None:
         ws = workspace(lib().mt_conv2d_workspace_f32(ctypes.byref(d)), x.device)
-    rc = lib().mt_conv2d_fwd_f32(ctypes.byref(d), x.data_ptr(), w.data_ptr(), _ptr(b),
-                                 out.data_ptr(), _ptr(ws), ws.numel() if ws is not None else 0,
-                                 _stream(stream))
-    _check(rc, "mt_conv2d_fwd_f32")
+    strides = (ctypes.c_int64 * 4)(*x.stride())
+    rc = lib().mt_conv2d_fwd_strided_f32(ctypes.byref(d), x.data_ptr(), strides, w.data_ptr(),
+                                         _ptr(b), out.data_ptr(), _ptr(ws),
+                                         ws.numel() if ws is not None else 0, _stream(stream))
+    _check(rc, "mt_conv2d_fwd_strided_f32")
     return out
 
 

@@ -33,13 +33,15 @@ COMMON = [
     "-Wno-unused-command-line-argument",
 ]
 
-N_CFG = 3
+N_CFG = 3      # register-staged tile configurations (TileCfg)
+N_DL_CFG = 4   # direct-to-LDS tile configurations (DlCfg)
 
 
 def _units():
     units = []
     for cfg in range(N_CFG):
         units.append((CSRC / "gemm_instances.hip", OBJDIR / f"gemm_cfg{cfg}.o", [f"-DMT_CFG={cfg}"]))
+    for cfg in range(N_DL_CFG):
         units.append((CSRC / "gemm_dl_instances.hip", OBJDIR / f"gemm_dl_cfg{cfg}.o",
                       [f"-DMT_CFG={cfg}"]))
     units.append((CSRC / "mtgemm_api.hip", OBJDIR / "mtgemm_api.o", []))

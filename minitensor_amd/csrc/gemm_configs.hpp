@@ -44,6 +44,11 @@ template <> struct DlCfg<1> { static constexpr int BM = 128, BN = 128, WM = 64, 
 // 4 waves of 32x32; 2 x 8 KB ring, up to eight workgroups per CU.  (Deeper
 // rings measured slower for these tiles: occupancy hides more latency.)
 template <> struct DlCfg<2> { static constexpr int BM = 64, BN = 64, WM = 32, WN = 32, STAGES = 2; };
+// 8 waves of 64x64; 2 x 24 KB ring.  Fills the chip where M is about 256
+// (e.g. convolutions with 256 output channels: 49 tiles x split 5 = 245).
+template <> struct DlCfg<3> { static constexpr int BM = 256, BN = 128, WM = 64, WN = 64, STAGES = 2; };
+
+constexpr int kNumDlCfg = 4;
 
 template <int CFG>
 constexpr int dl_threads() {
@@ -54,5 +59,11 @@ constexpr int dl_threads() {
 GemmLaunchFn dl_launcher_cfg0(int la, int lb);
 GemmLaunchFn dl_launcher_cfg1(int la, int lb);
 GemmLaunchFn dl_launcher_cfg2(int la, int lb);
+GemmLaunchFn dl_launcher_cfg3(int la, int lb);
+// Implicit-im2col convolution: A = weights (L_KV), B = L_IM (GemmParams::cv).
+GemmLaunchFn dl_conv_launcher_cfg0();
+GemmLaunchFn dl_conv_launcher_cfg1();
+GemmLaunchFn dl_conv_launcher_cfg2();
+GemmLaunchFn dl_conv_launcher_cfg3();
 
 }  // namespace mtk

@@ -1,6 +1,7 @@
 // gemm_dl_instances.hip -- instantiates gemm_f32_dl for one tile
-// configuration (selected with -DMT_CFG=<n>) and the 2x2 vector operand
-// layouts (k-contiguous / mn-contiguous for A and for B).
+// configuration (selected with -DMT_CFG=<n>): the 2x2 vector operand layouts
+// (k-contiguous / mn-contiguous for A and for B), and the implicit-im2col
+// convolution (A k-contiguous weights, B = L_IM).
 #include "gemm_configs.hpp"
 #include "gemm_dl_kernel.hpp"
 
@@ -30,16 +31,25 @@ GemmLaunchFn dl_launcher_cfg0(int la, int lb) {
     static const GemmLaunchFn table[2][2] = MT_DL_TABLE(0);
     return table[la][lb];
 }
+GemmLaunchFn dl_conv_launcher_cfg0() { return launch_dl<0, L_KV, L_IM>; }
 #elif MT_CFG == 1
 GemmLaunchFn dl_launcher_cfg1(int la, int lb) {
     static const GemmLaunchFn table[2][2] = MT_DL_TABLE(1);
     return table[la][lb];
 }
+GemmLaunchFn dl_conv_launcher_cfg1() { return launch_dl<1, L_KV, L_IM>; }
 #elif MT_CFG == 2
 GemmLaunchFn dl_launcher_cfg2(int la, int lb) {
     static const GemmLaunchFn table[2][2] = MT_DL_TABLE(2);
     return table[la][lb];
 }
+GemmLaunchFn dl_conv_launcher_cfg2() { return launch_dl<2, L_KV, L_IM>; }
+#elif MT_CFG == 3
+GemmLaunchFn dl_launcher_cfg3(int la, int lb) {
+    static const GemmLaunchFn table[2][2] = MT_DL_TABLE(3);
+    return table[la][lb];
+}
+GemmLaunchFn dl_conv_launcher_cfg3() { return launch_dl<3, L_KV, L_IM>; }
 #else
 #error "unknown MT_CFG"
 #endif

@@ -28,18 +28,21 @@
 // documented in gemm_kernel.hpp.
 #pragma once
 
+#include <type_traits>
+
 #include "gemm_kernel.hpp"
 
 namespace mtk {
 
 // Geometry of one 16-deep K-chunk of an operand tile with BMN rows, moved by
-// NW waves.
+// NW waves: 16 B per lane (global_load_lds_dwordx4), 256 floats per wave
+// instruction.  The implicit-im2col operand uses the k-contiguous tile.
 template <int L, int BMN, int NW>
 struct DlTile {
-    static_assert(L == L_KV || L == L_MV, "direct-to-LDS needs a 16-byte vector layout");
-    static constexpr bool kc = (L == L_KV);
+    static_assert(L == L_KV || L == L_MV || L == L_IM, "direct-to-LDS needs a DMA layout");
+    static constexpr bool kc = (L == L_KV || L == L_IM);
     static constexpr int floats = BMN * 16;
-    static constexpr int insts = floats / 256;            // 256 floats per wave instruction
+    static constexpr int insts = floats / 256;
     static_assert(insts % NW == 0, "tile must split evenly over the waves");
     static constexpr int per_wave = insts / NW;
 };
@@ -123,6 +126,71 @@ struct DlTail {
     }
 };
 
+// Zero source for gather lanes that fall in the padding or beyond N: the DMA
+// writes every lane, so those lanes read 16 bytes of zeros.
+static __device__ const float __attribute__((aligned(16))) dl_zero_page[4] = {0.f, 0.f, 0.f,
+                                                                              0.f};
+
+// Implicit im2col of a channels-last input as the B operand, in the
+// k-contiguous tile layout of L_KV ([BMN][16], k-groups swizzled).  Lane
+// (row r, group g) of an instruction loads channels ci0 + 4g' .. +3 (g' the
+// k-group stored at g) of output pixel n0 + r at the chunk's filter tap
+// (rt, st): 16 contiguous, 16-byte aligned bytes of xt, or the zero page when
+// the tap falls in the padding or n >= N.  The tap and channel offset are the
+// same for every lane (scalar registers, the wave index is uniform) and step
+// through (rt, st, ci0) once per chunk; per lane only the bounds test and one
+// address add remain.  Chunks must be issued in order 0, 1, 2, ...
+template <int BMN, int NW>
+struct DlImLoader {
+    using T = DlTile<L_IM, BMN, NW>;
+    const float* pix[T::per_wave];   // xt + img*img_stride + (ih0*w + iw0)*c + 4g
+    int ih0[T::per_wave], iw0[T::per_wave];
+    int rt, st, ci0;                 // filter tap and first channel of the next chunk
+    int c, h, w, kw;
+
+    __device__ __forceinline__ void init(const GemmParams& p, const float* X, int n0, int k0,
+                                         int /*kend*/, int wave, int lane) {
+        const ConvGeom& g = p.cv;
+        c = g.c; h = g.h; w = g.w; kw = g.kw;
+        const int hw = g.ho * g.wo;
+#pragma unroll
+        for (int j = 0; j < T::per_wave; ++j) {
+            const int r = (j * NW + wave) * 16 + (lane >> 2);
+            const int grp = (lane & 3) ^ kswz(r);
+            const int n = n0 + r;
+            const int img = n / hw, rem = n - img * hw;
+            const int oh = rem / g.wo, ow = rem - oh * g.wo;
+            ih0[j] = n < p.N ? oh * g.stride - g.pad : -(1 << 30);   // past N: zeros
+            iw0[j] = ow * g.stride - g.pad;
+            pix[j] = X + (int64_t)img * g.img_stride +
+                     ((int64_t)ih0[j] * g.w + iw0[j]) * g.c + grp * 4;
+        }
+        const int tap = k0 / g.c;
+        ci0 = k0 - tap * g.c;
+        rt = tap / g.kw;
+        st = tap - rt * g.kw;
+    }
+
+    __device__ __forceinline__ void issue(float* tile, int /*chunk*/, int wave) {
+        const int64_t toff = ((int64_t)rt * w + st) * c + ci0;
+#pragma unroll
+        for (int j = 0; j < T::per_wave; ++j) {
+            const int q = j * NW + wave;
+            const bool ok = (unsigned)(ih0[j] + rt) < (unsigned)h &&
+                            (unsigned)(iw0[j] + st) < (unsigned)w;
+            const float* src = ok ? pix[j] + toff : dl_zero_page;
+            __builtin_amdgcn_global_load_lds(
+                (const void __attribute__((address_space(1)))*)src,
+                (void __attribute__((address_space(3)))*)(tile + q * 256), 16, 0, 0);
+        }
+        ci0 += 16;                   // next chunk
+        if (ci0 == c) {
+            ci0 = 0;
+            if (++st == kw) { st = 0; ++rt; }
+        }
+    }
+};
+
 // The 8 k-values (permuted order) of one 32-row MFMA block from a chunk tile.
 template <int L, int BMN>
 __device__ __forceinline__ void dl_frag(const float* tile, int row0, int lane, float (&f)[8]) {
@@ -180,7 +248,9 @@ gemm_f32_dl(GemmParams p) {
 
     const int t = threadIdx.x;
     const int lane = t & 63;
-    const int wave = t >> 6;
+    // Uniform across the wave: keeps per-wave loader state and LDS (M0)
+    // addresses in scalar registers.
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const int ra = wm * WM, rb = wn * WN;     // this wave's first row in the A / B tile
 
@@ -190,7 +260,8 @@ gemm_f32_dl(GemmParams p) {
     const int k_end = min(p.K, k_begin + p.k_per_split);
     const int klen = k_end > k_begin ? k_end - k_begin : 0;
     const int nk = klen >> 4;                 // full chunks
-    const bool tail = (klen & 15) != 0;
+    // The implicit operand has c % 16 == 0, so its K ranges hold whole chunks.
+    const bool tail = LB != L_IM && (klen & 15) != 0;
     const float* Ab = p.A + (int64_t)id.bz * p.a_b;
     const float* Bb = p.B + (int64_t)id.bz * p.b_b;
 
@@ -202,8 +273,10 @@ gemm_f32_dl(GemmParams p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
+    constexpr bool im = (LB == L_IM);
+    constexpr int LBF = im ? L_KV : LB;       // LDS layout of B's tile
     DlTail<LA, BM, NT> ta;
-    DlTail<LB, BN, NT> tb;
+    DlTail<LBF, BN, NT> tb;
     if (tail) {
         const int kt0 = k_begin + nk * 16;
         ta.load(Ab, p.a_mn, p.a_k, p.M, m0, kt0, k_end, t);
@@ -211,9 +284,10 @@ gemm_f32_dl(GemmParams p) {
     }
 
     DlLoader<LA, BM, NW> la;
-    DlLoader<LB, BN, NW> lb;
+    std::conditional_t<im, DlImLoader<BN, NW>, DlLoader<LBF, BN, NW>> lb;
     la.init(Ab, p.a_mn, p.a_k, p.M, m0, k_begin, wave, lane);
-    lb.init(Bb, p.b_mn, p.b_k, p.N, n0, k_begin, wave, lane);
+    if constexpr (im) lb.init(p, Bb, n0, k_begin, k_end, wave, lane);
+    else lb.init(Bb, p.b_mn, p.b_k, p.N, n0, k_begin, wave, lane);
 
 #pragma unroll
     for (int c = 0; c < STAGES - 1; ++c)
@@ -231,7 +305,7 @@ gemm_f32_dl(GemmParams p) {
         __builtin_amdgcn_s_barrier();
         float fa[MB][8], fb[NB][8];
         dl_frags<LA, BM, MB>(st, ra, lane, fa);
-        dl_frags<LB, BN, NB>(st + TA::floats, rb, lane, fb);
+        dl_frags<LBF, BN, NB>(st + TA::floats, rb, lane, fb);
         mfma_chunk<MB, NB>(acc, fa, fb);
     }
 
@@ -251,7 +325,7 @@ gemm_f32_dl(GemmParams p) {
         const float* At = smem + (kt % STAGES) * STAGE;
         float fa[MB][8], fb[NB][8];
         dl_frags<LA, BM, MB>(At, ra, lane, fa);
-        dl_frags<LB, BN, NB>(At + TA::floats, rb, lane, fb);
+        dl_frags<LBF, BN, NB>(At + TA::floats, rb, lane, fb);
         mfma_chunk<MB, NB>(acc, fa, fb);
     }
 

@@ -53,7 +53,19 @@ enum : int {
     L_KV = 0,  // k contiguous (stride 1), 16-byte vector loads
     L_MV = 1,  // mn contiguous (stride 1), 16-byte vector loads
     L_KS = 2,  // k-contiguous LDS tile, scalar gathers (any strides)
-    L_MS = 3   // mn-contiguous LDS tile, scalar gathers (any strides)
+    L_MS = 3,  // mn-contiguous LDS tile, scalar gathers (any strides)
+    L_IM = 4   // B only, direct-to-LDS kernel: implicit im2col of a channels-last input
+};
+
+// Geometry of an implicit-im2col B operand over a channels-last input
+// xt[img][ih][iw][ci] (image stride img_stride, dense within an image):
+// B(k, n) with k = (r*kw + s)*c + ci and n = (img*ho + oh)*wo + ow reads
+// xt[img][oh*stride - pad + r][ow*stride - pad + s][ci], zero outside the
+// image.  c % 16 == 0, so a 16-deep K-chunk is 16 consecutive channels of one
+// filter tap.
+struct ConvGeom {
+    int64_t img_stride;
+    int c, h, w, kh, kw, stride, pad, ho, wo;
 };
 
 struct GemmParams {
@@ -70,6 +82,7 @@ struct GemmParams {
     int splits, k_per_split;                  // k_per_split is a multiple of BK
     int c_vec;    // C takes 16-byte stores of 4 consecutive columns (c_n == 1, aligned)
     int ws_vec;   // the split-K workspace takes 16-byte stores (N % 4 == 0, aligned)
+    ConvGeom cv;  // B = implicit im2col of the input at B (layout L_IM only)
     int tiles_m, tiles_n, group_m;
 };
 

@@ -78,6 +78,7 @@ const char* layout_name(int l) {
     switch (l) {
         case L_KV: return "kv";
         case L_MV: return "mv";
+        case L_IM: return "im2col";
         case L_KS: return "ks";
         default: return "ms";
     }
@@ -85,49 +86,63 @@ const char* layout_name(int l) {
 
 struct Plan {
     bool dl = false;   // direct-to-LDS kernel (both operands in a vector layout)
-    int cfg = 0;
+    int cfg = 0;       // TileCfg index (register-staged) or DlCfg index (direct-to-LDS)
+    int bm = 0, bn = 0;
     int splits = 1;
     int kps = 0;
     int tiles_m = 0, tiles_n = 0;
     size_t ws_bytes = 0;
 };
 
-constexpr int kBM[kNumCfg] = {TileCfg<0>::BM, TileCfg<1>::BM, TileCfg<2>::BM};
-constexpr int kBN[kNumCfg] = {TileCfg<0>::BN, TileCfg<1>::BN, TileCfg<2>::BN};
 constexpr int kBK = 16;
 static_assert(TileCfg<0>::BK == kBK && TileCfg<1>::BK == kBK && TileCfg<2>::BK == kBK,
               "split-K granularity assumes one BK for all configurations");
+
+// One tile configuration as the cost model sees it.
+struct CfgCost {
+    int bm, bn;
+    double eff;   // sustained fraction of the CU's MFMA rate inside a workgroup
+    int occ;      // resident workgroups per CU
+};
 
 // Cost model (in CU cycles) used to pick the tile configuration and split-K
 // factor.  Work per workgroup is priced at the CU's fp32 MFMA rate (256
 // flop/clk) with a per-configuration efficiency, plus the epilogue's store of
 // its tile; each round of resident workgroups pays a fixed latency; split-K
-// pays for its partial traffic and the reduction launch.  Row 0: register-
-// staged kernel (any layout); row 1: direct-to-LDS kernel (both operands in a
-// vector layout).  The constants are a least-squares fit to measured times of
-// every configuration and split factor on the benchmark shapes (MI355X).
+// pays for its partial traffic and the reduction launch.  The constants are a
+// least-squares fit to measured times of every configuration and split factor
+// on the benchmark shapes (MI355X).
+constexpr CfgCost kRsCost[kNumCfg] = {      // register-staged kernel, any layout
+    {TileCfg<0>::BM, TileCfg<0>::BN, 0.84, 1},
+    {TileCfg<1>::BM, TileCfg<1>::BN, 0.73, 2},
+    {TileCfg<2>::BM, TileCfg<2>::BN, 0.63, 4}};
+constexpr CfgCost kDlCost[kNumDlCfg] = {    // direct-to-LDS kernel, vector layouts
+    {DlCfg<0>::BM, DlCfg<0>::BN, 0.88, 1},
+    {DlCfg<1>::BM, DlCfg<1>::BN, 0.84, 4},
+    {DlCfg<2>::BM, DlCfg<2>::BN, 0.71, 8},
+    {DlCfg<3>::BM, DlCfg<3>::BN, 0.86, 3}};
 struct CostModel {
-    double eff[2][kNumCfg] = {{0.84, 0.73, 0.63}, {0.88, 0.84, 0.71}};
-    int occ[2][kNumCfg] = {{1, 2, 4}, {1, 4, 8}};   // resident workgroups per CU
     double round_latency = 9000.0;           // cycles of fill/drain per round
     double epilogue_bytes_per_cycle = 10.7;  // one workgroup's tile store
     double bytes_per_cycle = 4260.0;         // device HBM bytes per CU-clock
     double launch_cycles = 8600.0;           // second (reduce) launch
 };
+constexpr int kMaxSplits = 16;
 
 Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool allow_split,
                bool dl) {
     static const CostModel cm;
-    static const int kSplits[] = {1, 2, 3, 4, 6, 8, 12, 16};
-    const int fam = dl ? 1 : 0;
+    const CfgCost* cfgs = dl ? kDlCost : kRsCost;
+    const int ncfg = dl ? kNumDlCfg : kNumCfg;
     Plan best;
     best.dl = dl;
     double best_t = 1e300;
-    for (int cfg = 0; cfg < kNumCfg; ++cfg) {
-        const int64_t tm = (M + kBM[cfg] - 1) / kBM[cfg];
-        const int64_t tn = (N + kBN[cfg] - 1) / kBN[cfg];
+    for (int cfg = 0; cfg < ncfg; ++cfg) {
+        const CfgCost& cc = cfgs[cfg];
+        const int64_t tm = (M + cc.bm - 1) / cc.bm;
+        const int64_t tn = (N + cc.bn - 1) / cc.bn;
         const int64_t tiles = tm * tn * batch;
-        for (int s : kSplits) {
+        for (int s = 1; s <= kMaxSplits; ++s) {
             if (s > 1 && !allow_split) break;
             int64_t kps = K > 0 ? ((K + s - 1) / s + kBK - 1) / kBK * kBK : kBK;
             if (s > 1 && kps < 64) break;
@@ -136,10 +151,10 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool all
             const int64_t wgs = tiles * splits;
             if (wgs * 512 >= ((int64_t)1 << 32)) continue;
             const double per_cu = std::ceil((double)wgs / cus);
-            const double rounds = std::ceil((double)wgs / ((double)cus * cm.occ[fam][cfg]));
-            const double work = (double)kBM[cfg] * kBN[cfg] * (double)std::max<int64_t>(kps, kBK) *
-                                2.0 / (256.0 * cm.eff[fam][cfg]);
-            const double epi = (double)kBM[cfg] * kBN[cfg] * 4.0 / cm.epilogue_bytes_per_cycle;
+            const double rounds = std::ceil((double)wgs / ((double)cus * cc.occ));
+            const double work = (double)cc.bm * cc.bn * (double)std::max<int64_t>(kps, kBK) *
+                                2.0 / (256.0 * cc.eff);
+            const double epi = (double)cc.bm * cc.bn * 4.0 / cm.epilogue_bytes_per_cycle;
             double t = per_cu * (work + epi) + rounds * cm.round_latency;
             if (splits > 1) {
                 const double bytes = (double)(2 * splits + 1) * M * N * batch * 4.0;
@@ -148,6 +163,8 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool all
             if (t < best_t) {
                 best_t = t;
                 best.cfg = cfg;
+                best.bm = cc.bm;
+                best.bn = cc.bn;
                 best.splits = (int)splits;
                 best.kps = (int)kps;
                 best.tiles_m = (int)tm;
@@ -157,6 +174,15 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool all
         }
     }
     return best;
+}
+
+GemmLaunchFn conv_launcher(int cfg) {
+    switch (cfg) {
+        case 0: return dl_conv_launcher_cfg0();
+        case 1: return dl_conv_launcher_cfg1();
+        case 2: return dl_conv_launcher_cfg2();
+        default: return dl_conv_launcher_cfg3();
+    }
 }
 
 // Workspace that covers the plan of either kernel family (for sizes queried
@@ -171,7 +197,8 @@ GemmLaunchFn pick_launcher(const Plan& plan, int la, int lb) {
         switch (plan.cfg) {
             case 0: return dl_launcher_cfg0(la, lb);
             case 1: return dl_launcher_cfg1(la, lb);
-            default: return dl_launcher_cfg2(la, lb);
+            case 2: return dl_launcher_cfg2(la, lb);
+            default: return dl_launcher_cfg3(la, lb);
         }
     }
     switch (plan.cfg) {
@@ -200,6 +227,7 @@ int check_gemm(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C,
 }
 
 // Sum split-K partials in split order, then apply bias and beta: deterministic.
+// Scalar form, for outputs that do not take 16-byte stores.
 __global__ void __launch_bounds__(256) splitk_reduce_f32(GemmParams p) {
     const int64_t MN = (int64_t)p.M * p.N;
     const int64_t total = MN * p.batch;
@@ -213,17 +241,84 @@ __global__ void __launch_bounds__(256) splitk_reduce_f32(GemmParams p) {
         for (int s = 0; s < p.splits; ++s) v += p.ws[((int64_t)s * p.batch + bz) * MN + mn];
         if (p.bias_axis == 1) v += p.bias[(int64_t)m * p.bias_stride];
         else if (p.bias_axis == 2) v += p.bias[(int64_t)n * p.bias_stride];
-        int64_t coff;
-        if (p.c_n_inner >= p.N) {
-            coff = (int64_t)n * p.c_n;
-        } else {
-            const int64_t no = n / p.c_n_inner, ni = n - no * p.c_n_inner;
-            coff = no * p.c_n_outer + ni * p.c_n;
-        }
-        float* dst = p.C + bz * p.c_b + (int64_t)m * p.c_m + coff;
+        float* dst = p.C + bz * p.c_b + (int64_t)m * p.c_m + col_offset(p, n);
         if (p.beta != 0.f) v += p.beta * *dst;
         *dst = v;
     }
+}
+
+// Vector form (ws_vec and c_vec: N % 4 == 0, 16-byte runs on both sides):
+// blockIdx.y walks output rows (batch-major), threads walk 4-column groups.
+// Same per-element summation order as the scalar form.
+__global__ void __launch_bounds__(256) splitk_reduce_vec_f32(GemmParams p) {
+    const int64_t MN = (int64_t)p.M * p.N;
+    const int64_t rows = (int64_t)p.M * p.batch;
+    for (int64_t row = blockIdx.y; row < rows; row += gridDim.y) {
+        const int bz = (int)(row / p.M);
+        const int m = (int)(row - (int64_t)bz * p.M);
+        const float brow = p.bias_axis == 1 ? p.bias[(int64_t)m * p.bias_stride] : 0.f;
+        const float* src = p.ws + (int64_t)bz * MN + (int64_t)m * p.N;
+        float* crow = p.C + (int64_t)bz * p.c_b + (int64_t)m * p.c_m;
+        for (int n = (blockIdx.x * blockDim.x + threadIdx.x) * 4; n < p.N;
+             n += gridDim.x * blockDim.x * 4) {
+            f32x4 v = {0.f, 0.f, 0.f, 0.f};
+            for (int s = 0; s < p.splits; ++s)
+                v += *reinterpret_cast<const f32x4*>(src + (int64_t)s * p.batch * MN + n);
+            v += brow;
+            if (p.bias_axis == 2)
+                for (int e = 0; e < 4; ++e) v[e] += p.bias[(int64_t)(n + e) * p.bias_stride];
+            f32x4* dst = reinterpret_cast<f32x4*>(crow + col_offset(p, n));
+            if (p.beta != 0.f) v += p.beta * *dst;
+            *dst = v;
+        }
+    }
+}
+
+// Completes the plan-dependent fields of p (tile grid, split-K, vector
+// epilogue flags), then launches the GEMM kernel and, for split-K, the
+// deterministic reduction.  lb == L_IM selects the implicit-im2col kernel.
+int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t ws_bytes,
+                hipStream_t stream) {
+    const int64_t M = p.M, N = p.N, K = p.K, batch = p.batch;
+    Plan plan = make_plan(M, N, K, batch, device_cu_count(), true, dl);
+    if (plan.splits > 1 && (workspace == nullptr || ws_bytes < plan.ws_bytes))
+        plan = make_plan(M, N, K, batch, device_cu_count(), false, dl);
+    p.splits = plan.splits;
+    p.k_per_split = plan.splits > 1 ? plan.kps : (int)std::max<int64_t>(K, 1);
+    p.tiles_m = plan.tiles_m;
+    p.tiles_n = plan.tiles_n;
+    p.group_m = 4;
+    p.ws = plan.splits > 1 ? static_cast<float*>(workspace) : nullptr;
+    // 16-byte epilogue stores: four consecutive columns must be contiguous,
+    // aligned, and (for a scattered output) never straddle a column group.
+    p.c_vec = p.c_n == 1 && (N & 3) == 0 && ((uintptr_t)p.C & 15u) == 0 && (p.c_m & 3) == 0 &&
+              (batch == 1 || (p.c_b & 3) == 0) &&
+              (p.c_n_inner >= N || ((p.c_n_inner & 3) == 0 && (p.c_n_outer & 3) == 0));
+    p.ws_vec = p.ws != nullptr && ((uintptr_t)p.ws & 15u) == 0 && (N & 3) == 0;
+
+    const int64_t nblocks = (int64_t)plan.tiles_m * plan.tiles_n * plan.splits * batch;
+    if (nblocks >= ((int64_t)1 << 31)) return MT_ERR_UNSUPPORTED;
+    std::snprintf(g_last_config, sizeof g_last_config, "%s %dx%d a=%s b=%s split=%d wgs=%lld",
+                  plan.dl ? "dl" : "rs", plan.bm, plan.bn, layout_name(la),
+                  layout_name(lb), plan.splits, (long long)nblocks);
+
+    GemmLaunchFn fn = lb == L_IM ? conv_launcher(plan.cfg) : pick_launcher(plan, la, lb);
+    hipError_t e = fn(p, (unsigned)nblocks, stream);
+    if (e == hipErrorStreamCaptureUnsupported) e = hipSuccess;
+    if (e != hipSuccess) return MT_ERR_HIP;
+    if (plan.splits > 1) {
+        if (p.ws_vec && p.c_vec) {
+            const dim3 grid((unsigned)std::min<int64_t>((N / 4 + 255) / 256, 64),
+                            (unsigned)std::min<int64_t>(M * batch, 65535));
+            hipLaunchKernelGGL(splitk_reduce_vec_f32, grid, dim3(256), 0, stream, p);
+        } else {
+            const int64_t total = M * N * batch;
+            const int64_t blocks = std::min<int64_t>((total + 255) / 256, 65536);
+            hipLaunchKernelGGL(splitk_reduce_f32, dim3((unsigned)blocks), dim3(256), 0, stream, p);
+        }
+        if (capture_safe_last_error() != hipSuccess) return MT_ERR_HIP;
+    }
+    return MT_OK;
 }
 
 int run_gemm(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C, int64_t c_n_inner,
@@ -263,38 +358,7 @@ int run_gemm(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C, int6
     const int lb = K == 0 ? L_KS : classify(p.B, p.b_mn, p.b_k, N, K, p.b_b, p.b_b != 0);
 
     const bool dl = (la == L_KV || la == L_MV) && (lb == L_KV || lb == L_MV);
-    Plan plan = make_plan(M, N, K, batch, device_cu_count(), true, dl);
-    if (plan.splits > 1 && (workspace == nullptr || ws_bytes < plan.ws_bytes))
-        plan = make_plan(M, N, K, batch, device_cu_count(), false, dl);
-    p.splits = plan.splits;
-    p.k_per_split = plan.splits > 1 ? plan.kps : (int)std::max<int64_t>(K, 1);
-    p.tiles_m = plan.tiles_m;
-    p.tiles_n = plan.tiles_n;
-    p.group_m = 4;
-    p.ws = plan.splits > 1 ? static_cast<float*>(workspace) : nullptr;
-    // 16-byte epilogue stores: four consecutive columns must be contiguous,
-    // aligned, and (for a scattered output) never straddle a column group.
-    p.c_vec = p.c_n == 1 && (N & 3) == 0 && ((uintptr_t)p.C & 15u) == 0 && (p.c_m & 3) == 0 &&
-              (batch == 1 || (p.c_b & 3) == 0) &&
-              (p.c_n_inner >= N || ((p.c_n_inner & 3) == 0 && (p.c_n_outer & 3) == 0));
-    p.ws_vec = p.ws != nullptr && ((uintptr_t)p.ws & 15u) == 0 && (N & 3) == 0;
-
-    const int64_t nblocks = (int64_t)plan.tiles_m * plan.tiles_n * plan.splits * batch;
-    if (nblocks >= ((int64_t)1 << 31)) return MT_ERR_UNSUPPORTED;
-    std::snprintf(g_last_config, sizeof g_last_config, "%s %dx%d a=%s b=%s split=%d wgs=%lld",
-                  plan.dl ? "dl" : "rs", kBM[plan.cfg], kBN[plan.cfg], layout_name(la), layout_name(lb), plan.splits,
-                  (long long)nblocks);
-
-    hipError_t e = pick_launcher(plan, la, lb)(p, (unsigned)nblocks, stream);
-    if (e == hipErrorStreamCaptureUnsupported) e = hipSuccess;
-    if (e != hipSuccess) return MT_ERR_HIP;
-    if (plan.splits > 1) {
-        const int64_t total = M * N * batch;
-        const int64_t blocks = std::min<int64_t>((total + 255) / 256, 65536);
-        hipLaunchKernelGGL(splitk_reduce_f32, dim3((unsigned)blocks), dim3(256), 0, stream, p);
-        if (capture_safe_last_error() != hipSuccess) return MT_ERR_HIP;
-    }
-    return MT_OK;
+    return launch_gemm(p, dl, la, lb, workspace, ws_bytes, stream);
 }
 
 size_t gemm_ws(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C) {
@@ -328,8 +392,8 @@ colsum_f32(const float* X, int64_t rs, int64_t cs, int R, int Cn, float* out, in
 // np decomposition is done once and the stores are coalesced along np.
 constexpr int kIm2colK = 32;
 __global__ void __launch_bounds__(256)
-im2col_f32(const float* in, float* col, int C, int H, int W, int kh, int kw, int st, int pad,
-           int Ho, int Wo, int64_t NP, int64_t Kg) {
+im2col_f32(const float* in, int64_t sn, int64_t sc, int64_t sh, int64_t sw, float* col, int H,
+           int W, int kh, int kw, int st, int pad, int Ho, int Wo, int64_t NP, int64_t Kg) {
     const int64_t np = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (np >= NP) return;
     const int64_t hw = (int64_t)Ho * Wo;
@@ -337,7 +401,7 @@ im2col_f32(const float* in, float* col, int C, int H, int W, int kh, int kw, int
     const int rem = (int)(np - img * hw);
     const int oh = rem / Wo, ow = rem - oh * Wo;
     const int iy0 = oh * st - pad, ix0 = ow * st - pad;
-    const float* src = in + img * (int64_t)C * H * W;
+    const float* src = in + img * sn;
     int64_t k = (int64_t)blockIdx.y * kIm2colK;
     const int64_t kend = std::min<int64_t>(Kg, k + kIm2colK);
     int s = (int)(k % kw);
@@ -346,7 +410,7 @@ im2col_f32(const float* in, float* col, int C, int H, int W, int kh, int kw, int
     for (; k < kend; ++k) {
         const int iy = iy0 + r, ix = ix0 + s;
         float v = 0.f;
-        if (iy >= 0 && iy < H && ix >= 0 && ix < W) v = src[((int64_t)c * H + iy) * W + ix];
+        if (iy >= 0 && iy < H && ix >= 0 && ix < W) v = src[c * sc + iy * sh + ix * sw];
         col[k * NP + np] = v;
         if (++s == kw) { s = 0; if (++r == kh) { r = 0; ++c; } }
     }
@@ -379,6 +443,21 @@ void conv_gemm_views(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, const floa
     *C = mt_mat_f32{output, 0, d->c_out, np, Ho * Wo, 1, 1, 0};
 }
 
+
+// The implicit-GEMM convolution gathers 16 consecutive channels per K-chunk
+// from a channels-last copy of the input, so it needs c_in % 16 == 0.
+bool implicit_geometry(const mt_conv2d_desc* d) {
+    return d->c_in > 0 && (d->c_in & 15) == 0;
+}
+
+// Workspace of the implicit path: channels-last input, OHWI weights, split-K.
+struct ImplicitWs {
+    size_t xt, wt;
+};
+ImplicitWs implicit_ws(const mt_conv2d_desc* d) {
+    return {align_up((size_t)d->n * d->c_in * d->h * d->w * sizeof(float), 256),
+            align_up((size_t)d->c_out * d->c_in * d->kh * d->kw * sizeof(float), 256)};
+}
 
 // ---- support kernels ---------------------------------------------------------
 __global__ void __launch_bounds__(256) fill_f32(float* p, int64_t n, float v) {
@@ -473,13 +552,62 @@ hipError_t transpose_dy(const mt_conv2d_desc* d, int64_t hw, const float* dy, fl
     return capture_safe_last_error();
 }
 
+// out[b][j][i] = in[b*sb + i*si + (j / jw)*sj1 + (j % jw)*sj0], out dense
+// [B][J][I]: a batched transpose through a 32x33 LDS tile, reads coalesced
+// along j (when sj0 == 1) and writes coalesced along i.  With b = image,
+// i = channel, j = pixel it turns an NCHW view into channels-last; with
+// b = c_out, i = c_in, j = filter tap it turns OIHW weights into OHWI.
+__global__ void __launch_bounds__(256)
+transpose_f32(const float* in, int64_t sb, int64_t si, int64_t sj1, int64_t sj0, int jw, int I,
+              int J, int B, float* out) {
+    __shared__ float tile[32][33];
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+    const int i0 = blockIdx.y * 32, j0 = blockIdx.x * 32;
+    for (int b = blockIdx.z; b < B; b += gridDim.z) {
+        const float* src = in + (int64_t)b * sb;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = i0 + ty + 8 * k, j = j0 + tx;
+            float v = 0.f;
+            if (i < I && j < J) {
+                const int jh = j / jw;
+                v = src[(int64_t)i * si + (int64_t)jh * sj1 + (int64_t)(j - jh * jw) * sj0];
+            }
+            tile[ty + 8 * k][tx] = v;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int j = j0 + ty + 8 * k, i = i0 + tx;
+            if (i < I && j < J) out[((int64_t)b * J + j) * I + i] = tile[tx][ty + 8 * k];
+        }
+        __syncthreads();
+    }
+}
+
+hipError_t launch_transpose(const float* in, int64_t sb, int64_t si, int64_t sj1, int64_t sj0,
+                            int64_t jw, int64_t I, int64_t J, int64_t B, float* out,
+                            hipStream_t s) {
+    if (I == 0 || J == 0 || B == 0) return hipSuccess;
+    dim3 grid((unsigned)((J + 31) / 32), (unsigned)((I + 31) / 32),
+              (unsigned)std::min<int64_t>(B, 65535));
+    hipLaunchKernelGGL(transpose_f32, grid, dim3(256), 0, s, in, sb, si, sj1, sj0, (int)jw,
+                       (int)I, (int)J, (int)B, out);
+    return capture_safe_last_error();
+}
+
+// Element strides of a dense NCHW tensor.
+void dense_strides(const mt_conv2d_desc* d, int64_t st[4]) {
+    st[3] = 1; st[2] = d->w; st[1] = d->h * d->w; st[0] = d->c_in * d->h * d->w;
+}
+
 hipError_t launch_im2col(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, const float* input,
-                         float* col, hipStream_t s) {
+                         const int64_t in_st[4], float* col, hipStream_t s) {
     const int64_t kg = d->c_in * d->kh * d->kw, np = d->n * Ho * Wo;
     dim3 grid((unsigned)((np + 255) / 256), (unsigned)((kg + kIm2colK - 1) / kIm2colK));
-    hipLaunchKernelGGL(im2col_f32, grid, dim3(256), 0, s, input, col, (int)d->c_in, (int)d->h,
-                       (int)d->w, (int)d->kh, (int)d->kw, (int)d->stride, (int)d->pad, (int)Ho,
-                       (int)Wo, np, kg);
+    hipLaunchKernelGGL(im2col_f32, grid, dim3(256), 0, s, input, in_st[0], in_st[1], in_st[2],
+                       in_st[3], col, (int)d->h, (int)d->w, (int)d->kh, (int)d->kw,
+                       (int)d->stride, (int)d->pad, (int)Ho, (int)Wo, np, kg);
     return capture_safe_last_error();
 }
 
@@ -564,29 +692,91 @@ size_t mt_conv2d_workspace_f32(const mt_conv2d_desc* d) {
     if (!conv_dims(d, &Ho, &Wo)) return 0;
     const int64_t kg = d->c_in * d->kh * d->kw, np = d->n * Ho * Wo;
     if (np == 0 || d->c_out == 0) return 0;
-    const size_t col = align_up((size_t)kg * np * sizeof(float), 256);
-    return col + plan_ws(d->c_out, np, kg, 1, device_cu_count());
+    const size_t gemm = plan_ws(d->c_out, np, kg, 1, device_cu_count());
+    if (implicit_geometry(d) && d->h * d->w < kMaxDim) {   // no column buffer
+        const ImplicitWs iw = implicit_ws(d);
+        return iw.xt + iw.wt + gemm;
+    }
+    return align_up((size_t)kg * np * sizeof(float), 256) + gemm;
 }
 
-int mt_conv2d_fwd_f32(const mt_conv2d_desc* d, const float* input, const float* weight,
-                      const float* bias, float* output, void* workspace, size_t ws_bytes,
-                      void* stream) {
+int mt_conv2d_fwd_strided_f32(const mt_conv2d_desc* d, const float* input,
+                              const int64_t in_strides[4], const float* weight, const float* bias,
+                              float* output, void* workspace, size_t ws_bytes, void* stream) {
     int64_t Ho, Wo;
-    if (!conv_dims(d, &Ho, &Wo)) return MT_ERR_INVALID;
-    const int64_t kg = d->c_in * d->kh * d->kw, np = d->n * Ho * Wo;
+    if (!conv_dims(d, &Ho, &Wo) || !in_strides) return MT_ERR_INVALID;
+    for (int i = 0; i < 4; ++i)
+        if (in_strides[i] < 0) return MT_ERR_INVALID;
+    const int64_t kg = d->c_in * d->kh * d->kw, np = d->n * Ho * Wo, hw = Ho * Wo;
     if (np == 0 || d->c_out == 0) return MT_OK;
     if (!output || (kg > 0 && (!input || !weight))) return MT_ERR_INVALID;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+
+    if (implicit_geometry(d) && d->h * d->w < kMaxDim) {
+        // Implicit GEMM: C[c_out, np] = Wt[c_out, kg] · im2col(xt)[kg, np] with
+        // k = (r*kw + s)*c_in + ci, the im2col operand gathered by the kernel
+        // from a channels-last input xt (the input itself when it already is
+        // one, else a transposed copy) and Wt the weights in OHWI order.
+        const ImplicitWs iw = implicit_ws(d);
+        if (!workspace || ws_bytes < iw.xt + iw.wt || ((uintptr_t)workspace & 15u) != 0)
+            return MT_ERR_WORKSPACE;
+        char* wsp = static_cast<char*>(workspace);
+        const int64_t c = d->c_in;
+        const bool nhwc = in_strides[1] == 1 && in_strides[3] == c && in_strides[2] == d->w * c &&
+                          (in_strides[0] & 3) == 0 && ((uintptr_t)input & 15u) == 0;
+        const float* xt = input;
+        int64_t img_stride = in_strides[0];
+        if (!nhwc) {
+            float* buf = reinterpret_cast<float*>(wsp);
+            if (launch_transpose(input, in_strides[0], in_strides[1], in_strides[2],
+                                 in_strides[3], d->w, c, d->h * d->w, d->n, buf, s) != hipSuccess)
+                return MT_ERR_HIP;
+            xt = buf;
+            img_stride = d->h * d->w * c;
+        }
+        float* wt = reinterpret_cast<float*>(wsp + iw.xt);
+        if (launch_transpose(weight, kg, d->kh * d->kw, d->kw, 1, d->kw, c, d->kh * d->kw,
+                             d->c_out, wt, s) != hipSuccess)
+            return MT_ERR_HIP;
+        GemmParams p{};
+        p.A = wt; p.a_mn = kg; p.a_k = 1; p.a_b = 0;
+        p.B = xt;
+        p.C = output; p.c_m = hw; p.c_n = 1; p.c_b = 0;
+        p.c_n_inner = hw; p.c_n_outer = d->c_out * hw;
+        p.bias = bias; p.bias_stride = 1; p.bias_axis = bias ? MT_BIAS_ROW : MT_BIAS_NONE;
+        p.beta = 0.f;
+        p.M = (int)d->c_out; p.N = (int)np; p.K = (int)kg; p.batch = 1;
+        ConvGeom& g = p.cv;
+        g.img_stride = img_stride;
+        g.c = (int)c; g.h = (int)d->h; g.w = (int)d->w;
+        g.kh = (int)d->kh; g.kw = (int)d->kw; g.stride = (int)d->stride; g.pad = (int)d->pad;
+        g.ho = (int)Ho; g.wo = (int)Wo;
+        return launch_gemm(p, true, L_KV, L_IM, wsp + iw.xt + iw.wt,
+                           ws_bytes - iw.xt - iw.wt, s);
+    }
+
+    // Explicit im2col into the workspace, then the GEMM on the column buffer.
     const size_t col_bytes = align_up((size_t)kg * np * sizeof(float), 256);
     if (kg > 0 && (!workspace || ws_bytes < col_bytes)) return MT_ERR_WORKSPACE;
-    hipStream_t s = static_cast<hipStream_t>(stream);
     float* col = static_cast<float*>(workspace);
-    if (kg > 0 && launch_im2col(d, Ho, Wo, input, col, s) != hipSuccess) return MT_ERR_HIP;
+    if (kg > 0 && launch_im2col(d, Ho, Wo, input, in_strides, col, s) != hipSuccess)
+        return MT_ERR_HIP;
     mt_mat_f32 A, B, C;
     conv_gemm_views(d, Ho, Wo, weight, col, output, &A, &B, &C);
     mt_epilogue_f32 ep{bias, 1, bias ? MT_BIAS_ROW : MT_BIAS_NONE, 0.f};
     char* gws = static_cast<char*>(workspace) + (kg > 0 ? col_bytes : 0);
     const size_t gws_bytes = ws_bytes > col_bytes ? ws_bytes - col_bytes : 0;
-    return run_gemm(&A, &B, &C, Ho * Wo, d->c_out * Ho * Wo, &ep, gws, gws_bytes, s);
+    return run_gemm(&A, &B, &C, hw, d->c_out * hw, &ep, gws, gws_bytes, s);
+}
+
+int mt_conv2d_fwd_f32(const mt_conv2d_desc* d, const float* input, const float* weight,
+                      const float* bias, float* output, void* workspace, size_t ws_bytes,
+                      void* stream) {
+    if (!d) return MT_ERR_INVALID;
+    int64_t st[4];
+    dense_strides(d, st);
+    return mt_conv2d_fwd_strided_f32(d, input, st, weight, bias, output, workspace, ws_bytes,
+                                     stream);
 }
 
 size_t mt_conv2d_bwd_workspace_f32(const mt_conv2d_desc* d) {
@@ -620,7 +810,9 @@ int mt_conv2d_bwd_weight_f32(const mt_conv2d_desc* d, const float* input, const 
     float* col = static_cast<float*>(workspace);
     float* dyt = reinterpret_cast<float*>(static_cast<char*>(workspace) + col_b);
     if (np > 0) {
-        if (launch_im2col(d, Ho, Wo, input, col, s) != hipSuccess) return MT_ERR_HIP;
+        int64_t st[4];
+        dense_strides(d, st);
+        if (launch_im2col(d, Ho, Wo, input, st, col, s) != hipSuccess) return MT_ERR_HIP;
         if (transpose_dy(d, hw, grad_out, dyt, s) != hipSuccess) return MT_ERR_HIP;
     }
     // dW[c_out, kg] = dYt[c_out, np] · colᵀ[np, kg]

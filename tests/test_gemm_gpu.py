@@ -342,3 +342,22 @@ def test_split_k_partials_ragged_n(dev, N):
     c = run(to_gpu(a, dev), to_gpu(b, dev))
     assert "split=1 " not in mt.last_config() + " "
     assert_close(c, oracle.matmul(a, b), 8192, amax(a), amax(b), f"split-K N={N}")
+
+
+@pytest.mark.parametrize("axis", [mt.BIAS_ROW, mt.BIAS_COL])
+def test_split_k_vector_reduce_bias_beta(dev, axis):
+    # split-K partials summed by the 16-byte reduction with the bias and
+    # beta*C epilogue applied there
+    M, N, K = 64, 132, 8192
+    a = oracle.uniform((M, K), 81)
+    b = oracle.uniform((K, N), 82)
+    bias = oracle.uniform((M if axis == mt.BIAS_ROW else N,), 83)
+    c0 = oracle.uniform((M, N), 84)
+    C = to_gpu(c0, dev)
+    mt.gemm(to_gpu(a, dev), to_gpu(b, dev), out=C, beta=1.0, bias=to_gpu(bias, dev),
+            bias_axis=axis)
+    torch.cuda.synchronize()
+    assert "split=1 " not in mt.last_config() + " ", mt.last_config()
+    want = oracle.matmul(a, b) + c0 + (bias[:, None] if axis == mt.BIAS_ROW else bias[None, :])
+    assert_close(C.cpu().numpy(), want, K, amax(a), amax(b), f"split-K bias {axis} + beta",
+                 extra=1e-6)

@@ -207,3 +207,67 @@ def test_config5a_conv_backward_adjoint(dev):
     _, wdw, wdb = oracle.conv2d_backward(x, w[ch], dy[:, ch], 1, 1)
     assert_close(dw[ch], wdw, 32 * 196, amax(dy), amax(x), "C5a dW sampled channels")
     assert_close(db, dy.astype(np.float64).sum(axis=(0, 2, 3)), 32 * 196, amax(dy), 1.0, "C5a db")
+
+
+# ---- implicit-GEMM convolution ------------------------------------------------
+# c_in % 16 == 0: the kernel gathers im2col columns from a channels-last copy
+# of the input (or the input itself when it is channels-last), 16 channels of
+# one filter tap per K-chunk; no column buffer.  Kernel sizes, strides,
+# padding, channel counts spanning several chunks per tap, N and c_out tails
+# and split-K are covered.  Other channel counts take the explicit im2col path.
+
+@pytest.mark.parametrize("n,c,h,wd,co,kh,kw,stride,pad", [
+    (2, 16, 8, 8, 32, 1, 1, 1, 0),     # 1x1
+    (2, 16, 9, 7, 6, 3, 3, 1, 1),
+    (3, 32, 11, 10, 6, 3, 2, 2, 2),    # 3x2 kernel, stride 2, pad 2
+    (1, 16, 17, 13, 8, 5, 5, 3, 1),    # 5x5, stride 3
+    (2, 16, 5, 5, 4, 7, 7, 1, 3),      # 7x7 on a 5x5 image: mostly padding
+    (1, 48, 6, 6, 5, 1, 1, 1, 0),      # three chunks per tap
+    (1, 512, 7, 7, 64, 3, 3, 1, 1),    # kg = 4608, np = 49: split-K, scalar reduce
+    (1, 512, 8, 8, 64, 3, 3, 1, 1),    # np = 64: split-K, vector reduce + row bias
+    (4, 16, 13, 13, 130, 3, 3, 1, 1),  # c_out tail (clamped weight rows), np = 676
+])
+def test_conv_implicit_shapes(dev, n, c, h, wd, co, kh, kw, stride, pad):
+    x = oracle.normal((n, c, h, wd), 7 * n + c)
+    w = oracle.normal((co, c, kh, kw), co + kh)
+    b = oracle.normal((co,), 5)
+    out = sync_np(mt.conv2d(g(x, dev), g(w, dev), g(b, dev), stride, pad))
+    cfg = mt.last_config()
+    print(f"[config] {cfg}")
+    assert "im2col" in cfg, cfg
+    want = oracle.conv2d(x, w, b, stride, pad)
+    assert_close(out, want, c * kh * kw, amax(x), amax(w), "implicit conv", extra=1e-5)
+
+
+@pytest.mark.parametrize("view", ["channel_slice", "spatial_crop", "nhwc", "batch_step"])
+@pytest.mark.parametrize("c", [16, 3])   # 16: implicit path; 3 (kg = 27): explicit im2col
+def test_conv_strided_input_views(dev, view, c):
+    # Non-contiguous NCHW inputs are read in place (reference
+    # conv2d_forward_kernel_strided, src/gpu_ops.cpp:2328-2399).  "nhwc" is a
+    # channels-last tensor, which the implicit path uses without a copy.
+    co, kh, kw, stride, pad = 6, 3, 3, 1, 1
+    if view == "channel_slice":
+        big = oracle.normal((2, c + 5, 9, 10), 11)
+        X = g(big, dev)[:, 2:2 + c]
+        xv = big[:, 2:2 + c]
+    elif view == "spatial_crop":
+        big = oracle.normal((2, c, 13, 15), 12)
+        X = g(big, dev)[:, :, 1:10, 3:13]
+        xv = big[:, :, 1:10, 3:13]
+    elif view == "nhwc":
+        nhwc = oracle.normal((2, 9, 10, c), 13)
+        X = g(nhwc, dev).permute(0, 3, 1, 2)          # NCHW view of NHWC storage
+        xv = nhwc.transpose(0, 3, 1, 2)
+    else:
+        big = oracle.normal((4, c, 9, 10), 14)
+        X = g(big, dev)[::2]
+        xv = big[::2]
+    assert not X.is_contiguous()
+    w = oracle.normal((co, c, kh, kw), 21)
+    b = oracle.normal((co,), 22)
+    out = sync_np(mt.conv2d(X, g(w, dev), g(b, dev), stride, pad))
+    cfg = mt.last_config()
+    print(f"[config] {view} c={c}: {cfg}")
+    assert ("im2col" in cfg) == (c == 16), cfg
+    want = oracle.conv2d(np.ascontiguousarray(xv), w, b, stride, pad)
+    assert_close(out, want, c * kh * kw, amax(xv), amax(w), f"conv {view}", extra=1e-5)
