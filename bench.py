@@ -45,6 +45,10 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run a 256 MiB device copy (rocprof counter calibration)")
+    p.add_argument("--only", default="",
+                   help="comma list of secondary configs (c1,c3,c4,c5a,c5b): run just those "
+                        "and print their JSON, without the headline and CPU legs "
+                        "(per-workload profiles)")
     return p.parse_args()
 
 
@@ -94,8 +98,12 @@ def time_graph(fn, calls: int = 20, replays: int = 10) -> float:
     return ms
 
 
-def secondary(dev) -> dict:
+SECONDARY = ("c1", "c3", "c4", "c5a", "c5b")
+
+
+def secondary(dev, only=SECONDARY) -> dict:
     """BASELINE configs 1, 3, 4, 5 (ms, TFLOPS; GB/s for the HBM-near batched one)."""
+    import ctypes
     import torch
     import minitensor_amd as mt
 
@@ -127,67 +135,69 @@ def secondary(dev) -> dict:
             d["kernel"] = cfg
         out[name] = d
 
-    # C1: MLP-Linear shape 256x512x512
-    A, B = u(256, 512), u(512, 512)
-    C = torch.empty(256, 512, device=dev)
-    ws = mt.workspace(mt.lib().mt_gemm_workspace_f32(mt.mat(A), mt.mat(B), mt.mat(C)), dev)
-    ms = both(lambda: mt.gemm(A, B, out=C, ws=ws), 200, 20)
-    rec("c1_256x512x512", ms, 2 * 256 * 512 * 512, 4 * (256 * 512 + 512 * 512 + 256 * 512),
-        mt.last_config())
+    def ws_for(A, B, C):
+        return mt.workspace(mt.lib().mt_gemm_workspace_f32(mt.mat(A), mt.mat(B), mt.mat(C)), dev)
 
-    # C3: C = A·Bᵀ with B [2048,1024] as a transpose view; and the slice A[128:]
-    A, B = n(2048, 1024), n(2048, 1024)
-    C = torch.empty(2048, 2048, device=dev)
-    ws3 = mt.workspace(mt.lib().mt_gemm_workspace_f32(mt.mat(A), mt.mat(B.t()), mt.mat(C)), dev)
-    ms = both(lambda: mt.gemm(A, B.t(), out=C, ws=ws3), 100, 10)
-    rec("c3a_2048x2048x1024_bT_view", ms, 2 * 2048 * 2048 * 1024, None, mt.last_config())
-    As = A[128:]
-    C2 = torch.empty(1920, 2048, device=dev)
-    ms = both(lambda: mt.gemm(As, B.t(), out=C2, ws=ws3), 100, 10)
-    rec("c3b_1920x2048x1024_slice_bT_view", ms, 2 * 1920 * 2048 * 1024, None, mt.last_config())
+    if "c1" in only:  # MLP-Linear shape 256x512x512
+        A, B = u(256, 512), u(512, 512)
+        C = torch.empty(256, 512, device=dev)
+        ws = ws_for(A, B, C)
+        ms = both(lambda: mt.gemm(A, B, out=C, ws=ws), 200, 20)
+        rec("c1_256x512x512", ms, 2 * 256 * 512 * 512, 4 * (256 * 512 + 512 * 512 + 256 * 512),
+            mt.last_config())
 
-    # C4: Linear fwd + bwd, ResNet50-fc shape
-    X = n(256, 2048)
-    W = n(1000, 2048, std=(2.0 / 2048) ** 0.5)
-    b = torch.zeros(1000, device=dev)
-    dY = n(256, 1000, std=0.01)
-    Y = torch.empty(256, 1000, device=dev)
-    dX = torch.empty(256, 2048, device=dev)
-    dW = torch.empty(1000, 2048, device=dev)
-    db = torch.empty(1000, device=dev)
-    lws = mt.workspace(mt.lib().mt_linear_workspace_f32(256, 2048, 1000), dev)
-    f = 2 * 256 * 1000 * 2048
-    ms_f = both(lambda: mt.linear(X, W, b, out=Y, ws=lws), 200, 20)
-    rec("c4_linear_fwd", ms_f, f, None, mt.last_config())
-    ms_dx = both(lambda: mt.linear_backward(dY, X, W, True, False, False, dx=dX, ws=lws),
-                        200, 20)
-    rec("c4_linear_dx", ms_dx, f, None, mt.last_config())
-    ms_dw = both(lambda: mt.linear_backward(dY, X, W, False, True, True, dw=dW, db=db,
-                                                   ws=lws), 200, 20)
-    rec("c4_linear_dw_db", ms_dw, f, None, mt.last_config())
-    ms_all = both(lambda: (mt.linear(X, W, b, out=Y, ws=lws),
-                                  mt.linear_backward(dY, X, W, dx=dX, dw=dW, db=db, ws=lws)),
-                         200, 20)
-    rec("c4_linear_fwd_bwd_total", ms_all, 3 * f)
+    if "c3" in only:  # C = A·Bᵀ with B [2048,1024] as a transpose view; and the slice A[128:]
+        A, B = n(2048, 1024), n(2048, 1024)
+        C = torch.empty(2048, 2048, device=dev)
+        ws = ws_for(A, B.t(), C)
+        ms = both(lambda: mt.gemm(A, B.t(), out=C, ws=ws), 100, 10)
+        rec("c3a_2048x2048x1024_bT_view", ms, 2 * 2048 * 2048 * 1024, None, mt.last_config())
+        As = A[128:]
+        C2 = torch.empty(1920, 2048, device=dev)
+        ms = both(lambda: mt.gemm(As, B.t(), out=C2, ws=ws), 100, 10)
+        rec("c3b_1920x2048x1024_slice_bT_view", ms, 2 * 1920 * 2048 * 1024, None,
+            mt.last_config())
 
-    # C5a: 3x3 conv as GEMM, ResNet50 bottleneck shape
-    x = n(32, 256, 14, 14)
-    w = n(256, 256, 3, 3, std=(2.0 / 2304) ** 0.5)
-    cb = torch.zeros(256, device=dev)
-    d = mt.Conv2dDesc(32, 256, 14, 14, 256, 3, 3, 1, 1)
-    import ctypes
-    cws = mt.workspace(mt.lib().mt_conv2d_workspace_f32(ctypes.byref(d)), dev)
-    ms = both(lambda: mt.conv2d(x, w, cb, 1, 1, ws=cws), 100, 10)
-    rec("c5a_conv3x3_n32_c256_14x14", ms, 2 * 6272 * 256 * 2304,
-        4 * (x.numel() + w.numel() + cb.numel() + 32 * 256 * 196), mt.last_config())
+    if "c4" in only:  # Linear fwd + bwd, ResNet50-fc shape
+        X = n(256, 2048)
+        W = n(1000, 2048, std=(2.0 / 2048) ** 0.5)
+        b = torch.zeros(1000, device=dev)
+        dY = n(256, 1000, std=0.01)
+        Y = torch.empty(256, 1000, device=dev)
+        dX = torch.empty(256, 2048, device=dev)
+        dW = torch.empty(1000, 2048, device=dev)
+        db = torch.empty(1000, device=dev)
+        lws = mt.workspace(mt.lib().mt_linear_workspace_f32(256, 2048, 1000), dev)
+        f = 2 * 256 * 1000 * 2048
+        ms = both(lambda: mt.linear(X, W, b, out=Y, ws=lws), 200, 20)
+        rec("c4_linear_fwd", ms, f, None, mt.last_config())
+        ms = both(lambda: mt.linear_backward(dY, X, W, True, False, False, dx=dX, ws=lws),
+                  200, 20)
+        rec("c4_linear_dx", ms, f, None, mt.last_config())
+        ms = both(lambda: mt.linear_backward(dY, X, W, False, True, True, dw=dW, db=db,
+                                             ws=lws), 200, 20)
+        rec("c4_linear_dw_db", ms, f, None, mt.last_config())
+        ms = both(lambda: (mt.linear(X, W, b, out=Y, ws=lws),
+                           mt.linear_backward(dY, X, W, dx=dX, dw=dW, db=db, ws=lws)), 200, 20)
+        rec("c4_linear_fwd_bwd_total", ms, 3 * f)
 
-    # C5b: batched 64 x [512,64]·[64,512]
-    A, B = u(64, 512, 64), u(64, 64, 512)
-    C = torch.empty(64, 512, 512, device=dev)
-    ws5 = mt.workspace(mt.lib().mt_gemm_workspace_f32(mt.mat(A), mt.mat(B), mt.mat(C)), dev)
-    ms = both(lambda: mt.gemm(A, B, out=C, ws=ws5), 200, 20)
-    rec("c5b_bmm_64x512x512x64", ms, 2 * 64 * 512 * 512 * 64,
-        4 * 64 * (512 * 64 + 64 * 512 + 512 * 512), mt.last_config())
+    if "c5a" in only:  # 3x3 conv as implicit GEMM, ResNet50 bottleneck shape
+        x = n(32, 256, 14, 14)
+        w = n(256, 256, 3, 3, std=(2.0 / 2304) ** 0.5)
+        cb = torch.zeros(256, device=dev)
+        d = mt.Conv2dDesc(32, 256, 14, 14, 256, 3, 3, 1, 1)
+        cws = mt.workspace(mt.lib().mt_conv2d_workspace_f32(ctypes.byref(d)), dev)
+        ms = both(lambda: mt.conv2d(x, w, cb, 1, 1, ws=cws), 100, 10)
+        rec("c5a_conv3x3_n32_c256_14x14", ms, 2 * 6272 * 256 * 2304,
+            4 * (x.numel() + w.numel() + cb.numel() + 32 * 256 * 196), mt.last_config())
+
+    if "c5b" in only:  # batched 64 x [512,64]·[64,512]
+        A, B = u(64, 512, 64), u(64, 64, 512)
+        C = torch.empty(64, 512, 512, device=dev)
+        ws = ws_for(A, B, C)
+        ms = both(lambda: mt.gemm(A, B, out=C, ws=ws), 200, 20)
+        rec("c5b_bmm_64x512x512x64", ms, 2 * 64 * 512 * 512 * 64,
+            4 * 64 * (512 * 64 + 64 * 512 + 512 * 512), mt.last_config())
     return out
 
 
@@ -244,6 +254,15 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.only:
+        names = tuple(x.strip() for x in args.only.split(",") if x.strip())
+        unknown = [x for x in names if x not in SECONDARY]
+        if unknown:
+            print(f"bench.py: unknown --only entries {unknown}; choose from {SECONDARY}",
+                  file=sys.stderr)
+            sys.exit(2)
+        print(json.dumps({"secondary": secondary(dev, names)}), flush=True)
+        return
     M = N = K = 4096
     g = torch.Generator(device=dev)
     g.manual_seed(42)
