@@ -65,5 +65,10 @@ GemmLaunchFn dl_conv_launcher_cfg0();
 GemmLaunchFn dl_conv_launcher_cfg1();
 GemmLaunchFn dl_conv_launcher_cfg2();
 GemmLaunchFn dl_conv_launcher_cfg3();
+// A and B mn-contiguous, with the row sums of A (GemmParams::rowsum).
+GemmLaunchFn dl_rowsum_launcher_cfg0();
+GemmLaunchFn dl_rowsum_launcher_cfg1();
+GemmLaunchFn dl_rowsum_launcher_cfg2();
+GemmLaunchFn dl_rowsum_launcher_cfg3();
 
 }  // namespace mtk

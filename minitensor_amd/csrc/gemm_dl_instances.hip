@@ -1,7 +1,8 @@
 // gemm_dl_instances.hip -- instantiates gemm_f32_dl for one tile
 // configuration (selected with -DMT_CFG=<n>): the 2x2 vector operand layouts
-// (k-contiguous / mn-contiguous for A and for B), and the implicit-im2col
-// convolution (A k-contiguous weights, B = L_IM).
+// (k-contiguous / mn-contiguous for A and for B), the implicit-im2col
+// convolution (A k-contiguous weights, B = L_IM), and the mn-contiguous pair
+// with fused row sums of A (the Linear dW GEMM with its bias gradient).
 #include "gemm_configs.hpp"
 #include "gemm_dl_kernel.hpp"
 
@@ -12,10 +13,10 @@
 namespace mtk {
 namespace {
 
-template <int CFG, int LA, int LB>
+template <int CFG, int LA, int LB, bool RS = false>
 hipError_t launch_dl(const GemmParams& p, unsigned nblocks, hipStream_t s) {
     using C = DlCfg<CFG>;
-    hipLaunchKernelGGL((gemm_f32_dl<C::BM, C::BN, C::WM, C::WN, LA, LB, C::STAGES>),
+    hipLaunchKernelGGL((gemm_f32_dl<C::BM, C::BN, C::WM, C::WN, LA, LB, C::STAGES, RS>),
                        dim3(nblocks), dim3(dl_threads<CFG>()), 0, s, p);
     return hipGetLastError();
 }
@@ -32,24 +33,28 @@ GemmLaunchFn dl_launcher_cfg0(int la, int lb) {
     return table[la][lb];
 }
 GemmLaunchFn dl_conv_launcher_cfg0() { return launch_dl<0, L_KV, L_IM>; }
+GemmLaunchFn dl_rowsum_launcher_cfg0() { return launch_dl<0, L_MV, L_MV, true>; }
 #elif MT_CFG == 1
 GemmLaunchFn dl_launcher_cfg1(int la, int lb) {
     static const GemmLaunchFn table[2][2] = MT_DL_TABLE(1);
     return table[la][lb];
 }
 GemmLaunchFn dl_conv_launcher_cfg1() { return launch_dl<1, L_KV, L_IM>; }
+GemmLaunchFn dl_rowsum_launcher_cfg1() { return launch_dl<1, L_MV, L_MV, true>; }
 #elif MT_CFG == 2
 GemmLaunchFn dl_launcher_cfg2(int la, int lb) {
     static const GemmLaunchFn table[2][2] = MT_DL_TABLE(2);
     return table[la][lb];
 }
 GemmLaunchFn dl_conv_launcher_cfg2() { return launch_dl<2, L_KV, L_IM>; }
+GemmLaunchFn dl_rowsum_launcher_cfg2() { return launch_dl<2, L_MV, L_MV, true>; }
 #elif MT_CFG == 3
 GemmLaunchFn dl_launcher_cfg3(int la, int lb) {
     static const GemmLaunchFn table[2][2] = MT_DL_TABLE(3);
     return table[la][lb];
 }
 GemmLaunchFn dl_conv_launcher_cfg3() { return launch_dl<3, L_KV, L_IM>; }
+GemmLaunchFn dl_rowsum_launcher_cfg3() { return launch_dl<3, L_MV, L_MV, true>; }
 #else
 #error "unknown MT_CFG"
 #endif

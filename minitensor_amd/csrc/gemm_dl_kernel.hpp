@@ -230,7 +230,9 @@ __device__ __forceinline__ void dl_frags(const float* tile, int row0, int lane, 
     for (int i = 0; i < MB; ++i) dl_frag<L, BMN>(tile, row0 + i * 32, lane, f[i]);
 }
 
-template <int BM, int BN, int WM, int WN, int LA, int LB, int STAGES>
+// RS: also produce the row sums of A (GemmParams::rowsum); a separate
+// instantiation so the other kernels do not pay its registers.
+template <int BM, int BN, int WM, int WN, int LA, int LB, int STAGES, bool RS = false>
 __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64)
 gemm_f32_dl(GemmParams p) {
     constexpr int WAVES_N = BN / WN;
@@ -275,6 +277,20 @@ gemm_f32_dl(GemmParams p) {
 
     constexpr bool im = (LB == L_IM);
     constexpr int LBF = im ? L_KV : LB;       // LDS layout of B's tile
+    // Fused row sums of A: the waves of the first wave column of the first
+    // tile column see every A fragment of their rows exactly once.
+    const bool do_rs = RS && id.tn == 0 && wn == 0;
+    float rsum[MB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) rsum[i] = 0.f;
+    auto add_rows = [&](const float (&fa)[MB][8]) {
+        if (RS && do_rs)
+#pragma unroll
+            for (int i = 0; i < MB; ++i)
+#pragma unroll
+                for (int s = 0; s < 8; ++s) rsum[i] += fa[i][s];
+    };
+
     DlTail<LA, BM, NT> ta;
     DlTail<LBF, BN, NT> tb;
     if (tail) {
@@ -307,6 +323,7 @@ gemm_f32_dl(GemmParams p) {
         dl_frags<LA, BM, MB>(st, ra, lane, fa);
         dl_frags<LBF, BN, NB>(st + TA::floats, rb, lane, fb);
         mfma_chunk<MB, NB>(acc, fa, fb);
+        add_rows(fa);
     }
 
     for (int kt = 0; kt < nk; ++kt) {
@@ -327,6 +344,21 @@ gemm_f32_dl(GemmParams p) {
         dl_frags<LA, BM, MB>(At, ra, lane, fa);
         dl_frags<LBF, BN, NB>(At + TA::floats, rb, lane, fb);
         mfma_chunk<MB, NB>(acc, fa, fb);
+        add_rows(fa);
+    }
+
+    if (RS && do_rs) {
+        // lanes c and c+32 hold the two k-halves of row c: combine, then
+        // the lower lane writes (same order for every row: deterministic)
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+            const float tot = rsum[i] + __shfl_xor(rsum[i], 32);
+            const int m = m0 + ra + i * 32 + (lane & 31);
+            if (lane < 32 && m < p.M) {
+                float* d = p.rowsum + (int64_t)m * p.rowsum_stride;
+                *d = (p.rowsum_beta != 0.f ? p.rowsum_beta * *d : 0.f) + tot;
+            }
+        }
     }
 
     store_tile<MB, NB>(p, acc, m0 + ra, n0 + rb, lane, id.split, id.bz);

@@ -83,6 +83,10 @@ struct GemmParams {
     int c_vec;    // C takes 16-byte stores of 4 consecutive columns (c_n == 1, aligned)
     int ws_vec;   // the split-K workspace takes 16-byte stores (N % 4 == 0, aligned)
     ConvGeom cv;  // B = implicit im2col of the input at B (layout L_IM only)
+    // Optional fused row sums of A (direct-to-LDS kernel, splits == 1 only):
+    // rowsum[m*rowsum_stride] = rowsum_beta*rowsum[...] + sum_k A(m, k).  In
+    // dW = dYᵀ·X this is the bias gradient db = sum over the batch of dY.
+    float* rowsum; int64_t rowsum_stride; float rowsum_beta;
     int tiles_m, tiles_n, group_m;
 };
 

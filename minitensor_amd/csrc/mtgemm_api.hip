@@ -176,6 +176,15 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool all
     return best;
 }
 
+GemmLaunchFn rowsum_launcher(int cfg) {
+    switch (cfg) {
+        case 0: return dl_rowsum_launcher_cfg0();
+        case 1: return dl_rowsum_launcher_cfg1();
+        case 2: return dl_rowsum_launcher_cfg2();
+        default: return dl_rowsum_launcher_cfg3();
+    }
+}
+
 GemmLaunchFn conv_launcher(int cfg) {
     switch (cfg) {
         case 0: return dl_conv_launcher_cfg0();
@@ -283,6 +292,11 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
     Plan plan = make_plan(M, N, K, batch, device_cu_count(), true, dl);
     if (plan.splits > 1 && (workspace == nullptr || ws_bytes < plan.ws_bytes))
         plan = make_plan(M, N, K, batch, device_cu_count(), false, dl);
+    // Row sums of A are fused only into a direct-to-LDS launch of two
+    // mn-contiguous operands without split-K (the caller sees p.rowsum cleared
+    // and computes them separately).
+    if (!plan.dl || plan.splits > 1 || batch != 1 || la != L_MV || lb != L_MV)
+        p.rowsum = nullptr;
     p.splits = plan.splits;
     p.k_per_split = plan.splits > 1 ? plan.kps : (int)std::max<int64_t>(K, 1);
     p.tiles_m = plan.tiles_m;
@@ -302,7 +316,9 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
                   plan.dl ? "dl" : "rs", plan.bm, plan.bn, layout_name(la),
                   layout_name(lb), plan.splits, (long long)nblocks);
 
-    GemmLaunchFn fn = lb == L_IM ? conv_launcher(plan.cfg) : pick_launcher(plan, la, lb);
+    GemmLaunchFn fn = lb == L_IM       ? conv_launcher(plan.cfg)
+                      : p.rowsum != nullptr ? rowsum_launcher(plan.cfg)
+                                            : pick_launcher(plan, la, lb);
     hipError_t e = fn(p, (unsigned)nblocks, stream);
     if (e == hipErrorStreamCaptureUnsupported) e = hipSuccess;
     if (e != hipSuccess) return MT_ERR_HIP;
@@ -321,9 +337,18 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
     return MT_OK;
 }
 
+// Optional fused row sums of A (see GemmParams::rowsum); `done` reports
+// whether the GEMM launch produced them.
+struct RowSums {
+    float* out;
+    int64_t stride;
+    float beta;
+    bool done;
+};
+
 int run_gemm(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C, int64_t c_n_inner,
              int64_t c_n_outer, const mt_epilogue_f32* ep, void* workspace, size_t ws_bytes,
-             hipStream_t stream) {
+             hipStream_t stream, RowSums* rows = nullptr) {
     int64_t M, N, K, batch;
     int rc = check_gemm(A, B, C, &M, &N, &K, &batch);
     if (rc != MT_OK) return rc;
@@ -358,7 +383,14 @@ int run_gemm(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C, int6
     const int lb = K == 0 ? L_KS : classify(p.B, p.b_mn, p.b_k, N, K, p.b_b, p.b_b != 0);
 
     const bool dl = (la == L_KV || la == L_MV) && (lb == L_KV || lb == L_MV);
-    return launch_gemm(p, dl, la, lb, workspace, ws_bytes, stream);
+    if (rows && K > 0) {
+        p.rowsum = rows->out;
+        p.rowsum_stride = rows->stride;
+        p.rowsum_beta = rows->beta;
+    }
+    rc = launch_gemm(p, dl, la, lb, workspace, ws_bytes, stream);
+    if (rows) rows->done = rc == MT_OK && p.rowsum != nullptr;
+    return rc;
 }
 
 size_t gemm_ws(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C) {
@@ -674,13 +706,17 @@ int mt_linear_backward_f32(const mt_mat_f32* dY, const mt_mat_f32* X, const mt_m
         int rc = run_gemm(dY, W, dX, 0, 0, nullptr, workspace, ws_bytes, s);
         if (rc != MT_OK) return rc;
     }
-    if (dW) {  // dW[out,in] = dYᵀ[out,B] · X[B,in] (+ beta_w·dW)
+    bool db_done = false;
+    if (dW) {  // dW[out,in] = dYᵀ[out,B] · X[B,in] (+ beta_w·dW); db = row sums of dYᵀ
         const mt_mat_f32 dYt = transposed(*dY);
         mt_epilogue_f32 ep{nullptr, 0, MT_BIAS_NONE, beta_w};
-        int rc = run_gemm(&dYt, X, dW, 0, 0, &ep, workspace, ws_bytes, s);
+        RowSums rows{db, db_stride, beta_b, false};
+        const bool fuse = db != nullptr && (dW->rows <= 1 || db_stride != 0);
+        int rc = run_gemm(&dYt, X, dW, 0, 0, &ep, workspace, ws_bytes, s, fuse ? &rows : nullptr);
         if (rc != MT_OK) return rc;
+        db_done = fuse && rows.done;
     }
-    if (db) {
+    if (db && !db_done) {
         int rc = mt_colsum_f32(dY, db, db_stride, beta_b, stream);
         if (rc != MT_OK) return rc;
     }

@@ -271,3 +271,38 @@ def test_conv_strided_input_views(dev, view, c):
     assert ("im2col" in cfg) == (c == 16), cfg
     want = oracle.conv2d(np.ascontiguousarray(xv), w, b, stride, pad)
     assert_close(out, want, c * kh * kw, amax(xv), amax(w), f"conv {view}", extra=1e-5)
+
+
+# ---- bias gradient fused into the dW GEMM -------------------------------------
+# db = Σ_batch dY is the row sum of dYᵀ, the A operand of dW = dYᵀ·X: the
+# direct-to-LDS kernel accumulates it from the A fragments when the plan has
+# no split-K; otherwise the column-sum kernel runs.  Both must give the same db.
+
+def test_linear_fused_bias_grad_accumulates(dev):
+    x = oracle.normal((128, 96), 31)
+    w = oracle.normal((64, 96), 32, std=0.1)
+    dy = oracle.normal((128, 64), 33, std=0.1)
+    X, W, dY = g(x, dev), g(w, dev), g(dy, dev)
+    dw = torch.empty(64, 96, device=dev)
+    db = torch.empty(64, device=dev)
+    mt.linear_backward(dY, X, W, need_dx=False, dw=dw, db=db)
+    print(f"[config] dW {mt.last_config()}")
+    _, wdw, wdb = oracle.linear_backward(dy, x, w)
+    assert_close(sync_np(db), wdb, 128, amax(dy), 1.0, "fused db")
+    assert_close(sync_np(dw), wdw, 128, amax(dy), amax(x), "dW")
+    mt.linear_backward(dY, X, W, need_dx=False, dw=dw, db=db, beta_w=1.0, beta_b=1.0)
+    assert_close(sync_np(db), 2 * wdb, 128, amax(dy), 1.0, "fused db accumulated", extra=1e-6)
+    assert_close(sync_np(dw), 2 * wdw, 128, amax(dy), amax(x), "dW accumulated", extra=1e-6)
+
+
+def test_linear_bias_grad_with_split_k_dw(dev):
+    x = oracle.normal((8192, 64), 41)
+    w = oracle.normal((32, 64), 42, std=0.1)
+    dy = oracle.normal((8192, 32), 43, std=0.1)
+    X, W, dY = g(x, dev), g(w, dev), g(dy, dev)
+    _, dw, db = mt.linear_backward(dY, X, W, need_dx=False)
+    print(f"[config] dW {mt.last_config()}")
+    assert "split=1 " not in mt.last_config() + " "
+    _, wdw, wdb = oracle.linear_backward(dy, x, w)
+    assert_close(sync_np(db), wdb, 8192, amax(dy), 1.0, "db (column sums)")
+    assert_close(sync_np(dw), wdw, 8192, amax(dy), amax(x), "dW split-K")
