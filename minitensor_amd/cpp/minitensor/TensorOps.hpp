@@ -318,20 +318,34 @@ void copy_strided(const Tensor<T>& src, Tensor<T>& dst) {
     else copy_strided_cpu(src, dst);
 }
 
+// The input is read in place through its strides (any NCHW view); weight,
+// bias and output are dense.  Covers conv2d_gpu and conv2d_gpu_strided
+// (reference src/gpu_ops.cpp:2237-2325, 2367-2399).
 template <typename T>
 void conv2d_gpu(const Tensor<T>& in, const Tensor<T>& w, const Tensor<T>& bias, Tensor<T>& out,
                 size_t stride, size_t padding) {
     mt_detail::require_float_gpu<T>();
-    Tensor<T> x = in.contiguous(), wt = w.contiguous();
+    Tensor<T> wt = w.contiguous();
     const bool has_b = bias.defined() && !bias.empty();
     Tensor<T> b = has_b ? bias.contiguous() : bias;
-    const mt_conv2d_desc d = mt_detail::conv_desc(x.shape(), wt.shape(), stride, padding);
+    Tensor<T> o = out.is_contiguous() ? out : Tensor<T>(out.shape(), out.device());
+    const mt_conv2d_desc d = mt_detail::conv_desc(in.shape(), wt.shape(), stride, padding);
+    const int64_t st[4] = {(int64_t)in.strides()[0], (int64_t)in.strides()[1],
+                           (int64_t)in.strides()[2], (int64_t)in.strides()[3]};
     mt_detail::Workspace ws(mt_conv2d_workspace_f32(&d), out.device());
-    mt_check_status(mt_conv2d_fwd_f32(&d, x.data() + x.offset(), wt.data() + wt.offset(),
-                                      has_b ? b.data() + b.offset() : nullptr,
-                                      out.data() + out.offset(), ws.get(), ws.size(),
-                                      active_stream()),
+    mt_check_status(mt_conv2d_fwd_strided_f32(&d, in.data() + in.offset(), st,
+                                              wt.data() + wt.offset(),
+                                              has_b ? b.data() + b.offset() : nullptr,
+                                              o.data() + o.offset(), ws.get(), ws.size(),
+                                              active_stream()),
                     "conv2d");
+    if (!out.is_contiguous()) copy_gpu_strided(o, out);
+}
+
+template <typename T>
+void conv2d_gpu_strided(const Tensor<T>& in, const Tensor<T>& w, const Tensor<T>& bias,
+                        Tensor<T>& out, size_t stride, size_t padding) {
+    conv2d_gpu(in, w, bias, out, stride, padding);
 }
 
 template <typename T>

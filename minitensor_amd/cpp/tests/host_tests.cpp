@@ -420,6 +420,24 @@ TEST_GPU(gpu_conv_equivalence_and_backward) {
     check_close(bg.grad(), b.grad(), 4 * 16 * 16, 1, 1);
 }
 
+TEST_GPU(gpu_conv_strided_input_views) {
+    // conv2d reads non-contiguous NCHW inputs in place (reference conv2d_gpu_strided,
+    // src/gpu_ops.cpp:2367-2399): channel slice (implicit GEMM, c_in = 16) and a
+    // transposed view (explicit im2col, c_in = 3), against the CPU device on copies.
+    Tensor<float> big = uniform({2, 20, 9, 10}, 4);
+    Tensor<float> w16 = uniform({6, 16, 3, 3}, 5), b6 = uniform({6}, 6);
+    Tensor<float> xs = big.to(GPU).slice(1, 2, 18);
+    CHECK(!xs.is_contiguous());
+    Tensor<float> want = conv2d(big.slice(1, 2, 18).contiguous(), w16, b6, 1, 1);
+    check_close(conv2d(xs, w16.to(GPU), b6.to(GPU), 1, 1), want, 16 * 9, 1, 1, 1e-5);
+    Tensor<float> t = uniform({2, 10, 3, 9}, 7);          // transpose(1, 2) -> [2, 3, 10, 9]
+    Tensor<float> w3 = uniform({4, 3, 3, 3}, 8), b4 = uniform({4}, 9);
+    Tensor<float> xt = t.to(GPU).transpose(1, 2);
+    CHECK(!xt.is_contiguous());
+    Tensor<float> want3 = conv2d(t.transpose(1, 2).contiguous(), w3, b4, 2, 1);
+    check_close(conv2d(xt, w3.to(GPU), b4.to(GPU), 2, 1), want3, 27, 1, 1, 1e-5);
+}
+
 TEST_GPU(gpu_contiguous_and_dispatch) {
     Tensor<float> a = uniform({37, 53}, 1);
     Tensor<float> t = a.to(GPU).transpose(0, 1);
