@@ -14,9 +14,9 @@
 //     instructions of chunk kt, since the later ones may still be landing.
 //   * LDS tiles are unpadded (the DMA writes 1 KB contiguous per
 //     instruction):  k-contiguous operands -> [BMN][16], with the four 16-B
-//     k-groups of row r stored at position g ^ ((r >> 1) & 3), so that the
-//     fragment reads (two ds_read_b128 per lane, 32 rows at stride 64 B) hit
-//     every bank group once;  mn-contiguous operands -> [16][BMN].
+//     k-groups of row r stored at position g ^ ((r >> 2) & 3), so that the
+//     fragment reads (two ds_read_b128 per lane, 16 rows per LDS cycle at
+//     stride 64 B) hit every bank once;  mn-contiguous operands -> [16][BMN].
 //   * Rows beyond M (or N) read a clamped, valid row: their products only
 //     reach output rows/columns that the epilogue never writes.
 //   * A K range that is not a multiple of 16 ends in a partial chunk.  It is
@@ -47,8 +47,12 @@ struct DlTile {
     static constexpr int per_wave = insts / NW;
 };
 
-// Position (in 16-B groups) of k-group g of row r inside a k-contiguous tile.
-__device__ __forceinline__ int kswz(int r) { return (r >> 1) & 3; }
+// Position (in 16-B groups) of k-group g of row r inside a k-contiguous tile
+// is g ^ kswz(r).  gfx950's LDS has 64 banks of 4 B and serves a
+// ds_read_b128 16 lanes (256 B) at a time; a fragment read has those lanes on
+// 16 consecutive rows at the same k-group.  Row r starts at bank 16*(r%4), so
+// XOR-ing the group with (r/4)%4 makes the 16 rows cover all 64 banks once.
+__device__ __forceinline__ int kswz(int r) { return (r >> 2) & 3; }
 
 template <int L, int BMN, int NW>
 struct DlLoader {
