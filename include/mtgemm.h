@@ -145,7 +145,11 @@ int mt_conv2d_fwd_strided_f32(const mt_conv2d_desc* d, const float* input,
 /* Conv2D backward as GEMMs (dense NCHW tensors, same descriptor as forward):
  *   weight: dW[c_out, c_in*kh*kw] = dY[c_out, n*h_out*w_out] · colᵀ (+ beta·dW)
  *           replaces conv2d_backward_weight_gpu (reference src/gpu_ops.cpp:2623-2713)
- *   input:  dcol = Wᵀ · dY, then a deterministic col2im gather into dX
+ *   input:  stride 1, square kernel, pad <= kh-1, c_out % 16 == 0: the
+ *           implicit-GEMM forward convolution of dY with the weights
+ *           transposed to [c_in][c_out] and flipped, padding kh-1-pad (no
+ *           column buffer); otherwise dcol = Wᵀ · dY, then a deterministic
+ *           col2im gather into dX
  *           replaces conv2d_backward_input_gpu + fused_backward_input_kernel
  *           (reference src/gpu_ops.cpp:2499-2550, 861-907)
  *   bias:   db[c] = Σ_{n,y,x} dY[n,c,y,x] (+ beta·db)

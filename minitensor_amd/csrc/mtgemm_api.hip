@@ -643,6 +643,57 @@ hipError_t launch_im2col(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, const 
     return capture_safe_last_error();
 }
 
+// Implicit-GEMM convolution: C[c_out, np] = Wt[c_out, kg] · im2col(xt)[kg, np]
+// with k = (r*kw + s)*c_in + ci, the im2col operand gathered by the kernel
+// from a channels-last input xt (the input itself when it already is one,
+// else a transposed copy in the workspace) and Wt the OHWI weights, which the
+// caller has already written at wsp + implicit_ws(d).xt.  Needs
+// implicit_geometry(d) and ws_bytes >= xt + wt.
+int run_conv_implicit(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, const float* input,
+                      const int64_t in_strides[4], const float* bias, float* output, char* wsp,
+                      size_t ws_bytes, hipStream_t s) {
+    const ImplicitWs iw = implicit_ws(d);
+    const int64_t c = d->c_in, kg = c * d->kh * d->kw, hw = Ho * Wo, np = d->n * hw;
+    const bool nhwc = in_strides[1] == 1 && in_strides[3] == c && in_strides[2] == d->w * c &&
+                      (in_strides[0] & 3) == 0 && ((uintptr_t)input & 15u) == 0;
+    const float* xt = input;
+    int64_t img_stride = in_strides[0];
+    if (!nhwc) {
+        float* buf = reinterpret_cast<float*>(wsp);
+        if (launch_transpose(input, in_strides[0], in_strides[1], in_strides[2], in_strides[3],
+                             d->w, c, d->h * d->w, d->n, buf, s) != hipSuccess)
+            return MT_ERR_HIP;
+        xt = buf;
+        img_stride = d->h * d->w * c;
+    }
+    GemmParams p{};
+    p.A = reinterpret_cast<const float*>(wsp + iw.xt); p.a_mn = kg; p.a_k = 1; p.a_b = 0;
+    p.B = xt;
+    p.C = output; p.c_m = hw; p.c_n = 1; p.c_b = 0;
+    p.c_n_inner = hw; p.c_n_outer = d->c_out * hw;
+    p.bias = bias; p.bias_stride = 1; p.bias_axis = bias ? MT_BIAS_ROW : MT_BIAS_NONE;
+    p.beta = 0.f;
+    p.M = (int)d->c_out; p.N = (int)np; p.K = (int)kg; p.batch = 1;
+    ConvGeom& g = p.cv;
+    g.img_stride = img_stride;
+    g.c = (int)c; g.h = (int)d->h; g.w = (int)d->w;
+    g.kh = (int)d->kh; g.kw = (int)d->kw; g.stride = (int)d->stride; g.pad = (int)d->pad;
+    g.ho = (int)Ho; g.wo = (int)Wo;
+    return launch_gemm(p, true, L_KV, L_IM, wsp + iw.xt + iw.wt, ws_bytes - iw.xt - iw.wt, s);
+}
+
+// dX of a stride-1 convolution with a square kernel and pad <= kh - 1 is the
+// forward convolution of dY (c_out channels, h_out x w_out) with the weights
+// transposed to [c_in][c_out] and flipped in both spatial axes, padding
+// kh - 1 - pad: dX[ci][ih][iw] = sum_{co,r,s} W[co][ci][r][s]·dY[co][ih+pad-r][iw+pad-s].
+// Returns the descriptor of that convolution, or false when it does not apply
+// (or would not take the implicit path).
+bool dx_as_forward(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, mt_conv2d_desc* t) {
+    if (d->stride != 1 || d->kh != d->kw || d->pad > d->kh - 1) return false;
+    *t = mt_conv2d_desc{d->n, d->c_out, Ho, Wo, d->c_in, d->kh, d->kw, 1, d->kh - 1 - d->pad};
+    return implicit_geometry(t) && Ho * Wo < kMaxDim;
+}
+
 }  // namespace
 
 extern "C" {
@@ -749,46 +800,15 @@ int mt_conv2d_fwd_strided_f32(const mt_conv2d_desc* d, const float* input,
     hipStream_t s = static_cast<hipStream_t>(stream);
 
     if (implicit_geometry(d) && d->h * d->w < kMaxDim) {
-        // Implicit GEMM: C[c_out, np] = Wt[c_out, kg] · im2col(xt)[kg, np] with
-        // k = (r*kw + s)*c_in + ci, the im2col operand gathered by the kernel
-        // from a channels-last input xt (the input itself when it already is
-        // one, else a transposed copy) and Wt the weights in OHWI order.
         const ImplicitWs iw = implicit_ws(d);
         if (!workspace || ws_bytes < iw.xt + iw.wt || ((uintptr_t)workspace & 15u) != 0)
             return MT_ERR_WORKSPACE;
         char* wsp = static_cast<char*>(workspace);
-        const int64_t c = d->c_in;
-        const bool nhwc = in_strides[1] == 1 && in_strides[3] == c && in_strides[2] == d->w * c &&
-                          (in_strides[0] & 3) == 0 && ((uintptr_t)input & 15u) == 0;
-        const float* xt = input;
-        int64_t img_stride = in_strides[0];
-        if (!nhwc) {
-            float* buf = reinterpret_cast<float*>(wsp);
-            if (launch_transpose(input, in_strides[0], in_strides[1], in_strides[2],
-                                 in_strides[3], d->w, c, d->h * d->w, d->n, buf, s) != hipSuccess)
-                return MT_ERR_HIP;
-            xt = buf;
-            img_stride = d->h * d->w * c;
-        }
-        float* wt = reinterpret_cast<float*>(wsp + iw.xt);
-        if (launch_transpose(weight, kg, d->kh * d->kw, d->kw, 1, d->kw, c, d->kh * d->kw,
-                             d->c_out, wt, s) != hipSuccess)
+        float* wt = reinterpret_cast<float*>(wsp + iw.xt);      // OIHW -> OHWI
+        if (launch_transpose(weight, kg, d->kh * d->kw, d->kw, 1, d->kw, d->c_in,
+                             d->kh * d->kw, d->c_out, wt, s) != hipSuccess)
             return MT_ERR_HIP;
-        GemmParams p{};
-        p.A = wt; p.a_mn = kg; p.a_k = 1; p.a_b = 0;
-        p.B = xt;
-        p.C = output; p.c_m = hw; p.c_n = 1; p.c_b = 0;
-        p.c_n_inner = hw; p.c_n_outer = d->c_out * hw;
-        p.bias = bias; p.bias_stride = 1; p.bias_axis = bias ? MT_BIAS_ROW : MT_BIAS_NONE;
-        p.beta = 0.f;
-        p.M = (int)d->c_out; p.N = (int)np; p.K = (int)kg; p.batch = 1;
-        ConvGeom& g = p.cv;
-        g.img_stride = img_stride;
-        g.c = (int)c; g.h = (int)d->h; g.w = (int)d->w;
-        g.kh = (int)d->kh; g.kw = (int)d->kw; g.stride = (int)d->stride; g.pad = (int)d->pad;
-        g.ho = (int)Ho; g.wo = (int)Wo;
-        return launch_gemm(p, true, L_KV, L_IM, wsp + iw.xt + iw.wt,
-                           ws_bytes - iw.xt - iw.wt, s);
+        return run_conv_implicit(d, Ho, Wo, input, in_strides, bias, output, wsp, ws_bytes, s);
     }
 
     // Explicit im2col into the workspace, then the GEMM on the column buffer.
@@ -825,7 +845,15 @@ size_t mt_conv2d_bwd_workspace_f32(const mt_conv2d_desc* d) {
                         align_up((size_t)d->c_out * np * sizeof(float), 256);
     const size_t g = std::max(plan_ws(d->c_out, kg, np, 1, cus),
                               plan_ws(kg, np, d->c_out, 1, cus));
-    return bufs + g;
+    size_t need = bufs + g;
+    mt_conv2d_desc t;
+    if (dx_as_forward(d, Ho, Wo, &t)) {   // implicit dX (usually smaller than the above)
+        const ImplicitWs iw = implicit_ws(&t);
+        need = std::max(need, iw.xt + iw.wt +
+                                  plan_ws(d->c_in, d->n * d->h * d->w, d->c_out * d->kh * d->kw,
+                                          1, cus));
+    }
+    return need;
 }
 
 int mt_conv2d_bwd_weight_f32(const mt_conv2d_desc* d, const float* input, const float* grad_out,
@@ -875,6 +903,24 @@ int mt_conv2d_bwd_input_f32(const mt_conv2d_desc* d, const float* grad_out, cons
         return capture_safe_last_error() == hipSuccess ? MT_OK : MT_ERR_HIP;
     }
     if (!grad_out || !weight) return MT_ERR_INVALID;
+    mt_conv2d_desc t;
+    if (dx_as_forward(d, Ho, Wo, &t)) {
+        // Implicit GEMM of dY with the flipped, transposed weights: no dcol buffer.
+        int64_t th, tw;
+        if (!conv_dims(&t, &th, &tw) || th != d->h || tw != d->w) return MT_ERR_INVALID;
+        const ImplicitWs iw = implicit_ws(&t);
+        if (!workspace || ws_bytes < iw.xt + iw.wt || ((uintptr_t)workspace & 15u) != 0)
+            return MT_ERR_WORKSPACE;
+        char* wsp = static_cast<char*>(workspace);
+        // Wt[ci][r'][s'][co] = W[co][ci][kh-1-r'][kw-1-s'] (negative tap strides)
+        const int64_t khw = d->kh * d->kw;
+        if (launch_transpose(weight + (khw - 1), khw, d->c_in * khw, -d->kw, -1, d->kw, d->c_out,
+                             khw, d->c_in, reinterpret_cast<float*>(wsp + iw.xt), s) != hipSuccess)
+            return MT_ERR_HIP;
+        const int64_t st[4] = {d->c_out * hw, hw, Wo, 1};   // dense dY
+        return run_conv_implicit(&t, d->h, d->w, grad_out, st, nullptr, grad_input, wsp, ws_bytes,
+                                 s);
+    }
     const size_t col_b = align_up((size_t)kg * np * sizeof(float), 256);
     const size_t dyt_b = align_up((size_t)d->c_out * np * sizeof(float), 256);
     if (!workspace || ws_bytes < col_b + dyt_b) return MT_ERR_WORKSPACE;

@@ -306,3 +306,30 @@ def test_linear_bias_grad_with_split_k_dw(dev):
     _, wdw, wdb = oracle.linear_backward(dy, x, w)
     assert_close(sync_np(db), wdb, 8192, amax(dy), 1.0, "db (column sums)")
     assert_close(sync_np(dw), wdw, 8192, amax(dy), amax(x), "dW split-K")
+
+
+# ---- implicit dX: stride-1 backward-input as a forward convolution ------------
+# dX = conv(dY, Wᵀ flipped, pad kh-1-pad) through the implicit-GEMM path
+# (c_out % 16 == 0, square kernel, stride 1, pad <= kh-1); other geometries
+# take the column-buffer path, covered by test_conv_backward_shapes.
+
+@pytest.mark.parametrize("n,c,h,wd,co,k,pad", [
+    (2, 5, 9, 7, 16, 3, 1),
+    (1, 3, 8, 8, 32, 5, 2),
+    (2, 4, 6, 6, 16, 1, 0),     # 1x1: pad' = 0
+    (1, 2, 7, 7, 16, 3, 0),     # pad 0: pad' = 2, output grows back to 7x7
+    (1, 8, 5, 6, 16, 5, 4),     # pad = kh-1: pad' = 0
+    (3, 7, 11, 10, 48, 3, 1),   # c_in tail (odd), three chunks per tap
+])
+def test_conv_backward_input_implicit(dev, n, c, h, wd, co, k, pad):
+    x = oracle.normal((n, c, h, wd), 51)
+    w = oracle.normal((co, c, k, k), 52)
+    ho, wo = oracle.conv_out(h, pad, k, 1), oracle.conv_out(wd, pad, k, 1)
+    dy = oracle.normal((n, co, ho, wo), 53)
+    dx, _, _ = mt.conv2d_backward(g(x, dev), g(w, dev), g(dy, dev), 1, pad, need_dw=False,
+                                  need_db=False)
+    cfg = mt.last_config()
+    print(f"[config] dX {cfg}")
+    assert "im2col" in cfg, cfg
+    wdx, _, _ = oracle.conv2d_backward(x, w, dy, 1, pad)
+    assert_close(sync_np(dx), wdx, co * k * k, amax(dy), amax(w), "implicit conv dX")
