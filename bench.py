@@ -190,6 +190,16 @@ def secondary(dev, only=SECONDARY) -> dict:
         ms = both(lambda: mt.conv2d(x, w, cb, 1, 1, ws=cws), 100, 10)
         rec("c5a_conv3x3_n32_c256_14x14", ms, 2 * 6272 * 256 * 2304,
             4 * (x.numel() + w.numel() + cb.numel() + 32 * 256 * 196), mt.last_config())
+        # the same layer's backward: dX (implicit, flipped weights) and dW (+ db)
+        dy = n(32, 256, 14, 14, std=0.01)
+        bws = mt.workspace(mt.lib().mt_conv2d_bwd_workspace_f32(ctypes.byref(d)), dev)
+        dwb = torch.empty_like(w)
+        ms = both(lambda: mt.conv2d_backward(x, w, dy, 1, 1, need_dw=False, need_db=False,
+                                             ws=bws), 100, 10)
+        rec("c5a_conv_backward_dx", ms, 2 * 6272 * 256 * 2304, None, mt.last_config())
+        ms = both(lambda: mt.conv2d_backward(x, w, dy, 1, 1, need_dx=False, ws=bws, dw=dwb),
+                  100, 10)
+        rec("c5a_conv_backward_dw_db", ms, 2 * 6272 * 256 * 2304, None, mt.last_config())
 
     if "c5b" in only:  # batched 64 x [512,64]·[64,512]
         A, B = u(64, 512, 64), u(64, 64, 512)

@@ -320,8 +320,12 @@ def conv2d(x: torch.Tensor, w: torch.Tensor, b: Optional[torch.Tensor] = None, s
 
 def conv2d_backward(x: torch.Tensor, w: torch.Tensor, dy: torch.Tensor, stride: int = 1,
                     padding: int = 0, need_dx: bool = True, need_dw: bool = True,
-                    need_db: bool = True, ws: Optional[torch.Tensor] = None, stream=None):
-    """Conv2D backward on dense NCHW tensors: returns (dX, dW, db), None where not asked."""
+                    need_db: bool = True, ws: Optional[torch.Tensor] = None, stream=None,
+                    dw: Optional[torch.Tensor] = None, beta_w: float = 0.0):
+    """Conv2D backward on dense NCHW tensors: returns (dX, dW, db), None where not asked.
+
+    dW = beta_w·dw + ∂L/∂W when an existing dense `dw` is passed (gradient
+    accumulation)."""
     _require_gpu(x, w, dy)
     x, w, dy = x.contiguous(), w.contiguous(), dy.contiguous()
     n, c, h, wd = x.shape
@@ -333,16 +337,21 @@ def conv2d_backward(x: torch.Tensor, w: torch.Tensor, dy: torch.Tensor, stride: 
     if ws is None:
         ws = workspace(lib().mt_conv2d_bwd_workspace_f32(ctypes.byref(d)), x.device)
     wp, wn = _ptr(ws), (ws.numel() if ws is not None else 0)
-    dx = dw = db = None
+    dx = db = None
+    if not need_dw:
+        dw = None
     s = _stream(stream)
     if need_dx:
         dx = torch.empty_like(x)
         _check(lib().mt_conv2d_bwd_input_f32(ctypes.byref(d), dy.data_ptr(), w.data_ptr(),
                                              dx.data_ptr(), wp, wn, s), "mt_conv2d_bwd_input_f32")
     if need_dw:
-        dw = torch.empty_like(w)
+        if dw is None:
+            dw = torch.empty_like(w)
+        elif tuple(dw.shape) != tuple(w.shape) or not dw.is_contiguous():
+            raise ValueError("conv2d_backward: dw must be a dense tensor shaped like w")
         _check(lib().mt_conv2d_bwd_weight_f32(ctypes.byref(d), x.data_ptr(), dy.data_ptr(),
-                                              dw.data_ptr(), 0.0, wp, wn, s),
+                                              dw.data_ptr(), float(beta_w), wp, wn, s),
                "mt_conv2d_bwd_weight_f32")
     if need_db:
         db = torch.empty((co,), dtype=torch.float32, device=x.device)

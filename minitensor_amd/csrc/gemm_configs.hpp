@@ -65,6 +65,11 @@ GemmLaunchFn dl_conv_launcher_cfg0();
 GemmLaunchFn dl_conv_launcher_cfg1();
 GemmLaunchFn dl_conv_launcher_cfg2();
 GemmLaunchFn dl_conv_launcher_cfg3();
+// Convolution weight gradient: A = dY [c_out][n*h_out*w_out] (L_KV), B = L_IMW.
+GemmLaunchFn dl_convw_launcher_cfg0();
+GemmLaunchFn dl_convw_launcher_cfg1();
+GemmLaunchFn dl_convw_launcher_cfg2();
+GemmLaunchFn dl_convw_launcher_cfg3();
 // A and B mn-contiguous, with the row sums of A (GemmParams::rowsum).
 GemmLaunchFn dl_rowsum_launcher_cfg0();
 GemmLaunchFn dl_rowsum_launcher_cfg1();

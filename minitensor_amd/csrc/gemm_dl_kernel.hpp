@@ -39,7 +39,8 @@ namespace mtk {
 // instruction.  The implicit-im2col operand uses the k-contiguous tile.
 template <int L, int BMN, int NW>
 struct DlTile {
-    static_assert(L == L_KV || L == L_MV || L == L_IM, "direct-to-LDS needs a DMA layout");
+    static_assert(L == L_KV || L == L_MV || L == L_IM || L == L_IMW,
+                  "direct-to-LDS needs a DMA layout");
     static constexpr bool kc = (L == L_KV || L == L_IM);
     static constexpr int floats = BMN * 16;
     static constexpr int insts = floats / 256;
@@ -195,6 +196,101 @@ struct DlImLoader {
     }
 };
 
+// Implicit im2colᵀ of a channels-last input as the B operand of the
+// convolution weight gradient (L_IMW), tile [16][BMN] (n contiguous, the L_MV
+// LDS layout).  A lane of instruction q covers k-row kr = (q*256 + 4*lane) / BMN
+// and the four columns n .. n+3 at (q*256 + 4*lane) % BMN: four consecutive
+// channels of one filter tap, i.e. 16 contiguous, 16-byte aligned bytes of xt
+// at the output pixel k, or the zero page when the tap falls in the padding,
+// n >= N or k >= k_end.  The column part (tap offsets, channel) is decoded
+// once; the output pixel (img, oh, ow) of k is decoded per chunk.
+template <int BMN, int NW>
+struct DlImwLoader {
+    using T = DlTile<L_IMW, BMN, NW>;
+    const float* X;
+    int kr[T::per_wave];          // k-row of each instruction within a chunk
+    int dr[T::per_wave], ds[T::per_wave], ci[T::per_wave];   // tap - pad, channel
+    bool nok[T::per_wave];        // column inside N
+    int k0, k_end;
+    ConvGeom g;
+
+    __device__ __forceinline__ void init(const GemmParams& p, const float* Xt, int n0, int kb,
+                                         int kend, int wave, int lane) {
+        g = p.cv;
+        X = Xt;
+        k0 = kb;
+        k_end = kend;
+#pragma unroll
+        for (int j = 0; j < T::per_wave; ++j) {
+            const int e = (j * NW + wave) * 256 + lane * 4;
+            kr[j] = e / BMN;
+            const int n = n0 + (e - kr[j] * BMN);
+            nok[j] = n < p.N;
+            const int tap = n / g.c;
+            ci[j] = n - tap * g.c;
+            const int r = tap / g.kw;
+            dr[j] = r - g.pad;
+            ds[j] = (tap - r * g.kw) - g.pad;
+        }
+    }
+
+    __device__ __forceinline__ void issue(float* tile, int chunk, int wave) const {
+        const int hw = g.ho * g.wo;
+#pragma unroll
+        for (int j = 0; j < T::per_wave; ++j) {
+            const int q = j * NW + wave;
+            const int k = k0 + chunk * 16 + kr[j];
+            const int img = k / hw, rem = k - img * hw;
+            const int oh = rem / g.wo, ow = rem - oh * g.wo;
+            const int ih = oh * g.stride + dr[j], iw = ow * g.stride + ds[j];
+            const bool ok = nok[j] && k < k_end && (unsigned)ih < (unsigned)g.h &&
+                            (unsigned)iw < (unsigned)g.w;
+            const float* src =
+                ok ? X + (int64_t)img * g.img_stride + ((int64_t)ih * g.w + iw) * g.c + ci[j]
+                   : dl_zero_page;
+            __builtin_amdgcn_global_load_lds(
+                (const void __attribute__((address_space(1)))*)src,
+                (void __attribute__((address_space(3)))*)(tile + q * 256), 16, 0, 0);
+        }
+    }
+};
+
+// Bounds-checked fetch of the partial chunk [kt0, k_end) of the L_IMW operand
+// into the [16][BMN] layout.
+template <int BMN, int NT>
+struct DlImwTail {
+    static constexpr int NI = BMN * 16 / NT;
+    static_assert(NI * NT == BMN * 16, "tail must split evenly over the threads");
+    float v[NI];
+
+    __device__ __forceinline__ void load(const GemmParams& p, const float* X, int n0, int kt0,
+                                         int k_end, int t) {
+        const ConvGeom& g = p.cv;
+        const int hw = g.ho * g.wo;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int e = t + i * NT;
+            const int kk = e / BMN, n = n0 + (e - kk * BMN), k = kt0 + kk;
+            float x = 0.f;
+            if (k < k_end && n < p.N) {
+                const int img = k / hw, rem = k - img * hw;
+                const int oh = rem / g.wo, ow = rem - oh * g.wo;
+                const int tap = n / g.c, c = n - tap * g.c;
+                const int r = tap / g.kw, s = tap - r * g.kw;
+                const int ih = oh * g.stride - g.pad + r, iw = ow * g.stride - g.pad + s;
+                if ((unsigned)ih < (unsigned)g.h && (unsigned)iw < (unsigned)g.w)
+                    x = X[(int64_t)img * g.img_stride + ((int64_t)ih * g.w + iw) * g.c + c];
+            }
+            v[i] = x;
+        }
+    }
+
+    __device__ __forceinline__ void store(float* tile, int t) const {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) tile[t + i * NT] = v[i];
+    }
+};
+
 // The 8 k-values (permuted order) of one 32-row MFMA block from a chunk tile.
 template <int L, int BMN>
 __device__ __forceinline__ void dl_frag(const float* tile, int row0, int lane, float (&f)[8]) {
@@ -280,7 +376,8 @@ gemm_f32_dl(GemmParams p) {
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     constexpr bool im = (LB == L_IM);
-    constexpr int LBF = im ? L_KV : LB;       // LDS layout of B's tile
+    constexpr bool imw = (LB == L_IMW);
+    constexpr int LBF = im ? L_KV : imw ? L_MV : LB;   // LDS layout of B's tile
     // Fused row sums of A: the waves of the first wave column of the first
     // tile column see every A fragment of their rows exactly once.
     const bool do_rs = RS && id.tn == 0 && wn == 0;
@@ -296,17 +393,19 @@ gemm_f32_dl(GemmParams p) {
     };
 
     DlTail<LA, BM, NT> ta;
-    DlTail<LBF, BN, NT> tb;
+    std::conditional_t<imw, DlImwTail<BN, NT>, DlTail<LBF, BN, NT>> tb;
     if (tail) {
         const int kt0 = k_begin + nk * 16;
         ta.load(Ab, p.a_mn, p.a_k, p.M, m0, kt0, k_end, t);
-        tb.load(Bb, p.b_mn, p.b_k, p.N, n0, kt0, k_end, t);
+        if constexpr (imw) tb.load(p, Bb, n0, kt0, k_end, t);
+        else tb.load(Bb, p.b_mn, p.b_k, p.N, n0, kt0, k_end, t);
     }
 
     DlLoader<LA, BM, NW> la;
-    std::conditional_t<im, DlImLoader<BN, NW>, DlLoader<LBF, BN, NW>> lb;
+    std::conditional_t<im, DlImLoader<BN, NW>,
+                       std::conditional_t<imw, DlImwLoader<BN, NW>, DlLoader<LBF, BN, NW>>> lb;
     la.init(Ab, p.a_mn, p.a_k, p.M, m0, k_begin, wave, lane);
-    if constexpr (im) lb.init(p, Bb, n0, k_begin, k_end, wave, lane);
+    if constexpr (im || imw) lb.init(p, Bb, n0, k_begin, k_end, wave, lane);
     else lb.init(Bb, p.b_mn, p.b_k, p.N, n0, k_begin, wave, lane);
 
 #pragma unroll

@@ -54,15 +54,20 @@ enum : int {
     L_MV = 1,  // mn contiguous (stride 1), 16-byte vector loads
     L_KS = 2,  // k-contiguous LDS tile, scalar gathers (any strides)
     L_MS = 3,  // mn-contiguous LDS tile, scalar gathers (any strides)
-    L_IM = 4   // B only, direct-to-LDS kernel: implicit im2col of a channels-last input
+    L_IM = 4,  // B only, direct-to-LDS kernel: implicit im2col of a channels-last input
+    L_IMW = 5  // B only, direct-to-LDS kernel: implicit im2colᵀ (conv weight gradient)
 };
 
 // Geometry of an implicit-im2col B operand over a channels-last input
 // xt[img][ih][iw][ci] (image stride img_stride, dense within an image):
-// B(k, n) with k = (r*kw + s)*c + ci and n = (img*ho + oh)*wo + ow reads
-// xt[img][oh*stride - pad + r][ow*stride - pad + s][ci], zero outside the
-// image.  c % 16 == 0, so a 16-deep K-chunk is 16 consecutive channels of one
-// filter tap.
+//   L_IM:  B(k, n) with k = (r*kw + s)*c + ci and n = (img*ho + oh)*wo + ow
+//          (forward convolution; c % 16 == 0, so a 16-deep K-chunk is 16
+//          consecutive channels of one filter tap);
+//   L_IMW: B(k, n) with k = (img*ho + oh)*wo + ow and n = (r*kw + s)*c + ci
+//          (weight gradient; c % 4 == 0, so 4 consecutive n are 4
+//          consecutive channels of one tap);
+// both read xt[img][oh*stride - pad + r][ow*stride - pad + s][ci], zero
+// outside the image.
 struct ConvGeom {
     int64_t img_stride;
     int c, h, w, kh, kw, stride, pad, ho, wo;

@@ -79,6 +79,7 @@ const char* layout_name(int l) {
         case L_KV: return "kv";
         case L_MV: return "mv";
         case L_IM: return "im2col";
+        case L_IMW: return "im2colT";
         case L_KS: return "ks";
         default: return "ms";
     }
@@ -182,6 +183,15 @@ GemmLaunchFn rowsum_launcher(int cfg) {
         case 1: return dl_rowsum_launcher_cfg1();
         case 2: return dl_rowsum_launcher_cfg2();
         default: return dl_rowsum_launcher_cfg3();
+    }
+}
+
+GemmLaunchFn convw_launcher(int cfg) {
+    switch (cfg) {
+        case 0: return dl_convw_launcher_cfg0();
+        case 1: return dl_convw_launcher_cfg1();
+        case 2: return dl_convw_launcher_cfg2();
+        default: return dl_convw_launcher_cfg3();
     }
 }
 
@@ -316,7 +326,8 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
                   plan.dl ? "dl" : "rs", plan.bm, plan.bn, layout_name(la),
                   layout_name(lb), plan.splits, (long long)nblocks);
 
-    GemmLaunchFn fn = lb == L_IM       ? conv_launcher(plan.cfg)
+    GemmLaunchFn fn = lb == L_IM          ? conv_launcher(plan.cfg)
+                      : lb == L_IMW         ? convw_launcher(plan.cfg)
                       : p.rowsum != nullptr ? rowsum_launcher(plan.cfg)
                                             : pick_launcher(plan, la, lb);
     hipError_t e = fn(p, (unsigned)nblocks, stream);
@@ -682,6 +693,12 @@ int run_conv_implicit(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, const flo
     return launch_gemm(p, true, L_KV, L_IM, wsp + iw.xt + iw.wt, ws_bytes - iw.xt - iw.wt, s);
 }
 
+// The implicit weight gradient reads 4 channels of one tap per 16-byte vector
+// (c_in % 4 == 0) and dYt [c_out][np] rows as 16-byte vectors (np % 4 == 0).
+bool implicit_dw(const mt_conv2d_desc* d, int64_t np) {
+    return np > 0 && (d->c_in & 3) == 0 && (np & 3) == 0 && d->h * d->w < kMaxDim;
+}
+
 // dX of a stride-1 convolution with a square kernel and pad <= kh - 1 is the
 // forward convolution of dY (c_out channels, h_out x w_out) with the weights
 // transposed to [c_in][c_out] and flipped in both spatial axes, padding
@@ -846,6 +863,10 @@ size_t mt_conv2d_bwd_workspace_f32(const mt_conv2d_desc* d) {
     const size_t g = std::max(plan_ws(d->c_out, kg, np, 1, cus),
                               plan_ws(kg, np, d->c_out, 1, cus));
     size_t need = bufs + g;
+    if (implicit_dw(d, np))
+        need = std::max(need, align_up((size_t)d->n * d->c_in * d->h * d->w * sizeof(float), 256) +
+                                  align_up((size_t)d->c_out * np * sizeof(float), 256) +
+                                  plan_ws(d->c_out, kg, np, 1, cus));
     mt_conv2d_desc t;
     if (dx_as_forward(d, Ho, Wo, &t)) {   // implicit dX (usually smaller than the above)
         const ImplicitWs iw = implicit_ws(&t);
@@ -867,10 +888,39 @@ int mt_conv2d_bwd_weight_f32(const mt_conv2d_desc* d, const float* input, const 
     hipStream_t s = static_cast<hipStream_t>(stream);
     const size_t col_b = align_up((size_t)kg * np * sizeof(float), 256);
     const size_t dyt_b = align_up((size_t)d->c_out * np * sizeof(float), 256);
-    if (np > 0) {
-        if (!input || !grad_out) return MT_ERR_INVALID;
-        if (!workspace || ws_bytes < col_b + dyt_b) return MT_ERR_WORKSPACE;
+    if (np > 0 && (!input || !grad_out)) return MT_ERR_INVALID;
+    if (implicit_dw(d, np)) {
+        // Implicit GEMM dW[c_out, (r,s,ci)] = dYt[c_out, np] · im2colᵀ(xt)[np, (r,s,ci)],
+        // the B operand gathered from a channels-last copy of the input and the
+        // columns scattered to OIHW by the epilogue: col(n) = tap + ci*kh*kw.
+        const size_t xt_b = align_up((size_t)d->n * d->c_in * d->h * d->w * sizeof(float), 256);
+        if (!workspace || ws_bytes < xt_b + dyt_b || ((uintptr_t)workspace & 15u) != 0)
+            return MT_ERR_WORKSPACE;
+        char* wsp = static_cast<char*>(workspace);
+        float* xt = reinterpret_cast<float*>(wsp);
+        float* dyt = reinterpret_cast<float*>(wsp + xt_b);
+        int64_t st[4];
+        dense_strides(d, st);
+        if (launch_transpose(input, st[0], st[1], st[2], st[3], d->w, d->c_in, d->h * d->w, d->n,
+                             xt, s) != hipSuccess)
+            return MT_ERR_HIP;
+        if (transpose_dy(d, hw, grad_out, dyt, s) != hipSuccess) return MT_ERR_HIP;
+        GemmParams p{};
+        p.A = dyt; p.a_mn = np; p.a_k = 1; p.a_b = 0;
+        p.B = xt;
+        p.C = grad_weight; p.c_m = kg; p.c_n = d->kh * d->kw; p.c_b = 0;
+        p.c_n_inner = d->c_in; p.c_n_outer = 1;
+        p.bias = nullptr; p.bias_stride = 0; p.bias_axis = MT_BIAS_NONE;
+        p.beta = beta;
+        p.M = (int)d->c_out; p.N = (int)kg; p.K = (int)np; p.batch = 1;
+        ConvGeom& g = p.cv;
+        g.img_stride = d->h * d->w * d->c_in;
+        g.c = (int)d->c_in; g.h = (int)d->h; g.w = (int)d->w;
+        g.kh = (int)d->kh; g.kw = (int)d->kw; g.stride = (int)d->stride; g.pad = (int)d->pad;
+        g.ho = (int)Ho; g.wo = (int)Wo;
+        return launch_gemm(p, true, L_KV, L_IMW, wsp + xt_b + dyt_b, ws_bytes - xt_b - dyt_b, s);
     }
+    if (np > 0 && (!workspace || ws_bytes < col_b + dyt_b)) return MT_ERR_WORKSPACE;
     float* col = static_cast<float*>(workspace);
     float* dyt = reinterpret_cast<float*>(static_cast<char*>(workspace) + col_b);
     if (np > 0) {

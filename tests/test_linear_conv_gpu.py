@@ -333,3 +333,33 @@ def test_conv_backward_input_implicit(dev, n, c, h, wd, co, k, pad):
     assert "im2col" in cfg, cfg
     wdx, _, _ = oracle.conv2d_backward(x, w, dy, 1, pad)
     assert_close(sync_np(dx), wdx, co * k * k, amax(dy), amax(w), "implicit conv dX")
+
+
+# ---- implicit dW: weight gradient without a column buffer ---------------------
+# dW[c_out, (r,s,ci)] = dYt · im2colᵀ(x) with the B operand gathered from a
+# channels-last copy of x (c_in % 4 == 0, n*h_out*w_out % 4 == 0) and the
+# columns scattered to OIHW by the epilogue.
+
+@pytest.mark.parametrize("n,c,h,wd,co,kh,kw,stride,pad", [
+    (2, 16, 9, 8, 6, 3, 3, 1, 1),
+    (4, 8, 11, 10, 6, 3, 2, 2, 2),    # stride 2, 3x2 kernel, np = 196 (K tail 4)
+    (1, 4, 8, 8, 5, 5, 5, 1, 2),
+    (2, 12, 5, 6, 4, 1, 1, 1, 0),     # 1x1, np = 60 (K tail 12)
+    (2, 64, 14, 14, 32, 3, 3, 1, 1),  # deep K (np = 392): split-K
+])
+def test_conv_backward_weight_implicit(dev, n, c, h, wd, co, kh, kw, stride, pad):
+    x = oracle.normal((n, c, h, wd), 61)
+    w = oracle.normal((co, c, kh, kw), 62)
+    ho, wo = oracle.conv_out(h, pad, kh, stride), oracle.conv_out(wd, pad, kw, stride)
+    dy = oracle.normal((n, co, ho, wo), 63)
+    X, W, dY = g(x, dev), g(w, dev), g(dy, dev)
+    _, dw, _ = mt.conv2d_backward(X, W, dY, stride, pad, need_dx=False, need_db=False)
+    cfg = mt.last_config()
+    print(f"[config] dW {cfg}")
+    assert "im2colT" in cfg, cfg
+    _, wdw, _ = oracle.conv2d_backward(x, w, dy, stride, pad)
+    assert_close(sync_np(dw), wdw, n * ho * wo, amax(dy), amax(x), "implicit conv dW")
+    # gradient accumulation: dW += ∂L/∂W through the epilogue's beta
+    mt.conv2d_backward(X, W, dY, stride, pad, need_dx=False, need_db=False, dw=dw, beta_w=1.0)
+    assert_close(sync_np(dw), 2 * wdw, n * ho * wo, amax(dy), amax(x), "implicit conv dW += ",
+                 extra=1e-6)
