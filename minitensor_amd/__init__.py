@@ -360,6 +360,16 @@ def conv2d_backward(x: torch.Tensor, w: torch.Tensor, dy: torch.Tensor, stride: 
     return dx, dw, db
 
 
+def axpby(x: torch.Tensor, y: torch.Tensor, alpha: float = 1.0, beta: float = 0.0,
+          stream=None) -> torch.Tensor:
+    """y = alpha·x + beta·y in place over 2-D/3-D views (x may have batch 1:
+    broadcast).  The strided copy / accumulate kernel of the host layer."""
+    _require_gpu(x, y)
+    rc = lib().mt_axpby_f32(mat(x), float(alpha), mat(y), float(beta), _stream(stream))
+    _check(rc, "mt_axpby_f32")
+    return y
+
+
 def last_config() -> str:
     return lib().mt_last_config().decode()
 

@@ -266,9 +266,10 @@ __global__ void __launch_bounds__(256) splitk_reduce_f32(GemmParams p) {
     }
 }
 
-// Vector form (ws_vec and c_vec: N % 4 == 0, 16-byte runs on both sides):
-// blockIdx.y walks output rows (batch-major), threads walk 4-column groups.
-// Same per-element summation order as the scalar form.
+// Vector form (ws_vec: N % 4 == 0, 16-byte partials): blockIdx.y walks output
+// rows (batch-major), threads walk 4-column groups; the group is stored as one
+// 16-byte vector when C allows (c_vec), else element by element through
+// col(n).  Same per-element summation order as the scalar form.
 __global__ void __launch_bounds__(256) splitk_reduce_vec_f32(GemmParams p) {
     const int64_t MN = (int64_t)p.M * p.N;
     const int64_t rows = (int64_t)p.M * p.batch;
@@ -286,9 +287,16 @@ __global__ void __launch_bounds__(256) splitk_reduce_vec_f32(GemmParams p) {
             v += brow;
             if (p.bias_axis == 2)
                 for (int e = 0; e < 4; ++e) v[e] += p.bias[(int64_t)(n + e) * p.bias_stride];
-            f32x4* dst = reinterpret_cast<f32x4*>(crow + col_offset(p, n));
-            if (p.beta != 0.f) v += p.beta * *dst;
-            *dst = v;
+            if (p.c_vec) {
+                f32x4* dst = reinterpret_cast<f32x4*>(crow + col_offset(p, n));
+                if (p.beta != 0.f) v += p.beta * *dst;
+                *dst = v;
+            } else {
+                for (int e = 0; e < 4; ++e) {
+                    float* dst = crow + col_offset(p, n + e);
+                    *dst = (p.beta != 0.f ? p.beta * *dst : 0.f) + v[e];
+                }
+            }
         }
     }
 }
@@ -334,7 +342,7 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
     if (e == hipErrorStreamCaptureUnsupported) e = hipSuccess;
     if (e != hipSuccess) return MT_ERR_HIP;
     if (plan.splits > 1) {
-        if (p.ws_vec && p.c_vec) {
+        if (p.ws_vec) {
             const dim3 grid((unsigned)std::min<int64_t>((N / 4 + 255) / 256, 64),
                             (unsigned)std::min<int64_t>(M * batch, 65535));
             hipLaunchKernelGGL(splitk_reduce_vec_f32, grid, dim3(256), 0, stream, p);
@@ -509,21 +517,50 @@ __global__ void __launch_bounds__(256) fill_f32(float* p, int64_t n, float v) {
         p[i] = v;
 }
 
-// Y = alpha*X + beta*Y over (batch, rows, cols) views; grid-stride over the
-// elements in row-major (batch, row, col) order.
+// Y = alpha*X + beta*Y over (batch, rows, cols) views.  blockIdx.y walks the
+// batch*rows rows, threads walk a row's columns: four at a time (16-byte
+// loads and stores) when vec says both rows are unit-stride and aligned.
 __global__ void __launch_bounds__(256)
 axpby_f32(const float* X, int64_t xb, int64_t xr, int64_t xc, float alpha, float* Y, int64_t yb,
-          int64_t yr, int64_t yc, float beta, int64_t rows, int64_t cols, int64_t total) {
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
-         e += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t rc = rows * cols;
-        const int64_t b = e / rc;
-        const int64_t rem = e - b * rc;
-        const int64_t r = rem / cols, c = rem - r * cols;
-        float* y = Y + b * yb + r * yr + c * yc;
-        const float v = alpha * X[b * xb + r * xr + c * xc];
-        *y = beta != 0.f ? v + beta * *y : v;
+          int64_t yr, int64_t yc, float beta, int64_t rows, int64_t cols, int64_t nrows,
+          int vec) {
+    for (int64_t row = blockIdx.y; row < nrows; row += gridDim.y) {
+        const int64_t b = row / rows, r = row - b * rows;
+        const float* x = X + b * xb + r * xr;
+        float* y = Y + b * yb + r * yr;
+        if (vec) {
+            for (int64_t c = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4; c < cols;
+                 c += (int64_t)gridDim.x * blockDim.x * 4) {
+                f32x4 v = alpha * *reinterpret_cast<const f32x4*>(x + c);
+                f32x4* d = reinterpret_cast<f32x4*>(y + c);
+                if (beta != 0.f) v += beta * *d;
+                *d = v;
+            }
+        } else {
+            for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < cols;
+                 c += (int64_t)gridDim.x * blockDim.x) {
+                const float v = alpha * x[c * xc];
+                float* d = y + c * yc;
+                *d = beta != 0.f ? v + beta * *d : v;
+            }
+        }
     }
+}
+
+hipError_t launch_axpby(const float* X, int64_t xb, int64_t xr, int64_t xc, float alpha,
+                        float* Y, int64_t yb, int64_t yr, int64_t yc, float beta, int64_t batch,
+                        int64_t rows, int64_t cols, hipStream_t s) {
+    const int64_t nrows = batch * rows;
+    if (nrows == 0 || cols == 0) return hipSuccess;
+    const bool vec = xc == 1 && yc == 1 && (cols & 3) == 0 && (xr & 3) == 0 && (yr & 3) == 0 &&
+                     (batch == 1 || ((xb & 3) == 0 && (yb & 3) == 0)) &&
+                     ((uintptr_t)X & 15u) == 0 && ((uintptr_t)Y & 15u) == 0;
+    const int64_t per_row = vec ? cols / 4 : cols;
+    dim3 grid((unsigned)std::min<int64_t>((per_row + 255) / 256, 64),
+              (unsigned)std::min<int64_t>(nrows, 65535));
+    hipLaunchKernelGGL(axpby_f32, grid, dim3(256), 0, s, X, xb, xr, xc, alpha, Y, yb, yr, yc,
+                       beta, rows, cols, nrows, vec ? 1 : 0);
+    return capture_safe_last_error();
 }
 
 unsigned grid_for(int64_t total) {
@@ -564,19 +601,33 @@ col2im_gather_f32(const float* dcol, float* dx, int C, int H, int W, int kh, int
 }
 
 // db[c] = beta*db[c] + Σ_{img, hw} dY[img][c][hw]; one workgroup per channel,
-// fixed-order tree reduction.
+// each thread summing a fixed set of positions (16-byte loads when HW % 4 == 0
+// and dY is aligned), then a fixed-order tree reduction: deterministic.
 __global__ void __launch_bounds__(256)
 conv_bias_grad_f32(const float* dy, float* db, int N, int C, int64_t HW, float beta) {
     __shared__ float red[256];
     const int c = blockIdx.x;
     const int t = threadIdx.x;
-    float s = 0.f;
-    const int64_t total = (int64_t)N * HW;
-    for (int64_t i = t; i < total; i += 256) {
-        const int64_t img = i / HW, hw = i - img * HW;
-        s += dy[(img * C + c) * HW + hw];
+    const bool vec = (HW & 3) == 0 && ((uintptr_t)dy & 15u) == 0;
+    const int64_t per_img = vec ? HW / 4 : HW;       // items per image
+    const int64_t total = (int64_t)N * per_img;
+    float s[4] = {0.f, 0.f, 0.f, 0.f};               // 4 independent loads in flight
+    for (int64_t i0 = t; i0 < total; i0 += 4 * 256) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t i = i0 + u * 256;
+            if (i >= total) break;
+            const int64_t img = i / per_img, j = i - img * per_img;
+            const float* p = dy + ((int64_t)img * C + c) * HW;
+            if (vec) {
+                const f32x4 v = *reinterpret_cast<const f32x4*>(p + 4 * j);
+                s[u] += (v[0] + v[1]) + (v[2] + v[3]);
+            } else {
+                s[u] += p[j];
+            }
+        }
     }
-    red[t] = s;
+    red[t] = (s[0] + s[1]) + (s[2] + s[3]);
     __syncthreads();
     for (int w = 128; w > 0; w >>= 1) {
         if (t < w) red[t] += red[t + w];
@@ -585,14 +636,12 @@ conv_bias_grad_f32(const float* dy, float* db, int N, int C, int64_t HW, float b
     if (t == 0) db[c] = (beta != 0.f ? beta * db[c] : 0.f) + red[0];
 }
 
-// dY [n][c_out][hw] -> dYt [c_out][n][hw] (contiguous), through the axpby kernel.
+// dY [n][c_out][hw] -> dYt [c_out][n][hw] (contiguous), through the axpby kernel
+// (batch = channel, rows = images, cols = positions).
 hipError_t transpose_dy(const mt_conv2d_desc* d, int64_t hw, const float* dy, float* dyt,
                         hipStream_t s) {
-    const int64_t total = d->c_out * d->n * hw;
-    hipLaunchKernelGGL(axpby_f32, dim3(grid_for(total)), dim3(256), 0, s, dy, hw,
-                       d->c_out * hw, (int64_t)1, 1.0f, dyt, d->n * hw, hw, (int64_t)1, 0.0f,
-                       d->n, hw, total);
-    return capture_safe_last_error();
+    return launch_axpby(dy, hw, d->c_out * hw, 1, 1.0f, dyt, d->n * hw, hw, 1, 0.0f, d->c_out,
+                        d->n, hw, s);
 }
 
 // out[b][j][i] = in[b*sb + i*si + (j / jw)*sj1 + (j % jw)*sj0], out dense
@@ -1021,12 +1070,12 @@ int mt_axpby_f32(const mt_mat_f32* X, float alpha, const mt_mat_f32* Y, float be
     if ((Y->rows > 1 && Y->row_stride == 0) || (Y->cols > 1 && Y->col_stride == 0) ||
         (Y->batch > 1 && Y->batch_stride == 0))
         return MT_ERR_INVALID;
-    hipLaunchKernelGGL(axpby_f32, dim3(grid_for(total)), dim3(256), 0,
-                       static_cast<hipStream_t>(stream), X->base + X->offset,
-                       X->batch == 1 ? 0 : X->batch_stride, X->row_stride, X->col_stride, alpha,
-                       const_cast<float*>(Y->base) + Y->offset, Y->batch_stride, Y->row_stride,
-                       Y->col_stride, beta, Y->rows, Y->cols, total);
-    return capture_safe_last_error() == hipSuccess ? MT_OK : MT_ERR_HIP;
+    const hipError_t e =
+        launch_axpby(X->base + X->offset, X->batch == 1 ? 0 : X->batch_stride, X->row_stride,
+                     X->col_stride, alpha, const_cast<float*>(Y->base) + Y->offset,
+                     Y->batch_stride, Y->row_stride, Y->col_stride, beta, Y->batch, Y->rows,
+                     Y->cols, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? MT_OK : MT_ERR_HIP;
 }
 
 const char* mt_strerror(int status) {
