@@ -6,6 +6,12 @@
 // the tensor's device; host blocks are 64-byte aligned heap memory (so CPU
 // tensors work on machines without a GPU).  Split-K partials and im2col
 // buffers are taken from here, so once warm no GEMM call allocates.
+//
+// Reservation (graph capture): blocks handed out while a Reservation is active
+// on the calling thread are not recycled when freed; they go back to the cache
+// only when the Reservation is destroyed.  A captured HIP graph keeps using
+// the addresses it recorded, so those blocks must not be given to other
+// tensors while the graph can still be replayed.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -14,6 +20,7 @@
 #include <mutex>
 #include <new>
 #include <unordered_map>
+#include <utility>
 #include <vector>
 
 #include "Defines.hpp"
@@ -26,40 +33,60 @@ public:
         return pool;
     }
 
+    class Reservation {
+    public:
+        Reservation() = default;
+        ~Reservation() { MemoryPool::get().end_reservation(*this); }
+        Reservation(const Reservation&) = delete;
+        Reservation& operator=(const Reservation&) = delete;
+        void start() { active() = this; }
+        void stop() {
+            if (active() == this) active() = nullptr;
+        }
+        size_t blocks() const { return blocks_.size(); }
+        size_t fresh_allocations() const { return fresh_; }  // blocks that needed a new malloc
+
+    private:
+        friend class MemoryPool;
+        static Reservation*& active() {
+            thread_local Reservation* r = nullptr;
+            return r;
+        }
+        std::vector<void*> blocks_;
+        size_t fresh_ = 0;
+    };
+
     void* allocate(size_t bytes, Device device) {
         if (bytes == 0) return nullptr;
         const size_t b = bin(bytes);
+        Reservation* r = Reservation::active();
         {
             std::lock_guard<std::mutex> lk(mu_);
             auto& fl = cache(device)[b];
             if (!fl.empty()) {
                 void* p = fl.back();
                 fl.pop_back();
+                if (r) reserve_locked(r, p, b, device);
                 return p;
             }
         }
-        if (device.is_gpu()) {
-            int prev = 0;
-            GPU_CHECK(hipGetDevice(&prev));
-            if (prev != device.index) GPU_CHECK(hipSetDevice(device.index));
-            void* p = nullptr;
-            hipError_t e = hipMalloc(&p, b);
-            if (e != hipSuccess) {  // release cached blocks once and retry
-                release(device);
-                e = hipMalloc(&p, b);
-            }
-            if (prev != device.index) (void)hipSetDevice(prev);
-            if (e != hipSuccess) mt_detail::hip_fail(e, __FILE__, __LINE__);
-            return p;
+        if (r) ++r->fresh_;
+        void* p = fresh(b, device);
+        if (r) {
+            std::lock_guard<std::mutex> lk(mu_);
+            reserve_locked(r, p, b, device);
         }
-        void* p = std::aligned_alloc(64, b);
-        if (!p) throw std::bad_alloc();
         return p;
     }
 
     void free(void* p, size_t bytes, Device device) {
         if (!p || bytes == 0) return;
         std::lock_guard<std::mutex> lk(mu_);
+        auto it = reserved_.find(p);
+        if (it != reserved_.end()) {  // held for a captured graph: recycled later
+            it->second.freed = true;
+            return;
+        }
         cache(device)[bin(bytes)].push_back(p);
     }
 
@@ -83,6 +110,49 @@ public:
     }
 
 private:
+    struct Held {
+        size_t bin;
+        Device device;
+        bool freed;
+    };
+
+    void reserve_locked(Reservation* r, void* p, size_t b, Device device) {
+        r->blocks_.push_back(p);
+        reserved_[p] = Held{b, device, false};
+    }
+
+    void end_reservation(Reservation& r) {
+        r.stop();
+        std::lock_guard<std::mutex> lk(mu_);
+        for (void* p : r.blocks_) {
+            auto it = reserved_.find(p);
+            if (it == reserved_.end()) continue;
+            if (it->second.freed) cache(it->second.device)[it->second.bin].push_back(p);
+            reserved_.erase(it);   // still owned by a live tensor: its free() caches it
+        }
+        r.blocks_.clear();
+    }
+
+    void* fresh(size_t b, Device device) {
+        if (device.is_gpu()) {
+            int prev = 0;
+            GPU_CHECK(hipGetDevice(&prev));
+            if (prev != device.index) GPU_CHECK(hipSetDevice(device.index));
+            void* p = nullptr;
+            hipError_t e = hipMalloc(&p, b);
+            if (e != hipSuccess) {  // release cached blocks once and retry
+                release(device);
+                e = hipMalloc(&p, b);
+            }
+            if (prev != device.index) (void)hipSetDevice(prev);
+            if (e != hipSuccess) mt_detail::hip_fail(e, __FILE__, __LINE__);
+            return p;
+        }
+        void* p = std::aligned_alloc(64, b);
+        if (!p) throw std::bad_alloc();
+        return p;
+    }
+
     static constexpr int kMaxGpus = 16;
     using Bins = std::unordered_map<size_t, std::vector<void*>>;
 
@@ -113,4 +183,5 @@ private:
     std::mutex mu_;
     Bins host_;
     Bins gpu_[kMaxGpus];
+    std::unordered_map<void*, Held> reserved_;   // blocks of live Reservations
 };

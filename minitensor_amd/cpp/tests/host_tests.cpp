@@ -16,6 +16,7 @@
 #include <vector>
 
 #include "minitensor/minitensor.hpp"
+#include "minitensor/GraphExecutor.hpp"
 
 namespace {
 
@@ -436,6 +437,90 @@ TEST_GPU(gpu_conv_strided_input_views) {
     CHECK(!xt.is_contiguous());
     Tensor<float> want3 = conv2d(t.transpose(1, 2).contiguous(), w3, b4, 2, 1);
     check_close(conv2d(xt, w3.to(GPU), b4.to(GPU), 2, 1), want3, 27, 1, 1, 1e-5);
+}
+
+void check_equal(const Tensor<float>& a, const Tensor<float>& b, const char* what) {
+    Tensor<float> ha = host(a), hb = host(b);
+    CHECK(ha.shape() == hb.shape());
+    if (std::memcmp(ha.data(), hb.data(), ha.total_elements() * sizeof(float)) != 0) {
+        std::printf("    %s differs\n", what);
+        CHECK(false);
+    }
+}
+
+TEST_GPU(gpu_graph_executor_training_loop) {
+    // A Linear layer trained with SGD on L = ½‖x·W + b - y‖² through GraphExecutor
+    // (eager warm-up, capture, replays; reference include/GraphExecutor.hpp:22-220),
+    // next to a copy trained by the same steps run eagerly: every weight, bias and
+    // loss gradient must be bit-identical, and the capture must allocate nothing.
+    const float lr = 0.05f;
+    Linear<float> a(64, 32, GPU), b(64, 32, GPU);
+    copy_gpu_strided(a.weight_, b.weight_);
+    copy_gpu_strided(a.bias_, b.bias_);
+    for (Linear<float>* m : {&a, &b}) {
+        m->weight_.grad() = Tensor<float>(m->weight_.shape(), GPU);
+        m->bias_.grad() = Tensor<float>(m->bias_.shape(), GPU);
+    }
+    auto make_step = [lr](Linear<float>& m) {
+        return [&m, lr](const Tensor<float>& x, const Tensor<float>& y) {
+            m.weight_.grad().fill(0.f);
+            m.bias_.grad().fill(0.f);
+            Tensor<float> yh = m.forward(x);                 // one GEMM, bias fused
+            Tensor<float> d(yh.shape(), yh.device());
+            copy_gpu_strided(yh, d);
+            mt_detail::axpby(y, -1.f, d, 1.f);               // dL/dyh = yh - y
+            yh.grad() = d;
+            yh.backward();                                    // dX-free: dW GEMM (+ db)
+            mt_detail::axpby(m.weight_.grad(), -lr, m.weight_, 1.f);
+            mt_detail::axpby(m.bias_.grad(), -lr, m.bias_, 1.f);
+            return d;
+        };
+    };
+    GraphExecutor<float> ex(make_step(a));
+    auto eager = make_step(b);
+    for (int it = 0; it < 5; ++it) {
+        Tensor<float> x = uniform({128, 64}, 100 + it).to(GPU);
+        Tensor<float> y = uniform({128, 32}, 200 + it).to(GPU);
+        Tensor<float> d1 = ex.step(x, y);
+        Tensor<float> d2 = eager(x, y);
+        GPU_CHECK(hipDeviceSynchronize());
+        check_equal(d1, d2, "loss gradient");
+        check_equal(a.weight_, b.weight_, "weight");
+        check_equal(a.bias_, b.bias_, "bias");
+    }
+    CHECK(ex.captured());
+    CHECK(ex.capture_allocations() == 0);
+    // a batch of another shape runs eagerly and still trains the same way
+    Tensor<float> x = uniform({96, 64}, 300).to(GPU), y = uniform({96, 32}, 301).to(GPU);
+    ex.step(x, y);
+    eager(x, y);
+    GPU_CHECK(hipDeviceSynchronize());
+    check_equal(a.weight_, b.weight_, "weight after an eager step");
+}
+
+TEST_CPU(cpu_pool_reservation) {
+    // Blocks handed out under a Reservation are not recycled until it ends.
+    MemoryPool& pool = MemoryPool::get();
+    void* p0 = pool.allocate(1000, CPU);
+    pool.free(p0, 1000, CPU);                     // cached
+    void* held = nullptr;
+    {
+        MemoryPool::Reservation r;
+        r.start();
+        held = pool.allocate(1000, CPU);          // reuses the cached block
+        r.stop();
+        CHECK(held == p0);
+        CHECK(r.fresh_allocations() == 0);
+        pool.free(held, 1000, CPU);               // held back for the reservation
+        void* other = pool.allocate(1000, CPU);   // must not get the held block
+        CHECK(other != held);
+        pool.free(other, 1000, CPU);
+    }
+    void* again = pool.allocate(1000, CPU);       // the held block is back in the cache
+    void* again2 = pool.allocate(1000, CPU);
+    CHECK(again == held || again2 == held);
+    pool.free(again, 1000, CPU);
+    pool.free(again2, 1000, CPU);
 }
 
 TEST_GPU(gpu_contiguous_and_dispatch) {
