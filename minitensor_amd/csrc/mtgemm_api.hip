@@ -517,34 +517,47 @@ __global__ void __launch_bounds__(256) fill_f32(float* p, int64_t n, float v) {
         p[i] = v;
 }
 
-// Y = alpha*X + beta*Y over (batch, rows, cols) views.  blockIdx.y walks the
-// batch*rows rows, threads walk a row's columns: four at a time (16-byte
-// loads and stores) when vec says both rows are unit-stride and aligned.
-__global__ void __launch_bounds__(256)
-axpby_f32(const float* X, int64_t xb, int64_t xr, int64_t xc, float alpha, float* Y, int64_t yb,
-          int64_t yr, int64_t yc, float beta, int64_t rows, int64_t cols, int64_t nrows,
-          int vec) {
-    for (int64_t row = blockIdx.y; row < nrows; row += gridDim.y) {
-        const int64_t b = row / rows, r = row - b * rows;
+// Y = alpha*X + beta*Y over (batch, rows, cols) views.  Grid-stride over
+// items of one row: four columns (16-byte loads and stores) when vec says both
+// rows are unit-stride and aligned, else one column.  Index math is 32-bit
+// when the item count allows (I = int or int64_t).
+template <typename I>
+__device__ __forceinline__ void axpby_items(const float* X, int64_t xb, int64_t xr, int64_t xc,
+                                            float alpha, float* Y, int64_t yb, int64_t yr,
+                                            int64_t yc, float beta, I rows, I per_row, I total,
+                                            bool vec) {
+    for (I i = (I)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (I)gridDim.x * blockDim.x) {
+        const I row = i / per_row, c = i - row * per_row;
+        const I b = row / rows, r = row - b * rows;
         const float* x = X + b * xb + r * xr;
         float* y = Y + b * yb + r * yr;
         if (vec) {
-            for (int64_t c = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4; c < cols;
-                 c += (int64_t)gridDim.x * blockDim.x * 4) {
-                f32x4 v = alpha * *reinterpret_cast<const f32x4*>(x + c);
-                f32x4* d = reinterpret_cast<f32x4*>(y + c);
-                if (beta != 0.f) v += beta * *d;
-                *d = v;
-            }
+            f32x4 v = alpha * *reinterpret_cast<const f32x4*>(x + 4 * (int64_t)c);
+            f32x4* d = reinterpret_cast<f32x4*>(y + 4 * (int64_t)c);
+            if (beta != 0.f) v += beta * *d;
+            *d = v;
         } else {
-            for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < cols;
-                 c += (int64_t)gridDim.x * blockDim.x) {
-                const float v = alpha * x[c * xc];
-                float* d = y + c * yc;
-                *d = beta != 0.f ? v + beta * *d : v;
-            }
+            const float v = alpha * x[c * xc];
+            float* d = y + c * yc;
+            *d = beta != 0.f ? v + beta * *d : v;
         }
     }
+}
+
+__global__ void __launch_bounds__(256)
+axpby_f32(const float* X, int64_t xb, int64_t xr, int64_t xc, float alpha, float* Y, int64_t yb,
+          int64_t yr, int64_t yc, float beta, int64_t rows, int64_t per_row, int64_t total,
+          int vec) {
+    if (total < ((int64_t)1 << 31))
+        axpby_items<int>(X, xb, xr, xc, alpha, Y, yb, yr, yc, beta, (int)rows, (int)per_row,
+                         (int)total, vec != 0);
+    else
+        axpby_items<int64_t>(X, xb, xr, xc, alpha, Y, yb, yr, yc, beta, rows, per_row, total,
+                             vec != 0);
+}
+
+unsigned grid_for(int64_t total) {
+    return (unsigned)std::max<int64_t>(1, std::min<int64_t>((total + 255) / 256, 8192));
 }
 
 hipError_t launch_axpby(const float* X, int64_t xb, int64_t xr, int64_t xc, float alpha,
@@ -556,16 +569,12 @@ hipError_t launch_axpby(const float* X, int64_t xb, int64_t xr, int64_t xc, floa
                      (batch == 1 || ((xb & 3) == 0 && (yb & 3) == 0)) &&
                      ((uintptr_t)X & 15u) == 0 && ((uintptr_t)Y & 15u) == 0;
     const int64_t per_row = vec ? cols / 4 : cols;
-    dim3 grid((unsigned)std::min<int64_t>((per_row + 255) / 256, 64),
-              (unsigned)std::min<int64_t>(nrows, 65535));
-    hipLaunchKernelGGL(axpby_f32, grid, dim3(256), 0, s, X, xb, xr, xc, alpha, Y, yb, yr, yc,
-                       beta, rows, cols, nrows, vec ? 1 : 0);
+    const int64_t total = nrows * per_row;
+    hipLaunchKernelGGL(axpby_f32, dim3(grid_for(total)), dim3(256), 0, s, X, xb, xr, xc, alpha,
+                       Y, yb, yr, yc, beta, rows, per_row, total, vec ? 1 : 0);
     return capture_safe_last_error();
 }
 
-unsigned grid_for(int64_t total) {
-    return (unsigned)std::max<int64_t>(1, std::min<int64_t>((total + 255) / 256, 8192));
-}
 
 // dX[img][c][y][x] = Σ_{r,s} dcol[(c*kh + r)*kw + s][(img*Ho + oh)*Wo + ow] over the
 // (r, s) whose window position (oh, ow) covers (y, x): a gather, so every input
