@@ -2,13 +2,13 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-secondary] [--no-cpu]
 
-Headline: one step = one C[4096,4096] = A·B fp32 GEMM,
+Headline (benchmark config 2): one step = one C[4096,4096] = A·B fp32 GEMM,
 A,B ~ U(-1,1), all operands resident in HBM.  `value` is TFLOPS =
 2·4096³ / (mean step time), timed with HIP events on the launch stream over
 exactly K steps bracketed by device synchronisation.  The GEMM is a single
 kernel launch per step, so the roofline figure uses the same events.
 
-Secondary lines (the other BASELINE configs: ms and TFLOPS, and HBM GB/s for
+Secondary lines (the other benchmark configs: ms and TFLOPS, and HBM GB/s for
 the batched one) are reported under "secondary".  Their kernels take 10-100
 us, less than a Python/ctypes call, so `ms` is device time: 20 calls are
 captured into a HIP graph and the graph is replayed between HIP events.
@@ -102,7 +102,7 @@ SECONDARY = ("c1", "c3", "c4", "c5a", "c5b")
 
 
 def secondary(dev, only=SECONDARY) -> dict:
-    """BASELINE configs 1, 3, 4, 5 (ms, TFLOPS; GB/s for the HBM-near batched one)."""
+    """benchmark configs 1, 3, 4, 5 (ms, TFLOPS; GB/s for the HBM-near batched one)."""
     import ctypes
     import torch
     import minitensor_amd as mt
@@ -255,7 +255,7 @@ def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(GEMM shards with no exchange; see DESIGN.md). Run with --gpus 1.",
+              "(a GEMM shards by row or column blocks with no exchange). Run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
 
@@ -329,7 +329,7 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (U(-1,1), torch generator seed 42, resident in HBM)",
-        "config": {"workload": "BASELINE config 2: C[4096,4096] = A[4096,4096]·B[4096,4096] "
+        "config": {"workload": "benchmark config 2: C[4096,4096] = A[4096,4096]·B[4096,4096] "
                                "fp32 row-major GEMM", "M": M, "N": N, "K": K,
                    "kernel": kernel_cfg, "wall_s_timed_region": round(wall, 4)},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": PEAK_TFLOPS,

@@ -364,7 +364,7 @@ TEST_GPU(gpu_bmm_forward_backward) {
 }
 
 TEST_GPU(gpu_linear_config4_equivalence) {
-    // BASELINE config 4 shape through the Linear module (W_ref [2048,1000]) and F::linear.
+    // benchmark config 4 shape through the Linear module (W_ref [2048,1000]) and F::linear.
     Linear<float> lin(2048, 1000);
     Tensor<float> x = uniform({256, 2048}, 42), dy = uniform({256, 1000}, 44, -0.01f, 0.01f);
     Linear<float> lg = lin;  // same parameters, moved to the GPU below

@@ -40,7 +40,7 @@ def test_fill_2_and_3(dev):
 
 
 def test_config1_mlp_linear_shape(dev):
-    # C[256,512] = A[256,512]·B[512,512], U(-1,1), seeds 42/43
+    # benchmark config 1: C[256,512] = A[256,512]·B[512,512], U(-1,1), seeds 42/43
     a = oracle.uniform((256, 512), 42)
     b = oracle.uniform((512, 512), 43)
     c = run(to_gpu(a, dev), to_gpu(b, dev))
@@ -174,7 +174,7 @@ def test_split_k_is_deterministic(dev):
 
 
 def test_batched_config5b(dev):
-    # BASELINE config 5b: [64]x[512,64]·[64,512], U(-1,1) seeds 42/43; one launch
+    # benchmark config 5b: [64]x[512,64]·[64,512], U(-1,1) seeds 42/43; one launch
     a = oracle.uniform((64, 512, 64), 42)
     b = oracle.uniform((64, 64, 512), 43)
     c = mt.bmm(to_gpu(a, dev), to_gpu(b, dev))
@@ -194,7 +194,7 @@ def test_batched_shared_weight(dev):
 
 
 def test_config2_4096_properties(dev):
-    # BASELINE config 2 (4096^3): the full oracle would take minutes, so check
+    # benchmark config 2 (4096^3): the full oracle would take minutes, so check
     # (1) 24 sampled rows against the oracle's fp64 brute force over the full K,
     # (2) the checksum identity C·1 = A·(B·1) in fp64 over all rows.
     a = oracle.uniform((4096, 4096), 42)
@@ -215,7 +215,7 @@ def test_config2_4096_properties(dev):
 
 
 def test_config3_transpose_and_slice_views(dev):
-    # C = A·Bᵀ with B [2048,1024] passed as a transpose view,
+    # benchmark config 3: C = A·Bᵀ with B [2048,1024] passed as a transpose view,
     # and the slice A[128:] (offset 131072); N(0,1) seeds 42/43.  Sampled rows
     # against the oracle (full K).
     a = oracle.normal((2048, 1024), 42)
@@ -361,3 +361,46 @@ def test_split_k_vector_reduce_bias_beta(dev, axis):
     want = oracle.matmul(a, b) + c0 + (bias[:, None] if axis == mt.BIAS_ROW else bias[None, :])
     assert_close(C.cpu().numpy(), want, K, amax(a), amax(b), f"split-K bias {axis} + beta",
                  extra=1e-6)
+
+
+# ---- maximum sizes: outputs past 2^31 elements (64-bit addressing) ---------------
+
+@pytest.mark.parametrize("path", ["dl", "rs"])
+def test_output_beyond_2pow31_elements(dev, path):
+    # C[40000, 60000] = 2.4e9 elements (9.6 GB): rows past 35791 start beyond
+    # 2^31, so any 32-bit element index in a kernel or epilogue would alias.
+    M, N, K = 40000, 60000, 32
+    a = oracle.uniform((M, K), 91)
+    b = oracle.uniform((K, N), 92)
+    A = to_gpu(a, dev)
+    if path == "rs":    # unaligned view of A: the register-staged kernel
+        buf = torch.empty(M * K + 1, device=dev)
+        buf[1:].copy_(A.reshape(-1))
+        A = buf[1:].view(M, K)
+    C = mt.gemm(A, to_gpu(b, dev))
+    torch.cuda.synchronize()
+    cfg = mt.last_config()
+    print(f"[config] {cfg}", flush=True)
+    assert cfg.startswith(path + " "), cfg
+    rows = np.array([0, 1, 35790, 35791, 35792, 39998, 39999], np.int64)
+    got = C[torch.from_numpy(rows).to(dev)].cpu().numpy()
+    assert_close(got, oracle.matmul(a[rows], b), K, amax(a), amax(b), f"{path} rows past 2^31")
+    del C, A
+    torch.cuda.empty_cache()
+
+
+def test_batched_output_beyond_2pow31_elements(dev):
+    # 3 x [32768, 32768]: batch 2 starts at element 2^31 of C.
+    Bt, M, N, K = 3, 32768, 32768, 16
+    a = oracle.uniform((Bt, M, K), 93)
+    b = oracle.uniform((Bt, K, N), 94)
+    C = mt.gemm(to_gpu(a, dev), to_gpu(b, dev))
+    torch.cuda.synchronize()
+    print(f"[config] {mt.last_config()}", flush=True)
+    for bz in (0, 2):
+        rows = np.array([0, 17, M - 1], np.int64)
+        got = C[bz, torch.from_numpy(rows).to(dev)].cpu().numpy()
+        assert_close(got, oracle.matmul(a[bz][rows], b[bz]), K, amax(a), amax(b),
+                     f"batch {bz} rows")
+    del C
+    torch.cuda.empty_cache()

@@ -24,7 +24,7 @@ def sync_np(t):
 
 
 def test_config4_linear_forward_backward(dev):
-    # BASELINE config 4 (ResNet50-fc): X[256,2048] ~ N(0,1), W[1000,2048] He-init,
+    # benchmark config 4 (ResNet50-fc): X[256,2048] ~ N(0,1), W[1000,2048] He-init,
     # b = 0, dY[256,1000] ~ N(0, 0.01); Y = X·Wᵀ + b, dX = dY·W, dW = dYᵀ·X, db = Σ dY.
     x = oracle.normal((256, 2048), 42)
     w = oracle.normal((1000, 2048), 43, std=(2.0 / 2048) ** 0.5)
@@ -146,7 +146,7 @@ def test_conv_shapes(dev, n, c, h, wd, co, kh, kw, stride, pad):
 
 
 def test_config5a_conv(dev):
-    # BASELINE config 5a: N=32, C=256, 14x14 -> 256, 3x3 s1 p1 (GEMM M=6272, K=2304, N=256).
+    # benchmark config 5a: N=32, C=256, 14x14 -> 256, 3x3 s1 p1 (GEMM M=6272, K=2304, N=256).
     # 16 sampled output channels against the oracle's direct conv, plus the
     # channel-sum identity Σ_co out = conv(x, Σ_co w) + Σ b over every position.
     x = oracle.normal((32, 256, 14, 14), 42)
@@ -186,7 +186,7 @@ def test_conv_backward_shapes(dev, n, c, h, wd, co, kh, kw, stride, pad):
 
 
 def test_config5a_conv_backward_adjoint(dev):
-    # BASELINE config 5a shape: dX and dW through the GEMM path, checked by the
+    # benchmark config 5a shape: dX and dW through the GEMM path, checked by the
     # size-independent adjoint identities <dY, conv(x,w)> = <dX, x> = <dW, w>
     # (fp64 sums over every element), plus 8 sampled dW output channels against
     # the oracle's conv2d_backward_weight_cpu.
