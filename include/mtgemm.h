@@ -189,6 +189,23 @@ int mt_version(void);
  * selected (tile, operand layouts, split-K), for tests and benchmarks. */
 const char* mt_last_config(void);
 
+/* Tuning and test hooks; no counterpart in the reference (its launcher has one
+ * fixed kernel per case, src/gpu_ops.cpp:1103-1144).  Kernel families: */
+enum {
+    MT_FAMILY_AUTO = 0,  /* the cost model chooses (default)                   */
+    MT_FAMILY_RS = 1,    /* register-staged kernel: any operand layout          */
+    MT_FAMILY_DL = 2     /* direct-to-LDS kernel: k- or mn-contiguous operands  */
+};
+/* Number of tile configurations of a family (0 for MT_FAMILY_AUTO). */
+int mt_gemm_config_count(int family);
+/* Forces tile configuration `cfg` of `family`, asked for `splits` K splits
+ * (1..64; fewer when K is short), on every later GEMM launch of the calling
+ * thread whose operands that family takes; the others keep the cost model.
+ * MT_FAMILY_AUTO clears it.  While it is set, workspace queries include its
+ * split-K partials and a launch given less returns MT_ERR_WORKSPACE.
+ * Returns MT_ERR_INVALID for an unknown family, configuration or split count. */
+int mt_gemm_force_config(int family, int cfg, int splits);
+
 #ifdef __cplusplus
 }
 #endif

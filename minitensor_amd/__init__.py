@@ -17,6 +17,7 @@ std::invalid_argument); runtime failures raise RuntimeError.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 from pathlib import Path
@@ -103,6 +104,8 @@ _SIGS = {
     "mt_strerror": (ctypes.c_char_p, [ctypes.c_int]),
     "mt_version": (ctypes.c_int, []),
     "mt_last_config": (ctypes.c_char_p, []),
+    "mt_gemm_config_count": (ctypes.c_int, [ctypes.c_int]),
+    "mt_gemm_force_config": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
 }
 
 _lib_handle: Optional[ctypes.CDLL] = None
@@ -372,6 +375,27 @@ def axpby(x: torch.Tensor, y: torch.Tensor, alpha: float = 1.0, beta: float = 0.
 
 def last_config() -> str:
     return lib().mt_last_config().decode()
+
+
+FAMILY_AUTO, FAMILY_RS, FAMILY_DL = 0, 1, 2
+
+
+def config_count(family: int) -> int:
+    """Tile configurations of a kernel family (FAMILY_RS or FAMILY_DL)."""
+    return lib().mt_gemm_config_count(int(family))
+
+
+@contextlib.contextmanager
+def forced_config(family: int, cfg: int, splits: int = 1):
+    """Force one kernel configuration on this thread's GEMM launches inside the
+    block (where the operand layouts allow that family); a tuning and test
+    hook.  Query workspace sizes inside the block: they include the forced
+    split-K partials."""
+    _check(lib().mt_gemm_force_config(int(family), int(cfg), int(splits)), "mt_gemm_force_config")
+    try:
+        yield
+    finally:
+        lib().mt_gemm_force_config(FAMILY_AUTO, 0, 1)
 
 
 def tolerance(K: int, amax: float, bmax: float) -> float:

@@ -108,27 +108,49 @@ struct CfgCost {
 
 // Cost model (in CU cycles) used to pick the tile configuration and split-K
 // factor.  Work per workgroup is priced at the CU's fp32 MFMA rate (256
-// flop/clk) with a per-configuration efficiency, plus the epilogue's store of
-// its tile; each round of resident workgroups pays a fixed latency; split-K
-// pays for its partial traffic and the reduction launch.  The constants are a
-// least-squares fit to measured times of every configuration and split factor
-// on the benchmark shapes (MI355X).
+// flop/clk) with a per-configuration efficiency; the epilogue's store of a
+// tile overlaps the work of the other workgroups resident on the CU, so it is
+// shared out over the occupancy; each round of resident workgroups pays a
+// fixed latency; split-K pays for its partial traffic and the reduction
+// launch.  The constants are fitted (log-time error plus selection regret) to
+// the measured times of every configuration and split factor on 29 shapes --
+// the benchmark shapes, square, ragged, tall, wide, skinny, batched and
+// convolution GEMMs -- on one MI355X.
 constexpr CfgCost kRsCost[kNumCfg] = {      // register-staged kernel, any layout
-    {TileCfg<0>::BM, TileCfg<0>::BN, 0.84, 1},
-    {TileCfg<1>::BM, TileCfg<1>::BN, 0.73, 2},
-    {TileCfg<2>::BM, TileCfg<2>::BN, 0.63, 4}};
+    {TileCfg<0>::BM, TileCfg<0>::BN, 0.86, 1},
+    {TileCfg<1>::BM, TileCfg<1>::BN, 0.75, 2},
+    {TileCfg<2>::BM, TileCfg<2>::BN, 0.57, 4}};
 constexpr CfgCost kDlCost[kNumDlCfg] = {    // direct-to-LDS kernel, vector layouts
-    {DlCfg<0>::BM, DlCfg<0>::BN, 0.88, 1},
-    {DlCfg<1>::BM, DlCfg<1>::BN, 0.84, 4},
-    {DlCfg<2>::BM, DlCfg<2>::BN, 0.71, 8},
-    {DlCfg<3>::BM, DlCfg<3>::BN, 0.86, 3}};
+    {DlCfg<0>::BM, DlCfg<0>::BN, 0.90, 1},
+    {DlCfg<1>::BM, DlCfg<1>::BN, 0.86, 4},
+    {DlCfg<2>::BM, DlCfg<2>::BN, 0.68, 8},
+    {DlCfg<3>::BM, DlCfg<3>::BN, 0.87, 3}};
 struct CostModel {
-    double round_latency = 9000.0;           // cycles of fill/drain per round
-    double epilogue_bytes_per_cycle = 10.7;  // one workgroup's tile store
-    double bytes_per_cycle = 4260.0;         // device HBM bytes per CU-clock
-    double launch_cycles = 8600.0;           // second (reduce) launch
+    double round_latency = 6200.0;           // cycles of fill/drain per round
+    double epilogue_bytes_per_cycle = 7.9;   // one workgroup's tile store
+    double bytes_per_cycle = 6400.0;         // device HBM bytes per CU-clock
+    double launch_cycles = 17700.0;          // second (reduce) launch
 };
 constexpr int kMaxSplits = 16;
+constexpr int kMaxForcedSplits = 64;
+
+// Tile grid and K split of configuration `cfg` asked for `s` splits (the
+// split count can come out lower: every split takes whole 16-deep chunks).
+Plan cfg_plan(const CfgCost& cc, int cfg, bool dl, int64_t M, int64_t N, int64_t K,
+              int64_t batch, int s) {
+    Plan pl;
+    pl.dl = dl;
+    pl.cfg = cfg;
+    pl.bm = cc.bm;
+    pl.bn = cc.bn;
+    pl.tiles_m = (int)((M + cc.bm - 1) / cc.bm);
+    pl.tiles_n = (int)((N + cc.bn - 1) / cc.bn);
+    const int64_t kps = K > 0 ? ((K + s - 1) / s + kBK - 1) / kBK * kBK : kBK;
+    pl.kps = (int)kps;
+    pl.splits = K > 0 ? (int)((K + kps - 1) / kps) : 1;
+    pl.ws_bytes = pl.splits > 1 ? (size_t)pl.splits * batch * M * N * sizeof(float) : 0;
+    return pl;
+}
 
 Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool allow_split,
                bool dl) {
@@ -140,41 +162,55 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool all
     double best_t = 1e300;
     for (int cfg = 0; cfg < ncfg; ++cfg) {
         const CfgCost& cc = cfgs[cfg];
-        const int64_t tm = (M + cc.bm - 1) / cc.bm;
-        const int64_t tn = (N + cc.bn - 1) / cc.bn;
-        const int64_t tiles = tm * tn * batch;
         for (int s = 1; s <= kMaxSplits; ++s) {
             if (s > 1 && !allow_split) break;
-            int64_t kps = K > 0 ? ((K + s - 1) / s + kBK - 1) / kBK * kBK : kBK;
-            if (s > 1 && kps < 64) break;
-            const int64_t splits = K > 0 ? (K + kps - 1) / kps : 1;
-            if (splits != s) continue;
-            const int64_t wgs = tiles * splits;
+            const Plan pl = cfg_plan(cc, cfg, dl, M, N, K, batch, s);
+            if (s > 1 && pl.kps < 64) break;
+            if (pl.splits != s) continue;
+            const int64_t wgs = (int64_t)pl.tiles_m * pl.tiles_n * batch * pl.splits;
             if (wgs * 512 >= ((int64_t)1 << 32)) continue;
             const double per_cu = std::ceil((double)wgs / cus);
             const double rounds = std::ceil((double)wgs / ((double)cus * cc.occ));
-            const double work = (double)cc.bm * cc.bn * (double)std::max<int64_t>(kps, kBK) *
+            const double work = (double)cc.bm * cc.bn * (double)std::max<int64_t>(pl.kps, kBK) *
                                 2.0 / (256.0 * cc.eff);
             const double epi = (double)cc.bm * cc.bn * 4.0 / cm.epilogue_bytes_per_cycle;
-            double t = per_cu * (work + epi) + rounds * cm.round_latency;
-            if (splits > 1) {
-                const double bytes = (double)(2 * splits + 1) * M * N * batch * 4.0;
+            double t = per_cu * work + per_cu * epi / cc.occ + rounds * cm.round_latency;
+            if (pl.splits > 1) {
+                const double bytes = (double)(2 * pl.splits + 1) * M * N * batch * 4.0;
                 t += bytes / (cm.bytes_per_cycle) + cm.launch_cycles;
             }
             if (t < best_t) {
                 best_t = t;
-                best.cfg = cfg;
-                best.bm = cc.bm;
-                best.bn = cc.bn;
-                best.splits = (int)splits;
-                best.kps = (int)kps;
-                best.tiles_m = (int)tm;
-                best.tiles_n = (int)tn;
-                best.ws_bytes = splits > 1 ? (size_t)splits * batch * M * N * sizeof(float) : 0;
+                best = pl;
             }
         }
     }
     return best;
+}
+
+// Configuration forced on this thread's launches by mt_gemm_force_config.
+struct ForcedConfig {
+    int family = MT_FAMILY_AUTO;
+    int cfg = 0;
+    int splits = 1;
+};
+thread_local ForcedConfig g_forced;
+
+// The plan of the forced configuration, when one is set and its family can
+// take these operands (dl_ok: both operands have direct-to-LDS layouts;
+// rs_ok: no implicit-im2col operand).
+bool forced_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dl_ok, bool rs_ok,
+                 Plan* out) {
+    const ForcedConfig f = g_forced;
+    if (f.family == MT_FAMILY_DL && dl_ok) {
+        *out = cfg_plan(kDlCost[f.cfg], f.cfg, true, M, N, K, batch, f.splits);
+        return true;
+    }
+    if (f.family == MT_FAMILY_RS && rs_ok) {
+        *out = cfg_plan(kRsCost[f.cfg], f.cfg, false, M, N, K, batch, f.splits);
+        return true;
+    }
+    return false;
 }
 
 GemmLaunchFn rowsum_launcher(int cfg) {
@@ -207,8 +243,11 @@ GemmLaunchFn conv_launcher(int cfg) {
 // Workspace that covers the plan of either kernel family (for sizes queried
 // before the operand pointers, and hence the layouts, are known).
 size_t plan_ws(int64_t M, int64_t N, int64_t K, int64_t batch, int cus) {
-    return std::max(make_plan(M, N, K, batch, cus, true, false).ws_bytes,
-                    make_plan(M, N, K, batch, cus, true, true).ws_bytes);
+    size_t ws = std::max(make_plan(M, N, K, batch, cus, true, false).ws_bytes,
+                         make_plan(M, N, K, batch, cus, true, true).ws_bytes);
+    Plan forced;
+    if (forced_plan(M, N, K, batch, true, true, &forced)) ws = std::max(ws, forced.ws_bytes);
+    return ws;
 }
 
 GemmLaunchFn pick_launcher(const Plan& plan, int la, int lb) {
@@ -307,9 +346,15 @@ __global__ void __launch_bounds__(256) splitk_reduce_vec_f32(GemmParams p) {
 int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t ws_bytes,
                 hipStream_t stream) {
     const int64_t M = p.M, N = p.N, K = p.K, batch = p.batch;
-    Plan plan = make_plan(M, N, K, batch, device_cu_count(), true, dl);
-    if (plan.splits > 1 && (workspace == nullptr || ws_bytes < plan.ws_bytes))
-        plan = make_plan(M, N, K, batch, device_cu_count(), false, dl);
+    Plan plan;
+    if (forced_plan(M, N, K, batch, dl, lb != L_IM && lb != L_IMW, &plan)) {
+        if (plan.splits > 1 && (workspace == nullptr || ws_bytes < plan.ws_bytes))
+            return MT_ERR_WORKSPACE;
+    } else {
+        plan = make_plan(M, N, K, batch, device_cu_count(), true, dl);
+        if (plan.splits > 1 && (workspace == nullptr || ws_bytes < plan.ws_bytes))
+            plan = make_plan(M, N, K, batch, device_cu_count(), false, dl);
+    }
     // Row sums of A are fused only into a direct-to-LDS launch of two
     // mn-contiguous operands without split-K (the caller sees p.rowsum cleared
     // and computes them separately).
@@ -330,9 +375,10 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
 
     const int64_t nblocks = (int64_t)plan.tiles_m * plan.tiles_n * plan.splits * batch;
     if (nblocks >= ((int64_t)1 << 31)) return MT_ERR_UNSUPPORTED;
-    std::snprintf(g_last_config, sizeof g_last_config, "%s %dx%d a=%s b=%s split=%d wgs=%lld",
-                  plan.dl ? "dl" : "rs", plan.bm, plan.bn, layout_name(la),
-                  layout_name(lb), plan.splits, (long long)nblocks);
+    std::snprintf(g_last_config, sizeof g_last_config,
+                  "%s %dx%d a=%s b=%s split=%d wgs=%lld cfg=%d", plan.dl ? "dl" : "rs", plan.bm,
+                  plan.bn, layout_name(la), layout_name(lb), plan.splits, (long long)nblocks,
+                  plan.cfg);
 
     GemmLaunchFn fn = lb == L_IM          ? conv_launcher(plan.cfg)
                       : lb == L_IMW         ? convw_launcher(plan.cfg)
@@ -1101,5 +1147,21 @@ const char* mt_strerror(int status) {
 int mt_version(void) { return MTGEMM_VERSION; }
 
 const char* mt_last_config(void) { return g_last_config; }
+
+int mt_gemm_config_count(int family) {
+    return family == MT_FAMILY_RS ? kNumCfg : family == MT_FAMILY_DL ? kNumDlCfg : 0;
+}
+
+int mt_gemm_force_config(int family, int cfg, int splits) {
+    if (family == MT_FAMILY_AUTO) {
+        g_forced = ForcedConfig{};
+        return MT_OK;
+    }
+    if ((family != MT_FAMILY_RS && family != MT_FAMILY_DL) || cfg < 0 ||
+        cfg >= mt_gemm_config_count(family) || splits < 1 || splits > kMaxForcedSplits)
+        return MT_ERR_INVALID;
+    g_forced = ForcedConfig{family, cfg, splits};
+    return MT_OK;
+}
 
 }  // extern "C"

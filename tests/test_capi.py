@@ -117,3 +117,33 @@ def test_python_front_end_errors():
         mt.matmul(torch.zeros(2, 3), torch.zeros(3, 2))          # CPU tensors: GPU only
     with pytest.raises(ValueError):
         mt.conv2d(torch.zeros(1, 1, 3, 3), torch.zeros(1, 1, 2, 2))
+
+
+def test_config_counts():
+    assert mt.config_count(mt.FAMILY_RS) == 3
+    assert mt.config_count(mt.FAMILY_DL) == 4
+    assert mt.config_count(mt.FAMILY_AUTO) == 0
+
+
+@pytest.mark.parametrize("family,cfg,splits", [
+    (3, 0, 1), (-1, 0, 1), (mt.FAMILY_RS, 3, 1), (mt.FAMILY_DL, 4, 1), (mt.FAMILY_DL, -1, 1),
+    (mt.FAMILY_DL, 0, 0), (mt.FAMILY_DL, 0, 65)])
+def test_force_config_rejects_unknown(family, cfg, splits):
+    assert mt.lib().mt_gemm_force_config(family, cfg, splits) == mt.MT_ERR_INVALID
+
+
+def test_forced_split_is_in_the_workspace_query():
+    """While a split-K configuration is forced, the workspace query covers its
+    partials ([splits][batch][M][N] floats); clearing restores the cost model."""
+    a, b, c = M(256, 512), M(512, 256), M(256, 256)
+    lib = mt.lib()
+    auto = lib.mt_gemm_workspace_f32(a, b, c)
+    with mt.forced_config(mt.FAMILY_DL, 2, 8):
+        assert lib.mt_gemm_workspace_f32(a, b, c) >= 8 * 256 * 256 * 4
+    with mt.forced_config(mt.FAMILY_RS, 0, 1):
+        assert lib.mt_gemm_workspace_f32(a, b, c) == auto
+    assert lib.mt_gemm_workspace_f32(a, b, c) == auto
+    # K = 40 holds three 16-deep chunks: at most three splits.
+    a, b = M(256, 40), M(40, 256)
+    with mt.forced_config(mt.FAMILY_DL, 1, 16):
+        assert lib.mt_gemm_workspace_f32(a, b, c) >= 3 * 256 * 256 * 4
