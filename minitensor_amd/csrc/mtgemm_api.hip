@@ -513,18 +513,30 @@ im2col_f32(const float* in, int64_t sn, int64_t sc, int64_t sh, int64_t sw, floa
     }
 }
 
+// a*b for a, b >= 0, or -1 once the product would reach 2^62 (or an operand
+// is already -1): sizes built from it never wrap.
+int64_t mul_capped(int64_t a, int64_t b) {
+    constexpr int64_t cap = (int64_t)1 << 62;
+    if (a < 0 || b < 0) return -1;
+    if (a != 0 && b >= cap / a) return -1;
+    return a * b;
+}
+
 bool conv_dims(const mt_conv2d_desc* d, int64_t* Ho, int64_t* Wo) {
     if (!d) return false;
-    if (d->n < 0 || d->c_in < 0 || d->h < 0 || d->w < 0 || d->c_out < 0 || d->kh < 1 ||
-        d->kw < 1 || d->stride < 1 || d->pad < 0)
-        return false;
+    for (int64_t v : {d->n, d->c_in, d->h, d->w, d->c_out, d->kh, d->kw, d->stride, d->pad})
+        if (v < 0 || v >= kMaxDim) return false;
+    if (d->kh < 1 || d->kw < 1 || d->stride < 1) return false;
     *Ho = (d->h + 2 * d->pad < d->kh) ? 0 : (d->h + 2 * d->pad - d->kh) / d->stride + 1;
     *Wo = (d->w + 2 * d->pad < d->kw) ? 0 : (d->w + 2 * d->pad - d->kw) / d->stride + 1;
-    const int64_t kg = d->c_in * d->kh * d->kw;
-    const int64_t np = d->n * *Ho * *Wo;
-    if (kg >= kMaxDim || np >= kMaxDim || d->c_out >= kMaxDim) return false;
-    if (d->h >= kMaxDim || d->w >= kMaxDim) return false;
-    return true;
+    // GEMM extents are 32-bit inside the kernels; tensor sizes must not wrap.
+    const int64_t kg = mul_capped(mul_capped(d->c_in, d->kh), d->kw);
+    const int64_t np = mul_capped(mul_capped(d->n, *Ho), *Wo);
+    const int64_t in_elems = mul_capped(mul_capped(mul_capped(d->n, d->c_in), d->h), d->w);
+    if (kg < 0 || np < 0 || in_elems < 0 || mul_capped(np, d->c_out) < 0 ||
+        mul_capped(kg, d->c_out) < 0)
+        return false;
+    return kg < kMaxDim && np < kMaxDim;
 }
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
@@ -873,6 +885,7 @@ int mt_linear_backward_f32(const mt_mat_f32* dY, const mt_mat_f32* X, const mt_m
                            void* stream) {
     if (!valid_mat(dY) || !valid_mat(X) || !valid_mat(W)) return MT_ERR_INVALID;
     if (dY->rows != X->rows || dY->cols != W->rows || X->cols != W->cols) return MT_ERR_INVALID;
+    if (db && db_stride < 0) return MT_ERR_INVALID;
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (dX) {  // dX[B,in] = dY[B,out] · W[out,in]
         int rc = run_gemm(dY, W, dX, 0, 0, nullptr, workspace, ws_bytes, s);

@@ -89,9 +89,16 @@ def test_conv_rejects_invalid_descriptors():
     for d in [mt.Conv2dDesc(1, 3, 8, 8, 4, 0, 3, 1, 0),    # kh = 0
               mt.Conv2dDesc(1, 3, 8, 8, 4, 3, 3, 0, 0),    # stride 0
               mt.Conv2dDesc(-1, 3, 8, 8, 4, 3, 3, 1, 0),   # negative batch
-              mt.Conv2dDesc(1, 3, 8, 8, 4, 3, 3, 1, -1)]:  # negative padding
+              mt.Conv2dDesc(1, 3, 8, 8, 4, 3, 3, 1, -1),   # negative padding
+              mt.Conv2dDesc(1, 1 << 31, 8, 8, 4, 3, 3, 1, 1),           # field past 32 bits
+              mt.Conv2dDesc(1, 1 << 20, 8, 8, 4, 1 << 11, 1, 1, 1 << 11),  # c_in*kh >= 2^31
+              mt.Conv2dDesc(1 << 30, 2, 1 << 30, 1 << 30, 1, 1, 1, 1 << 30, 0),
+              # n*c_in*h*w and c_out*kg wrap int64 unless capped
+              mt.Conv2dDesc(1 << 30, 1 << 30, 1 << 30, 1 << 30, 1, 1, 1, 1 << 30, 0),
+              mt.Conv2dDesc(1, 1 << 15, 1, 1, (1 << 31) - 1, 1 << 15, 1, 1, 1 << 15)]:
         rc = lib.mt_conv2d_fwd_f32(ctypes.byref(d), 0x1000, 0x1000, None, 0x1000, None, 0, None)
-        assert rc == mt.MT_ERR_INVALID
+        assert rc == mt.MT_ERR_INVALID, (d.n, d.c_in, d.h, d.w, d.c_out, d.kh, d.kw)
+        assert lib.mt_conv2d_workspace_f32(ctypes.byref(d)) == 0
     # kernel larger than the padded input: the reference's safe_out_size gives 0 -> no work
     d = mt.Conv2dDesc(1, 3, 2, 2, 4, 5, 5, 1, 0)
     assert lib.mt_conv2d_workspace_f32(ctypes.byref(d)) == 0
@@ -108,6 +115,13 @@ def test_linear_rejects_mismatched_shapes():
     lib = mt.lib()
     rc = lib.mt_linear_backward_f32(M(8, 10), M(8, 6), M(11, 6), None, None, 0.0, None, 0, 0.0,
                                     None, 0, None)
+    assert rc == mt.MT_ERR_INVALID
+
+
+def test_linear_backward_rejects_negative_bias_grad_stride():
+    lib = mt.lib()
+    rc = lib.mt_linear_backward_f32(M(8, 10), M(8, 6), M(10, 6), None, M(10, 6), 0.0, 0x2000, -1,
+                                    0.0, None, 0, None)
     assert rc == mt.MT_ERR_INVALID
 
 
