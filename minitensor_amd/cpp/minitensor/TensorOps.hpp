@@ -348,38 +348,60 @@ void conv2d_gpu_strided(const Tensor<T>& in, const Tensor<T>& w, const Tensor<T>
     conv2d_gpu(in, w, bias, out, stride, padding);
 }
 
+// The backward kernels take dense tensors: views are copied in (and a strided
+// output is produced densely, then copied out; with beta != 0 its current
+// contents are copied in first).
+namespace mt_detail {
+template <typename T>
+Tensor<T> dense_out(const Tensor<T>& out, float beta) {
+    if (out.is_contiguous()) return out;
+    Tensor<T> o(out.shape(), out.device());
+    if (beta != 0.f) copy_gpu_strided(out, o);
+    return o;
+}
+}  // namespace mt_detail
+
 template <typename T>
 void conv2d_backward_input_gpu(const Tensor<T>& go, const Tensor<T>& w, Tensor<T>& gi,
                                size_t stride, size_t padding) {
     mt_detail::require_float_gpu<T>();
-    const mt_conv2d_desc d = mt_detail::conv_desc(gi.shape(), w.shape(), stride, padding);
+    const Tensor<T> g = go.contiguous(), wd = w.contiguous();
+    Tensor<T> o = mt_detail::dense_out(gi, 0.f);
+    const mt_conv2d_desc d = mt_detail::conv_desc(gi.shape(), wd.shape(), stride, padding);
     mt_detail::Workspace ws(mt_conv2d_bwd_workspace_f32(&d), gi.device());
-    mt_check_status(mt_conv2d_bwd_input_f32(&d, go.data() + go.offset(), w.data() + w.offset(),
-                                            gi.data() + gi.offset(), ws.get(), ws.size(),
+    mt_check_status(mt_conv2d_bwd_input_f32(&d, g.data() + g.offset(), wd.data() + wd.offset(),
+                                            o.data() + o.offset(), ws.get(), ws.size(),
                                             active_stream()),
                     "conv2d backward input");
+    if (!gi.is_contiguous()) copy_gpu_strided(o, gi);
 }
 
 template <typename T>
 void conv2d_backward_weight_gpu(const Tensor<T>& go, const Tensor<T>& in, Tensor<T>& gw,
                                 size_t stride, size_t padding, float beta = 0.f) {
     mt_detail::require_float_gpu<T>();
-    const mt_conv2d_desc d = mt_detail::conv_desc(in.shape(), gw.shape(), stride, padding);
+    const Tensor<T> g = go.contiguous(), x = in.contiguous();
+    Tensor<T> o = mt_detail::dense_out(gw, beta);
+    const mt_conv2d_desc d = mt_detail::conv_desc(x.shape(), gw.shape(), stride, padding);
     mt_detail::Workspace ws(mt_conv2d_bwd_workspace_f32(&d), gw.device());
-    mt_check_status(mt_conv2d_bwd_weight_f32(&d, in.data() + in.offset(), go.data() + go.offset(),
-                                             gw.data() + gw.offset(), beta, ws.get(), ws.size(),
+    mt_check_status(mt_conv2d_bwd_weight_f32(&d, x.data() + x.offset(), g.data() + g.offset(),
+                                             o.data() + o.offset(), beta, ws.get(), ws.size(),
                                              active_stream()),
                     "conv2d backward weight");
+    if (!gw.is_contiguous()) copy_gpu_strided(o, gw);
 }
 
 template <typename T>
 void conv2d_backward_bias_gpu(const Tensor<T>& go, Tensor<T>& gb, float beta = 0.f) {
     mt_detail::require_float_gpu<T>();
-    const auto& s = go.shape();
+    const Tensor<T> g = go.contiguous();
+    Tensor<T> o = mt_detail::dense_out(gb, beta);
+    const auto& s = g.shape();
     mt_conv2d_desc d{(int64_t)s[0], 1, (int64_t)s[2], (int64_t)s[3], (int64_t)s[1], 1, 1, 1, 0};
-    mt_check_status(mt_conv2d_bwd_bias_f32(&d, go.data() + go.offset(), gb.data() + gb.offset(),
+    mt_check_status(mt_conv2d_bwd_bias_f32(&d, g.data() + g.offset(), o.data() + o.offset(),
                                            beta, active_stream()),
                     "conv2d backward bias");
+    if (!gb.is_contiguous()) copy_gpu_strided(o, gb);
 }
 
 // ======================================================================

@@ -439,6 +439,52 @@ TEST_GPU(gpu_conv_strided_input_views) {
     check_close(conv2d(xt, w3.to(GPU), b4.to(GPU), 2, 1), want3, 27, 1, 1, 1e-5);
 }
 
+TEST_GPU(gpu_conv_backward_views) {
+    // conv2d_backward_{input,weight,bias}_gpu on strided views: dY a transposed
+    // view, dX and dW slices of wider tensors (their neighbours must survive),
+    // dW and db accumulated with beta = 1 into a view; against the CPU device on
+    // dense copies.  Both dX geometries: implicit (c_out = 16) and column buffer.
+    for (size_t co : {16, 6}) {
+        const size_t n = 2, c = 4, h = 7, w = 8, k = 3;
+        Tensor<float> x = uniform({n, c, h, w}, 21), wt = uniform({co, c, k, k}, 22);
+        Tensor<float> dyt = uniform({n, co, w, h}, 23);            // stored W-major
+        Tensor<float> dy = dyt.transpose(2, 3).contiguous();       // [n, co, h, w]
+        Tensor<float> dx_want({n, c, h, w}), dw_want({co, c, k, k}), db_want({co});
+        conv2d_backward_input(dy, wt, dx_want, 1, 1);
+        conv2d_backward_weight(dy, x, dw_want, 1, 1);
+        conv2d_backward_bias(dy, db_want);
+
+        Tensor<float> dyg = dyt.to(GPU).transpose(2, 3);
+        CHECK(!dyg.is_contiguous());
+        Tensor<float> dx_big({n, c + 3, h, w}, GPU);
+        dx_big.fill(7.f);
+        Tensor<float> dx = dx_big.slice(1, 1, 1 + c);
+        CHECK(!dx.is_contiguous());
+        conv2d_backward_input(dyg, wt.to(GPU), dx, 1, 1);
+        check_close(dx, dx_want, co * k * k, 1, 1);
+        CHECK_EQ_F(val(dx_big.slice(1, 0, 1).contiguous(), 5), 7.f);
+        CHECK_EQ_F(val(dx_big.slice(1, c + 1, c + 2).contiguous(), 3), 7.f);
+
+        Tensor<float> dw_big({co, c + 2, k, k}, GPU);
+        dw_big.fill(1.f);
+        Tensor<float> dw = dw_big.slice(1, 2, 2 + c);
+        conv2d_backward_weight_gpu(dyg, x.to(GPU), dw, 1, 1, 1.f);   // dW = 1 + ∂L/∂W
+        Tensor<float> ones({co, c, k, k});
+        ones.fill(1.f);
+        check_close(dw, dw_want + ones, n * h * w, 1, 1, 1e-6);
+        CHECK_EQ_F(val(dw_big.slice(1, 0, 1).contiguous(), 0), 1.f);
+
+        Tensor<float> db_big({2 * co}, GPU);
+        db_big.fill(2.f);
+        Tensor<float> db = db_big.as_strided({co}, {2}, 0);          // every other element
+        conv2d_backward_bias_gpu(dyg, db, 1.f);                       // db = 2 + Σ dY
+        Tensor<float> twos({co});
+        twos.fill(2.f);
+        check_close(db, db_want + twos, n * h * w, 1, 1, 1e-6);
+        CHECK_EQ_F(val(db_big, 1), 2.f);
+    }
+}
+
 void check_equal(const Tensor<float>& a, const Tensor<float>& b, const char* what) {
     Tensor<float> ha = host(a), hb = host(b);
     CHECK(ha.shape() == hb.shape());
