@@ -187,3 +187,37 @@ def test_forced_split_without_workspace_is_an_error(dev):
     with mt.forced_config(mt.FAMILY_DL, 2, 4):
         rc = mt.lib().mt_gemm_f32(mt.mat(a), mt.mat(b), mt.mat(c), None, None, 0, None)
     assert rc == mt.MT_ERR_WORKSPACE
+
+
+@pytest.mark.parametrize("fc", CONFIGS, ids=IDS)
+@pytest.mark.parametrize("splits", [1, 4])
+def test_forced_config_special_values(dev, fc, splits):
+    # IEEE special values go through every kernel as through matmul_cpu
+    # (include/TensorOps.hpp:139-160): fp32 denormal operands and products are
+    # kept (no flush to zero; exact here, every product and partial sum is a
+    # multiple of 2^-149 well inside range), NaN and ±Inf reach the same
+    # outputs with the same signs, and the accumulator starts at +0.
+    family, cfg = fc
+    M, N, K = 72, 68, 128
+    with mt.forced_config(family, cfg, splits):
+        a = np.full((M, K), 2.0 ** -70, np.float32)
+        b = np.full((K, N), 2.0 ** -70, np.float32)            # products 2^-140: denormal
+        c = mt.gemm(g(a, dev), g(b, dev))
+        check_config(family, cfg, splits)
+        np.testing.assert_array_equal(sync_np(c), oracle.matmul(a, b))
+        assert sync_np(c)[0, 0] == np.float32(K * 2.0 ** -140) != 0
+
+        a = oracle.uniform((M, K), 31)
+        b = oracle.uniform((K, N), 32)
+        a[3, 5], a[7, 2], b[4, 9], b[100, 60] = np.nan, np.inf, -np.inf, np.nan
+        got, want = sync_np(mt.gemm(g(a, dev), g(b, dev))), oracle.matmul(a, b)
+        np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
+        np.testing.assert_array_equal(np.isposinf(got), np.isposinf(want))
+        np.testing.assert_array_equal(np.isneginf(got), np.isneginf(want))
+        fin = np.isfinite(want)
+        assert_close(np.where(fin, got, 0), np.where(fin, want, 0), K, 1.0, 1.0,
+                     f"forced {family}/{cfg} finite entries next to NaN/Inf")
+
+        z = np.zeros((M, K), np.float32) * -1.0                  # -0.0 operands
+        got = sync_np(mt.gemm(g(z, dev), g(np.ones((K, N), np.float32), dev)))
+        np.testing.assert_array_equal(np.signbit(got), np.signbit(oracle.matmul(z, np.ones((K, N), np.float32))))
