@@ -152,8 +152,8 @@ Plan cfg_plan(const CfgCost& cc, int cfg, bool dl, int64_t M, int64_t N, int64_t
     return pl;
 }
 
-Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool allow_split,
-               bool dl) {
+Plan make_plan_uncached(int64_t M, int64_t N, int64_t K, int64_t batch, int cus,
+                        bool allow_split, bool dl) {
     static const CostModel cm;
     const CfgCost* cfgs = dl ? kDlCost : kRsCost;
     const int ncfg = dl ? kNumDlCfg : kNumCfg;
@@ -186,6 +186,31 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool all
         }
     }
     return best;
+}
+
+// The cost model is a pure function of its arguments; a training loop asks
+// for the same few shapes again and again (workspace query, then launch), so
+// each thread keeps its last few plans.
+Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool allow_split,
+               bool dl) {
+    struct Entry {
+        int64_t M = -1, N = -1, K = -1, batch = -1;
+        int cus = 0;
+        bool allow_split = false, dl = false;
+        Plan plan;
+    };
+    constexpr int kEntries = 8;
+    thread_local Entry cache[kEntries];
+    thread_local int next = 0;
+    for (const Entry& e : cache)
+        if (e.M == M && e.N == N && e.K == K && e.batch == batch && e.cus == cus &&
+            e.allow_split == allow_split && e.dl == dl)
+            return e.plan;
+    Entry& e = cache[next];
+    next = (next + 1) % kEntries;
+    e = Entry{M, N, K, batch, cus, allow_split, dl,
+              make_plan_uncached(M, N, K, batch, cus, allow_split, dl)};
+    return e.plan;
 }
 
 // Configuration forced on this thread's launches by mt_gemm_force_config.
