@@ -34,7 +34,7 @@ COMMON = [
 ]
 
 N_CFG = 3      # register-staged tile configurations (TileCfg)
-N_DL_CFG = 4   # direct-to-LDS tile configurations (DlCfg)
+N_DL_CFG = 4   # gemm_f32_dl tile configurations (DlCfg 0..3; DlCfg 4 is gemm_f32_dlp)
 
 
 def _units():
@@ -44,6 +44,7 @@ def _units():
     for cfg in range(N_DL_CFG):
         units.append((CSRC / "gemm_dl_instances.hip", OBJDIR / f"gemm_dl_cfg{cfg}.o",
                       [f"-DMT_CFG={cfg}"]))
+    units.append((CSRC / "gemm_dlp_instances.hip", OBJDIR / "gemm_dlp.o", []))
     units.append((CSRC / "mtgemm_api.hip", OBJDIR / "mtgemm_api.o", []))
     return units
 

@@ -1,0 +1,188 @@
+// gemm_dlp_kernel.hpp -- direct-to-LDS fp32 MFMA GEMM with one 128x128 wave
+// tile per SIMD and its fragments prefetched a chunk ahead.
+//
+// The 256x256 block tile of gemm_f32_dl's first configuration, computed by
+// four waves instead of eight:
+//   * Each wave owns a 128x128 accumulator tile (4 x 4 MFMA blocks, 256
+//     accumulator registers), so a SIMD runs one wave.  Per 16-deep K-chunk a
+//     wave reads 16 KB of fragments from LDS for 128 MFMAs, against 12 KB for
+//     64 MFMAs with 128x64 wave tiles: two thirds of the LDS read traffic per
+//     flop.
+//   * With no second wave on the SIMD to cover the LDS latency, chunk kt+1's
+//     fragments are read while chunk kt's MFMAs issue: two register sets
+//     alternate (the loop is unrolled by two so that each set is a fixed set
+//     of registers).  The body has no branches, so the scheduler can spread
+//     the fragment reads and the next DMA over the MFMA stream (the
+//     sched_group_barrier pattern in dlp_interleave).
+//   * Ring of STAGES LDS slots, one s_barrier per chunk.  At the barrier of
+//     step kt, chunk kt+1 has landed (each wave waited for its own DMA) and
+//     every wave has retired its reads of chunk kt's slot, which the step then
+//     refills with chunk kt+STAGES.  Refills past the last chunk re-fetch the
+//     last chunk (always in bounds) into slots nobody reads again, so the DMA
+//     count per step, and hence every vmcnt, is the same on every step.
+// Host contract (checked in the dispatcher): operand layouts L_KV / L_MV,
+// every split's K range a whole number (>= 1) of 16-deep chunks, and a vector
+// epilogue (c_vec; ws_vec with split-K).  Rows or columns beyond M or N read
+// clamped, valid rows, as in gemm_f32_dl.
+#pragma once
+
+#include "gemm_dl_kernel.hpp"
+
+namespace mtk {
+
+// Epilogue with the 16-byte forms of store_tile only, written as one path for
+// both destinations: a split-K partial is the same store into the workspace
+// with bias and beta switched off.  (Separate paths make the compiler copy the
+// 256 accumulators out of their registers before the branch.)
+template <int MB, int NB>
+__device__ __forceinline__ void store_tile_vec(const GemmParams& p, const f32x16 (&acc)[MB][NB],
+                                               int mw0, int nw0, int lane, int split, int bz) {
+    const int h = lane >> 5, c = lane & 31;
+    const bool part = p.splits > 1;
+    float* const base = part ? p.ws + ((int64_t)split * p.batch + bz) * (int64_t)p.M * p.N
+                             : p.C + (int64_t)bz * p.c_b;
+    const int64_t rs = part ? (int64_t)p.N : p.c_m;
+    const int bias_axis = part ? 0 : p.bias_axis;
+    const float beta = part ? 0.f : p.beta;
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+        const int m = mw0 + i * 32 + c;
+        if (m >= p.M) continue;
+        float* const Cr = base + (int64_t)m * rs;
+        const float brow = bias_axis == 1 ? p.bias[(int64_t)m * p.bias_stride] : 0.f;
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int n = nw0 + j * 32 + 8 * q + 4 * h;
+                if (n >= p.N) continue;
+                f32x4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    o[e] = acc[i][j][4 * q + e] + brow;
+                    if (bias_axis == 2) o[e] += p.bias[(int64_t)(n + e) * p.bias_stride];
+                }
+                f32x4* const dst = reinterpret_cast<f32x4*>(Cr + (part ? (int64_t)n : col_offset(p, n)));
+                if (beta != 0.f) o += beta * *dst;
+                *dst = o;
+            }
+    }
+}
+
+// Spread one step's instructions over its 128 MFMAs: the DMA of the refill
+// (up to 8 wave instructions) first, one per MFMA, then the fragment reads of
+// the next chunk (up to 40 LDS instructions), one per two MFMAs.  Groups
+// without instructions of their kind stay empty.
+__device__ __forceinline__ void dlp_interleave() {
+    constexpr int kMfma = 0x008, kVmemRead = 0x020, kDsRead = 0x100;
+    __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+        __builtin_amdgcn_sched_group_barrier(kVmemRead, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+    }
+#pragma unroll
+    for (int g = 0; g < 40; ++g) {
+        __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kMfma, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kMfma, 128, 0);
+}
+
+template <int LA, int LB, int STAGES>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+gemm_f32_dlp(GemmParams p) {
+    constexpr int BM = 256, BN = 256, WM = 128, WN = 128, NW = 4;
+    constexpr int MB = WM / 32, NB = WN / 32;
+    static_assert(STAGES >= 2, "the ring needs at least two slots");
+    static_assert((LA == L_KV || LA == L_MV) && (LB == L_KV || LB == L_MV),
+                  "vector operand layouts only");
+    using TA = DlTile<LA, BM, NW>;
+    using TB = DlTile<LB, BN, NW>;
+    constexpr int STAGE = TA::floats + TB::floats;
+    constexpr int LOADS = TA::per_wave + TB::per_wave;   // wave instructions per chunk
+    static_assert(LOADS * (STAGES - 1) < 64, "vmcnt holds at most 63");
+    __shared__ __attribute__((aligned(1024))) float smem[STAGES * STAGE];
+
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int ra = (wave >> 1) * WM, rb = (wave & 1) * WN;
+
+    const TileId id = tile_id(p);
+    const int m0 = id.tm * BM, n0 = id.tn * BN;
+    const int k_begin = id.split * p.k_per_split;
+    const int k_end = min(p.K, k_begin + p.k_per_split);
+    const int nk = (k_end - k_begin) >> 4;   // >= 1 by the host contract
+    const float* Ab = p.A + (int64_t)id.bz * p.a_b;
+    const float* Bb = p.B + (int64_t)id.bz * p.b_b;
+
+    f32x16 acc[MB][NB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    DlLoader<LA, BM, NW> la;
+    DlLoader<LB, BN, NW> lb;
+    la.init(Ab, p.a_mn, p.a_k, p.M, m0, k_begin, wave, lane);
+    lb.init(Bb, p.b_mn, p.b_k, p.N, n0, k_begin, wave, lane);
+#pragma unroll
+    for (int c = 0; c < STAGES; ++c) {
+        const int cc = min(c, nk - 1);
+        la.issue(smem + c * STAGE, cc, wave);
+        lb.issue(smem + c * STAGE + TA::floats, cc, wave);
+    }
+    // chunk 0 landed (own DMA), then everyone's
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(LOADS * (STAGES - 1)));
+    __builtin_amdgcn_s_barrier();
+    float fa0[MB][8], fb0[NB][8], fa1[MB][8], fb1[NB][8];
+    dl_frags<LA, BM, MB>(smem, ra, lane, fa0);
+    dl_frags<LB, BN, NB>(smem + TA::floats, rb, lane, fb0);
+
+    // Step kt: multiply chunk kt (registers ca/cb) while reading chunk kt+1
+    // into na/nb and refilling chunk kt's slot with chunk kt+STAGES.
+    auto step = [&](int kt, const float (&ca)[MB][8], const float (&cb)[NB][8],
+                    float (&na)[MB][8], float (&nb)[NB][8]) {
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(LOADS * (STAGES - 2)));
+        __builtin_amdgcn_s_barrier();
+        float* const refill = smem + (kt % STAGES) * STAGE;
+        const int cn = min(kt + STAGES, nk - 1);
+        la.issue(refill, cn, wave);
+        lb.issue(refill + TA::floats, cn, wave);
+        const float* const next = smem + ((kt + 1) % STAGES) * STAGE;
+        dl_frags<LA, BM, MB>(next, ra, lane, na);
+        dl_frags<LB, BN, NB>(next + TA::floats, rb, lane, nb);
+        mfma_chunk<MB, NB>(acc, ca, cb);
+        dlp_interleave();
+    };
+
+    int kt = 0;
+    for (; kt + 2 < nk; kt += 2) {
+        step(kt, fa0, fb0, fa1, fb1);
+        step(kt + 1, fa1, fb1, fa0, fb0);
+    }
+    if (kt + 1 < nk) {
+        // one more step leaves the last chunk in set 1; moving it to set 0
+        // keeps a single final MFMA block (an MFMA block per branch arm makes
+        // the compiler copy the accumulators out of their registers)
+        step(kt, fa0, fb0, fa1, fb1);
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+            for (int s = 0; s < 8; ++s) fa0[i][s] = fa1[i][s];
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int s = 0; s < 8; ++s) fb0[j][s] = fb1[j][s];
+    }
+    mfma_chunk<MB, NB>(acc, fa0, fb0);
+    // The re-fetches past the last chunk may still be landing in LDS.
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+
+    store_tile_vec<MB, NB>(p, acc, m0 + ra, n0 + rb, lane, id.split, id.bz);
+}
+
+}  // namespace mtk

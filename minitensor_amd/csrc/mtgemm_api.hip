@@ -124,7 +124,8 @@ constexpr CfgCost kDlCost[kNumDlCfg] = {    // direct-to-LDS kernel, vector layo
     {DlCfg<0>::BM, DlCfg<0>::BN, 0.90, 1},
     {DlCfg<1>::BM, DlCfg<1>::BN, 0.86, 4},
     {DlCfg<2>::BM, DlCfg<2>::BN, 0.68, 8},
-    {DlCfg<3>::BM, DlCfg<3>::BN, 0.87, 3}};
+    {DlCfg<3>::BM, DlCfg<3>::BN, 0.87, 3},
+    {DlCfg<4>::BM, DlCfg<4>::BN, 0.93, 1}};
 struct CostModel {
     double round_latency = 6200.0;           // cycles of fill/drain per round
     double epilogue_bytes_per_cycle = 7.9;   // one workgroup's tile store
@@ -152,8 +153,10 @@ Plan cfg_plan(const CfgCost& cc, int cfg, bool dl, int64_t M, int64_t N, int64_t
     return pl;
 }
 
+// wide: the direct-to-LDS configuration kDlpCfg may be chosen (see
+// wide_ok in launch_gemm).
 Plan make_plan_uncached(int64_t M, int64_t N, int64_t K, int64_t batch, int cus,
-                        bool allow_split, bool dl) {
+                        bool allow_split, bool dl, bool wide) {
     static const CostModel cm;
     const CfgCost* cfgs = dl ? kDlCost : kRsCost;
     const int ncfg = dl ? kNumDlCfg : kNumCfg;
@@ -161,6 +164,7 @@ Plan make_plan_uncached(int64_t M, int64_t N, int64_t K, int64_t batch, int cus,
     best.dl = dl;
     double best_t = 1e300;
     for (int cfg = 0; cfg < ncfg; ++cfg) {
+        if (dl && cfg == kDlpCfg && !wide) continue;
         const CfgCost& cc = cfgs[cfg];
         for (int s = 1; s <= kMaxSplits; ++s) {
             if (s > 1 && !allow_split) break;
@@ -192,11 +196,11 @@ Plan make_plan_uncached(int64_t M, int64_t N, int64_t K, int64_t batch, int cus,
 // for the same few shapes again and again (workspace query, then launch), so
 // each thread keeps its last few plans.
 Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool allow_split,
-               bool dl) {
+               bool dl, bool wide) {
     struct Entry {
         int64_t M = -1, N = -1, K = -1, batch = -1;
         int cus = 0;
-        bool allow_split = false, dl = false;
+        bool allow_split = false, dl = false, wide = false;
         Plan plan;
     };
     constexpr int kEntries = 8;
@@ -204,12 +208,12 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool all
     thread_local int next = 0;
     for (const Entry& e : cache)
         if (e.M == M && e.N == N && e.K == K && e.batch == batch && e.cus == cus &&
-            e.allow_split == allow_split && e.dl == dl)
+            e.allow_split == allow_split && e.dl == dl && e.wide == wide)
             return e.plan;
     Entry& e = cache[next];
     next = (next + 1) % kEntries;
-    e = Entry{M, N, K, batch, cus, allow_split, dl,
-              make_plan_uncached(M, N, K, batch, cus, allow_split, dl)};
+    e = Entry{M, N, K, batch, cus, allow_split, dl, wide,
+              make_plan_uncached(M, N, K, batch, cus, allow_split, dl, wide)};
     return e.plan;
 }
 
@@ -223,11 +227,12 @@ thread_local ForcedConfig g_forced;
 
 // The plan of the forced configuration, when one is set and its family can
 // take these operands (dl_ok: both operands have direct-to-LDS layouts;
-// rs_ok: no implicit-im2col operand).
+// rs_ok: no implicit-im2col operand; wide_ok: configuration kDlpCfg can take
+// them too).
 bool forced_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dl_ok, bool rs_ok,
-                 Plan* out) {
+                 bool wide_ok, Plan* out) {
     const ForcedConfig f = g_forced;
-    if (f.family == MT_FAMILY_DL && dl_ok) {
+    if (f.family == MT_FAMILY_DL && dl_ok && (f.cfg != kDlpCfg || wide_ok)) {
         *out = cfg_plan(kDlCost[f.cfg], f.cfg, true, M, N, K, batch, f.splits);
         return true;
     }
@@ -238,12 +243,15 @@ bool forced_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dl_ok, boo
     return false;
 }
 
+// The implicit-im2col and row-sum forms exist for DlCfg 0..3; the planner
+// never picks kDlpCfg for them (nullptr is a safety net).
 GemmLaunchFn rowsum_launcher(int cfg) {
     switch (cfg) {
         case 0: return dl_rowsum_launcher_cfg0();
         case 1: return dl_rowsum_launcher_cfg1();
         case 2: return dl_rowsum_launcher_cfg2();
-        default: return dl_rowsum_launcher_cfg3();
+        case 3: return dl_rowsum_launcher_cfg3();
+        default: return nullptr;
     }
 }
 
@@ -252,7 +260,8 @@ GemmLaunchFn convw_launcher(int cfg) {
         case 0: return dl_convw_launcher_cfg0();
         case 1: return dl_convw_launcher_cfg1();
         case 2: return dl_convw_launcher_cfg2();
-        default: return dl_convw_launcher_cfg3();
+        case 3: return dl_convw_launcher_cfg3();
+        default: return nullptr;
     }
 }
 
@@ -261,17 +270,19 @@ GemmLaunchFn conv_launcher(int cfg) {
         case 0: return dl_conv_launcher_cfg0();
         case 1: return dl_conv_launcher_cfg1();
         case 2: return dl_conv_launcher_cfg2();
-        default: return dl_conv_launcher_cfg3();
+        case 3: return dl_conv_launcher_cfg3();
+        default: return nullptr;
     }
 }
 
 // Workspace that covers the plan of either kernel family (for sizes queried
 // before the operand pointers, and hence the layouts, are known).
 size_t plan_ws(int64_t M, int64_t N, int64_t K, int64_t batch, int cus) {
-    size_t ws = std::max(make_plan(M, N, K, batch, cus, true, false).ws_bytes,
-                         make_plan(M, N, K, batch, cus, true, true).ws_bytes);
+    size_t ws = std::max({make_plan(M, N, K, batch, cus, true, false, false).ws_bytes,
+                          make_plan(M, N, K, batch, cus, true, true, false).ws_bytes,
+                          make_plan(M, N, K, batch, cus, true, true, true).ws_bytes});
     Plan forced;
-    if (forced_plan(M, N, K, batch, true, true, &forced)) ws = std::max(ws, forced.ws_bytes);
+    if (forced_plan(M, N, K, batch, true, true, true, &forced)) ws = std::max(ws, forced.ws_bytes);
     return ws;
 }
 
@@ -281,7 +292,8 @@ GemmLaunchFn pick_launcher(const Plan& plan, int la, int lb) {
             case 0: return dl_launcher_cfg0(la, lb);
             case 1: return dl_launcher_cfg1(la, lb);
             case 2: return dl_launcher_cfg2(la, lb);
-            default: return dl_launcher_cfg3(la, lb);
+            case 3: return dl_launcher_cfg3(la, lb);
+            default: return dlp_launcher(la, lb);
         }
     }
     switch (plan.cfg) {
@@ -371,14 +383,25 @@ __global__ void __launch_bounds__(256) splitk_reduce_vec_f32(GemmParams p) {
 int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t ws_bytes,
                 hipStream_t stream) {
     const int64_t M = p.M, N = p.N, K = p.K, batch = p.batch;
+    const bool implicit = lb == L_IM || lb == L_IMW;
+    // 16-byte epilogue stores: four consecutive columns must be contiguous,
+    // aligned, and (for a scattered output) never straddle a column group.
+    p.c_vec = p.c_n == 1 && (N & 3) == 0 && ((uintptr_t)p.C & 15u) == 0 && (p.c_m & 3) == 0 &&
+              (batch == 1 || (p.c_b & 3) == 0) &&
+              (p.c_n_inner >= N || ((p.c_n_inner & 3) == 0 && (p.c_n_outer & 3) == 0));
+    // Configuration kDlpCfg's contract: vector layouts, no fused row sums,
+    // whole 16-deep chunks in every split (kps is a multiple of 16, so
+    // K % 16 == 0 suffices), 16-byte stores to C and to the workspace.
+    const bool wide_ok = dl && !implicit && p.rowsum == nullptr && K > 0 && (K & 15) == 0 &&
+                         p.c_vec && ((uintptr_t)workspace & 15u) == 0;
     Plan plan;
-    if (forced_plan(M, N, K, batch, dl, lb != L_IM && lb != L_IMW, &plan)) {
+    if (forced_plan(M, N, K, batch, dl, !implicit, wide_ok, &plan)) {
         if (plan.splits > 1 && (workspace == nullptr || ws_bytes < plan.ws_bytes))
             return MT_ERR_WORKSPACE;
     } else {
-        plan = make_plan(M, N, K, batch, device_cu_count(), true, dl);
+        plan = make_plan(M, N, K, batch, device_cu_count(), true, dl, wide_ok);
         if (plan.splits > 1 && (workspace == nullptr || ws_bytes < plan.ws_bytes))
-            plan = make_plan(M, N, K, batch, device_cu_count(), false, dl);
+            plan = make_plan(M, N, K, batch, device_cu_count(), false, dl, wide_ok);
     }
     // Row sums of A are fused only into a direct-to-LDS launch of two
     // mn-contiguous operands without split-K (the caller sees p.rowsum cleared
@@ -391,11 +414,6 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
     p.tiles_n = plan.tiles_n;
     p.group_m = 4;
     p.ws = plan.splits > 1 ? static_cast<float*>(workspace) : nullptr;
-    // 16-byte epilogue stores: four consecutive columns must be contiguous,
-    // aligned, and (for a scattered output) never straddle a column group.
-    p.c_vec = p.c_n == 1 && (N & 3) == 0 && ((uintptr_t)p.C & 15u) == 0 && (p.c_m & 3) == 0 &&
-              (batch == 1 || (p.c_b & 3) == 0) &&
-              (p.c_n_inner >= N || ((p.c_n_inner & 3) == 0 && (p.c_n_outer & 3) == 0));
     p.ws_vec = p.ws != nullptr && ((uintptr_t)p.ws & 15u) == 0 && (N & 3) == 0;
 
     const int64_t nblocks = (int64_t)plan.tiles_m * plan.tiles_n * plan.splits * batch;
@@ -409,6 +427,7 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
                       : lb == L_IMW         ? convw_launcher(plan.cfg)
                       : p.rowsum != nullptr ? rowsum_launcher(plan.cfg)
                                             : pick_launcher(plan, la, lb);
+    if (fn == nullptr) return MT_ERR_UNSUPPORTED;
     hipError_t e = fn(p, (unsigned)nblocks, stream);
     if (e == hipErrorStreamCaptureUnsupported) e = hipSuccess;
     if (e != hipSuccess) return MT_ERR_HIP;

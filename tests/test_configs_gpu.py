@@ -20,11 +20,15 @@ from util_parity import amax, assert_close
 
 pytestmark = pytest.mark.gpu
 
-# (family, configuration): 3 register-staged and 4 direct-to-LDS tiles
-# (a CPU test pins these counts against the library).
+# (family, configuration): 3 register-staged and 4 direct-to-LDS tiles that
+# take every operand form; direct-to-LDS configuration 4 (DLP, the
+# prefetching 4-wave 256x256 tile) takes only vector-epilogue GEMMs with
+# K % 16 == 0 and has tests of its own below.  (A CPU test pins the counts
+# against the library.)
 CONFIGS = [(mt.FAMILY_RS, c) for c in range(3)] + [(mt.FAMILY_DL, c) for c in range(4)]
 DL_CONFIGS = [c for f, c in CONFIGS if f == mt.FAMILY_DL]
 IDS = [f"{'rs' if f == mt.FAMILY_RS else 'dl'}{c}" for f, c in CONFIGS]
+DLP = 4
 
 
 def g(a: np.ndarray, dev) -> torch.Tensor:
@@ -189,7 +193,7 @@ def test_forced_split_without_workspace_is_an_error(dev):
     assert rc == mt.MT_ERR_WORKSPACE
 
 
-@pytest.mark.parametrize("fc", CONFIGS, ids=IDS)
+@pytest.mark.parametrize("fc", CONFIGS + [(mt.FAMILY_DL, DLP)], ids=IDS + [f"dl{DLP}"])
 @pytest.mark.parametrize("splits", [1, 4])
 def test_forced_config_special_values(dev, fc, splits):
     # IEEE special values go through every kernel as through matmul_cpu
@@ -221,3 +225,92 @@ def test_forced_config_special_values(dev, fc, splits):
         z = np.zeros((M, K), np.float32) * -1.0                  # -0.0 operands
         got = sync_np(mt.gemm(g(z, dev), g(np.ones((K, N), np.float32), dev)))
         np.testing.assert_array_equal(np.signbit(got), np.signbit(oracle.matmul(z, np.ones((K, N), np.float32))))
+
+
+def expected_splits(K: int, asked: int) -> int:
+    kps = -(-(-(-K // asked)) // 16) * 16
+    return -(-K // kps)
+
+
+@pytest.mark.parametrize("splits", [1, 3])
+@pytest.mark.parametrize("la", ["row", "col"])
+@pytest.mark.parametrize("lb", ["row", "col"])
+@pytest.mark.parametrize("M,N,K", [(300, 264, 96), (260, 260, 16), (512, 256, 48),
+                                   (1000, 1020, 272)])
+def test_forced_dlp_layouts(dev, splits, la, lb, M, N, K):
+    # The prefetching kernel on every vector layout: ragged M and N (clamped
+    # loads, masked stores), 1, 2, 3 (odd: the unrolled loop's last step) and
+    # 17 chunks per split, a single tile and a 4x4 grid.
+    a = oracle.uniform((M, K), 1100 + K)
+    b = oracle.uniform((K, N), 1200 + K)
+    A, B = operand(a, la, dev), operand(b, lb, dev)
+    with mt.forced_config(mt.FAMILY_DL, DLP, splits):
+        C = mt.gemm(A, B)
+        check_config(mt.FAMILY_DL, DLP, expected_splits(K, splits))
+    assert_close(sync_np(C), oracle.matmul(a, b), K, amax(a), amax(b),
+                 f"forced dl{DLP} split {splits} a={la} b={lb} {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("splits", [1, 2])
+@pytest.mark.parametrize("axis", [mt.BIAS_ROW, mt.BIAS_COL])
+def test_forced_dlp_batched_bias_beta(dev, splits, axis):
+    batch, M, N, K = 3, 96, 72, 64
+    a = oracle.uniform((batch, M, K), 1300)
+    b = oracle.uniform((batch, K, N), 1400)
+    c0 = oracle.uniform((batch, M, N), 1500)
+    bias = oracle.uniform((M if axis == mt.BIAS_ROW else N,), 1600)
+    C = g(c0, dev)
+    with mt.forced_config(mt.FAMILY_DL, DLP, splits):
+        mt.gemm(g(a, dev), g(b, dev), out=C, bias=g(bias, dev), bias_axis=axis, beta=0.5)
+        check_config(mt.FAMILY_DL, DLP, splits)
+    bb = bias[None, :, None] if axis == mt.BIAS_ROW else bias[None, None, :]
+    want = oracle.bmm(a, b) + bb + 0.5 * c0
+    assert_close(sync_np(C), want, K, amax(a), amax(b),
+                 f"forced dl{DLP} batched bias {axis} beta", extra=2e-6)
+
+
+def test_forced_dlp_strided_output_view(dev):
+    # A row slice of a wider, 16-byte-aligned buffer (row stride 264 > N):
+    # vector stores through c_m, neighbours untouched.
+    M, N, K = 130, 256, 32
+    a = oracle.uniform((M, K), 1700)
+    b = oracle.uniform((K, N), 1701)
+    wide = torch.zeros(M, N + 8, device=dev)
+    with mt.forced_config(mt.FAMILY_DL, DLP, 1):
+        mt.gemm(g(a, dev), g(b, dev), out=wide[:, 4:4 + N])
+        check_config(mt.FAMILY_DL, DLP, 1)
+    got = sync_np(wide)
+    assert_close(got[:, 4:4 + N], oracle.matmul(a, b), K, amax(a), amax(b), "dlp strided out")
+    assert not got[:, :4].any() and not got[:, 4 + N:].any(), "wrote outside the view"
+
+
+def _not_dlp(name: str) -> None:
+    print(f"[config] {name}", flush=True)
+    assert not (name.startswith("dl ") and name.endswith(f" cfg={DLP}")), name
+
+
+def test_forced_dlp_outside_its_contract_uses_the_cost_model(dev):
+    # Forced configuration 4 where its contract does not hold: the launch
+    # takes the cost model's plan instead, and the result is still exact.
+    cases = [(128, 128, 76, 0), (128, 130, 64, 0), (128, 128, 64, 1)]   # K tail, N % 4, misaligned C
+    for M, N, K, off in cases:
+        a = oracle.uniform((M, K), 1800 + K)
+        b = oracle.uniform((K, N), 1900 + N)
+        buf = torch.zeros(M * N + off, device=dev)
+        C = buf[off:].view(M, N)
+        with mt.forced_config(mt.FAMILY_DL, DLP, 1):
+            mt.gemm(g(a, dev), g(b, dev), out=C)
+            _not_dlp(mt.last_config())
+        assert_close(sync_np(C), oracle.matmul(a, b), K, amax(a), amax(b), f"fallback {M}x{N}x{K}+{off}")
+    # the Linear weight gradient with its fused row sums keeps a row-sum kernel
+    x = oracle.normal((301, 96), 2000)
+    w = oracle.normal((72, 96), 2001, std=0.1)
+    dy = oracle.normal((301, 72), 2002, std=0.1)
+    dw = torch.empty(72, 96, device=dev)
+    db = torch.empty(72, device=dev)
+    with mt.forced_config(mt.FAMILY_DL, DLP, 1):
+        mt.linear_backward(g(dy, dev), g(x, dev), g(w, dev), need_dx=False, dw=dw, db=db)
+        _not_dlp(mt.last_config())
+    _, wdw, wdb = oracle.linear_backward(dy, x, w)
+    assert_close(sync_np(dw), wdw, 301, amax(dy), amax(x), "dlp fallback dW")
+    assert_close(sync_np(db), wdb, 301, amax(dy), 1.0, "dlp fallback db")
