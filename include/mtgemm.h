@@ -203,8 +203,7 @@ int mt_gemm_config_count(int family);
  * thread whose operands that family takes; the others keep the cost model.
  * (Direct-to-LDS configuration 4, the prefetching 4-wave 256x256 tile, takes
  * only GEMMs without implicit-im2col operands or fused row sums, with
- * K % 16 == 0 and 16-byte output rows: N % 4 == 0, aligned, unit column
- * stride.)
+ * K % 16 == 0.)
  * MT_FAMILY_AUTO clears it.  While it is set, workspace queries include its
  * split-K partials and a launch given less returns MT_ERR_WORKSPACE.
  * Returns MT_ERR_INVALID for an unknown family, configuration or split count. */

@@ -48,8 +48,8 @@ template <> struct DlCfg<2> { static constexpr int BM = 64, BN = 64, WM = 32, WN
 // (e.g. convolutions with 256 output channels: 49 tiles x split 5 = 245).
 template <> struct DlCfg<3> { static constexpr int BM = 256, BN = 128, WM = 64, WN = 64, STAGES = 2; };
 // 4 waves of 128x128 (one per SIMD) with fragment prefetch: the separate
-// kernel gemm_f32_dlp (gemm_dlp_kernel.hpp).  Vector layouts, whole 16-deep
-// K chunks and a vector epilogue only; no implicit-im2col or row-sum form.
+// kernel gemm_f32_dlp (gemm_dlp_kernel.hpp).  Vector layouts and whole
+// 16-deep K chunks only; no implicit-im2col or row-sum form.
 template <> struct DlCfg<4> { static constexpr int BM = 256, BN = 256, WM = 128, WN = 128, STAGES = 2; };
 
 constexpr int kNumDlCfg = 5;

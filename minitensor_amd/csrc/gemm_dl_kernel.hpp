@@ -309,9 +309,6 @@ __device__ __forceinline__ void dl_frag(const float* tile, int row0, int lane, f
     }
 }
 
-// s_waitcnt immediate (gfx9 encoding): vmcnt(n), lgkmcnt(0), expcnt unconstrained.
-constexpr int waitcnt_vm_lgkm0(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4); }
-
 template <int MB, int NB>
 __device__ __forceinline__ void mfma_chunk(f32x16 (&acc)[MB][NB], const float (&fa)[MB][8],
                                            const float (&fb)[NB][8]) {
@@ -464,7 +461,8 @@ gemm_f32_dl(GemmParams p) {
         }
     }
 
-    store_tile<MB, NB>(p, acc, m0 + ra, n0 + rb, lane, id.split, id.bz);
+    store_tile_lds<MB, NB, NW, WAVES_N, WM, WN, STAGES * STAGE>(p, acc, smem, m0, n0, wave, lane,
+                                                               id.split, id.bz);
 }
 
 }  // namespace mtk

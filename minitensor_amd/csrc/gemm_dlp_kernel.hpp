@@ -20,54 +20,15 @@
 //     refills with chunk kt+STAGES.  Refills past the last chunk re-fetch the
 //     last chunk (always in bounds) into slots nobody reads again, so the DMA
 //     count per step, and hence every vmcnt, is the same on every step.
-// Host contract (checked in the dispatcher): operand layouts L_KV / L_MV,
-// every split's K range a whole number (>= 1) of 16-deep chunks, and a vector
-// epilogue (c_vec; ws_vec with split-K).  Rows or columns beyond M or N read
-// clamped, valid rows, as in gemm_f32_dl.
+//   * The epilogue is store_tile_lds, as in gemm_f32_dl.
+// Host contract (checked in the dispatcher): operand layouts L_KV / L_MV and
+// every split's K range a whole number (>= 1) of 16-deep chunks.  Rows or
+// columns beyond M or N read clamped, valid rows, as in gemm_f32_dl.
 #pragma once
 
 #include "gemm_dl_kernel.hpp"
 
 namespace mtk {
-
-// Epilogue with the 16-byte forms of store_tile only, written as one path for
-// both destinations: a split-K partial is the same store into the workspace
-// with bias and beta switched off.  (Separate paths make the compiler copy the
-// 256 accumulators out of their registers before the branch.)
-template <int MB, int NB>
-__device__ __forceinline__ void store_tile_vec(const GemmParams& p, const f32x16 (&acc)[MB][NB],
-                                               int mw0, int nw0, int lane, int split, int bz) {
-    const int h = lane >> 5, c = lane & 31;
-    const bool part = p.splits > 1;
-    float* const base = part ? p.ws + ((int64_t)split * p.batch + bz) * (int64_t)p.M * p.N
-                             : p.C + (int64_t)bz * p.c_b;
-    const int64_t rs = part ? (int64_t)p.N : p.c_m;
-    const int bias_axis = part ? 0 : p.bias_axis;
-    const float beta = part ? 0.f : p.beta;
-#pragma unroll
-    for (int i = 0; i < MB; ++i) {
-        const int m = mw0 + i * 32 + c;
-        if (m >= p.M) continue;
-        float* const Cr = base + (int64_t)m * rs;
-        const float brow = bias_axis == 1 ? p.bias[(int64_t)m * p.bias_stride] : 0.f;
-#pragma unroll
-        for (int j = 0; j < NB; ++j)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int n = nw0 + j * 32 + 8 * q + 4 * h;
-                if (n >= p.N) continue;
-                f32x4 o;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    o[e] = acc[i][j][4 * q + e] + brow;
-                    if (bias_axis == 2) o[e] += p.bias[(int64_t)(n + e) * p.bias_stride];
-                }
-                f32x4* const dst = reinterpret_cast<f32x4*>(Cr + (part ? (int64_t)n : col_offset(p, n)));
-                if (beta != 0.f) o += beta * *dst;
-                *dst = o;
-            }
-    }
-}
 
 // Spread one step's instructions over its 128 MFMAs: the DMA of the refill
 // (up to 8 wave instructions) first, one per MFMA, then the fragment reads of
@@ -179,10 +140,9 @@ gemm_f32_dlp(GemmParams p) {
             for (int s = 0; s < 8; ++s) fb0[j][s] = fb1[j][s];
     }
     mfma_chunk<MB, NB>(acc, fa0, fb0);
-    // The re-fetches past the last chunk may still be landing in LDS.
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
-
-    store_tile_vec<MB, NB>(p, acc, m0 + ra, n0 + rb, lane, id.split, id.bz);
+    // (store_tile_lds first waits for the re-fetches past the last chunk.)
+    store_tile_lds<MB, NB, NW, 2, WM, WN, STAGES * STAGE>(p, acc, smem, m0, n0, wave, lane, id.split,
+                                                          id.bz);
 }
 
 }  // namespace mtk

@@ -31,7 +31,8 @@
 //        D: lane l, register r holds D[8*(r/4) + 4*(l/32) + r%4][l%32].
 //     The kernels pass B's fragment as src0 and A's as src1, i.e. they
 //     accumulate the transposed block, so each lane owns four consecutive
-//     columns of one output row per register quad (16-byte stores).
+//     columns of one output row per register quad (one 16-byte LDS write
+//     when the epilogue stages the tile, store_tile_lds).
 //   * Work decomposition: one workgroup per (tile, split, batch) in a 1-D grid.
 //     Consecutive workgroup ids are dealt round-robin to the 8 XCDs, so ids
 //     are remapped to give each XCD a contiguous range of tiles, which are
@@ -237,7 +238,7 @@ __device__ __forceinline__ TileId tile_id(const GemmParams& p) {
 // block and lane l, register r holds C(m, n) with
 //     m = m_blk + l%32,   n = n_blk + 8*(r/4) + 4*(l/32) + r%4.
 // Registers 4q..4q+3 of a lane are four consecutive columns of one row: the
-// epilogue stores them as one 16-byte vector when the output allows it.
+// epilogue writes them to LDS as one 16-byte group.
 __device__ __forceinline__ f32x16 mfma_32x32x2(float a, float b, const f32x16& c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(b, a, c, 0, 0, 0);
 }
@@ -249,92 +250,145 @@ __device__ __forceinline__ int64_t col_offset(const GemmParams& p, int n) {
     return no * p.c_n_outer + ni * p.c_n;
 }
 
-// Epilogue of one wave: (MB x NB) 32x32 accumulators whose first element is
-// C(mw0, nw0).  With split-K the raw partial goes to the workspace; otherwise
-// bias and beta*C are applied and the column index is scattered through
-// col(n).  Each lane holds groups of four consecutive columns of one row.
-// When the host has established that every group is a whole, aligned,
-// contiguous 16-byte run (ws_vec / c_vec, which imply N % 4 == 0) a group is
-// one vector store; otherwise every element is stored on its own.  The two
-// variants are separate loops so the compiler never keeps both live.
-template <int MB, int NB>
-__device__ __forceinline__ void store_tile(const GemmParams& p, const f32x16 (&acc)[MB][NB],
-                                           int mw0, int nw0, int lane, int split, int bz) {
-    const int h = lane >> 5, c = lane & 31;
-    if (p.splits > 1) {
-        float* W = p.ws + ((int64_t)split * p.batch + bz) * (int64_t)p.M * p.N;
-#pragma unroll
-        for (int i = 0; i < MB; ++i) {
-            const int m = mw0 + i * 32 + c;
-            if (m >= p.M) continue;
-            float* Wr = W + (int64_t)m * p.N;
-#pragma unroll
-            for (int j = 0; j < NB; ++j)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int n = nw0 + j * 32 + 8 * q + 4 * h;
-                    if (p.ws_vec) {
-                        if (n < p.N) {
-                            const f32x4 v = {acc[i][j][4 * q], acc[i][j][4 * q + 1],
-                                             acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-                            *reinterpret_cast<f32x4*>(Wr + n) = v;
-                        }
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            if (n + e < p.N) Wr[n + e] = acc[i][j][4 * q + e];
-                    }
-                }
-        }
-        return;
-    }
+// s_waitcnt immediate (gfx9 encoding): vmcnt(n), lgkmcnt(0), expcnt unconstrained.
+constexpr int waitcnt_vm_lgkm0(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4); }
 
-    float* Cb = p.C + (int64_t)bz * p.c_b;
-    if (p.c_vec) {
+// ---- Epilogue through LDS ---------------------------------------------------
+// The accumulators leave through LDS, one pass per (block row i, group of JP
+// block columns): every wave writes its JP 32x32 blocks acc[i][j0..j0+JP-1]
+// as 16-byte groups, then all threads store the staged rows, four consecutive
+// columns per thread and consecutive threads along a row (32*JP floats of a
+// row are contiguous in C).  The store loop is not unrolled, so the whole
+// epilogue -- bounds, bias, beta, split-K partials, scattered columns and the
+// element-wise form -- stays a few hundred instructions: a fully unrolled
+// epilogue over 128-256 accumulator registers is 30-200 KB of code that runs
+// once per tile, every line of it an instruction-cache miss.
+//
+// Staged row r of a wave block is RG = 8*JP groups of 16 bytes; group g sits
+// at g ^ stage_swz(r).  A ds_write_b128 covers rows c = 0..15 at one group
+// (lanes 0-15) per LDS cycle: for RG >= 16 the XOR with r & 15 spreads them
+// over all 16 four-bank groups; for RG == 8 rows 2 apart differ by 8 groups
+// and the XOR with (r >> 1) & 7 separates the rest.
+template <int RG>
+__device__ __forceinline__ int stage_swz(int r) {
+    if constexpr (RG >= 16) return r & 15;
+    else return (r >> 1) & 7;
+}
+
+// Block columns per pass: the most (dividing NB) whose staging fits the ring.
+template <int NB, int NW, int RING>
+constexpr int stage_blocks() {
+    int jp = NB;
+    while (jp > 1 && 1024 * NW * jp > RING) jp /= 2;
+    return jp;
+}
+
+// Epilogue of a workgroup of NW waves (wave tiles WM x WN, WAVES_N per tile
+// row) whose first output element is (m0, n0).  `lds` is the kernel's ring of
+// RING floats; the main loop must be finished with it (the first pass waits
+// for every wave's outstanding DMA and LDS reads before writing).  Writes
+// C(m, n) = acc + bias + beta*C, or the raw partial into split `split`'s
+// workspace slab.
+template <int MB, int NB, int NW, int WAVES_N, int WM, int WN, int RING>
+__device__ __forceinline__ void store_tile_lds(const GemmParams& p, const f32x16 (&acc)[MB][NB],
+                                               float* lds, int m0, int n0, int wave, int lane,
+                                               int split, int bz) {
+    constexpr int NT = NW * 64;
+    constexpr int JP = stage_blocks<NB, NW, RING>();
+    static_assert(1024 * NW * JP <= RING, "the staging must fit the ring");
+    constexpr int RG = 8 * JP;
+    constexpr int PER = 4 * JP;   // 16-byte groups per thread per pass
+    constexpr int U = 4;
+    const int t = threadIdx.x;
+    const int h = lane >> 5, c = lane & 31;
+    const bool part = p.splits > 1;
+    float* const base = part ? p.ws + ((int64_t)split * p.batch + bz) * (int64_t)p.M * p.N
+                             : p.C + (int64_t)bz * p.c_b;
+    const int64_t rs = part ? (int64_t)p.N : p.c_m;
+    const int bias_axis = part ? 0 : p.bias_axis;
+    const float beta = part ? 0.f : p.beta;
+    const bool vec = part ? p.ws_vec : p.c_vec;
+    // 16-byte stores of the bare sums to unscattered columns: the common case,
+    // with a loop of its own that batches its LDS reads.
+    const bool plain = vec && bias_axis == 0 && beta == 0.f && (part || p.c_n_inner >= p.N);
+    f32x4* const sl = reinterpret_cast<f32x4*>(lds);
+    // Every wave's DMA has landed and its fragment reads are done before any
+    // wave overwrites the ring.
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
 #pragma unroll
-        for (int i = 0; i < MB; ++i) {
-            const int m = mw0 + i * 32 + c;
-            if (m >= p.M) continue;
-            float* Cr = Cb + (int64_t)m * p.c_m;
-            const float brow = (p.bias_axis == 1) ? p.bias[(int64_t)m * p.bias_stride] : 0.f;
+    for (int i = 0; i < MB; ++i)
 #pragma unroll
-            for (int j = 0; j < NB; ++j)
+        for (int j0 = 0; j0 < NB; j0 += JP) {
+            __syncthreads();
+#pragma unroll
+            for (int jj = 0; jj < JP; ++jj)
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    const int n = nw0 + j * 32 + 8 * q + 4 * h;
-                    if (n >= p.N) continue;
+                    const int g = 8 * jj + 2 * q + h;
+                    const f32x4 v = {acc[i][j0 + jj][4 * q], acc[i][j0 + jj][4 * q + 1],
+                                     acc[i][j0 + jj][4 * q + 2], acc[i][j0 + jj][4 * q + 3]};
+                    sl[(wave * 32 + c) * RG + (g ^ stage_swz<RG>(c))] = v;
+                }
+            __syncthreads();
+            auto where = [&](int k, int* m, int* n, int* idx) {
+                const int e = k * NT + t;
+                const int w = e / (32 * RG), r = (e / RG) & 31, g = e % RG;
+                *idx = (w * 32 + r) * RG + (g ^ stage_swz<RG>(r));
+                *m = m0 + (w / WAVES_N) * WM + 32 * i + r;
+                *n = n0 + (w % WAVES_N) * WN + 32 * j0 + 4 * g;
+            };
+            if (plain) {
+                // U groups per iteration, their LDS reads issued together
+#pragma unroll 1
+                for (int k0 = 0; k0 < PER; k0 += U) {
+                    f32x4 vs[U];
+                    int ms[U], ns[U];
+#pragma unroll
+                    for (int u = 0; u < U; ++u) {
+                        int idx;
+                        where(k0 + u, &ms[u], &ns[u], &idx);
+                        vs[u] = sl[idx];
+                    }
+#pragma unroll
+                    for (int u = 0; u < U; ++u)
+                        if (ms[u] < p.M && ns[u] < p.N)
+                            *reinterpret_cast<f32x4*>(base + (int64_t)ms[u] * rs + ns[u]) =
+                                vs[u] + 0.f;
+                }
+                continue;
+            }
+#pragma unroll 1
+            for (int k = 0; k < PER; ++k) {
+                int m, n, idx;
+                where(k, &m, &n, &idx);
+                const f32x4 v = sl[idx];
+                if (m >= p.M || n >= p.N) continue;
+                float* const row = base + (int64_t)m * rs;
+                const float brow = bias_axis == 1 ? p.bias[(int64_t)m * p.bias_stride] : 0.f;
+                if (vec) {
                     f32x4 o;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        o[e] = acc[i][j][4 * q + e] + brow;
-                        if (p.bias_axis == 2) o[e] += p.bias[(int64_t)(n + e) * p.bias_stride];
+                    for (int x = 0; x < 4; ++x) {
+                        o[x] = v[x] + brow;
+                        if (bias_axis == 2) o[x] += p.bias[(int64_t)(n + x) * p.bias_stride];
                     }
-                    f32x4* dst = reinterpret_cast<f32x4*>(Cr + col_offset(p, n));
-                    if (p.beta != 0.f) o += p.beta * *dst;
+                    f32x4* const dst =
+                        reinterpret_cast<f32x4*>(row + (part ? (int64_t)n : col_offset(p, n)));
+                    if (beta != 0.f) o += beta * *dst;
                     *dst = o;
+                } else {
+#pragma unroll
+                    for (int x = 0; x < 4; ++x) {
+                        if (n + x >= p.N) break;
+                        float o = v[x] + brow;
+                        if (bias_axis == 2) o += p.bias[(int64_t)(n + x) * p.bias_stride];
+                        float* const dst = row + (part ? (int64_t)(n + x) : col_offset(p, n + x));
+                        if (beta != 0.f) o += beta * *dst;
+                        *dst = o;
+                    }
                 }
-        }
-        return;
-    }
-#pragma unroll
-    for (int i = 0; i < MB; ++i) {
-        const int m = mw0 + i * 32 + c;
-        if (m >= p.M) continue;
-        float* Cr = Cb + (int64_t)m * p.c_m;
-        const float brow = (p.bias_axis == 1) ? p.bias[(int64_t)m * p.bias_stride] : 0.f;
-#pragma unroll
-        for (int j = 0; j < NB; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int n = nw0 + j * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                if (n >= p.N) continue;
-                float o = acc[i][j][r] + brow;
-                if (p.bias_axis == 2) o += p.bias[(int64_t)n * p.bias_stride];
-                float* dst = Cr + col_offset(p, n);
-                if (p.beta != 0.f) o += p.beta * *dst;
-                *dst = o;
             }
-    }
+        }
 }
 
 // MINW: minimum resident waves per SIMD the register allocation must allow
@@ -422,7 +476,9 @@ gemm_f32_mfma(GemmParams p) {
         }
     }
 
-    store_tile<MB, NB>(p, acc, m0 + wm * WM, n0 + wn * WN, lane, split, bz);
+    store_tile_lds<MB, NB, (BM / WM) * WAVES_N, WAVES_N, WM, WN,
+                   2 * (GA::lds_floats + GB::lds_floats)>(p, acc, smem, m0, n0, wave, lane, split,
+                                                          bz);
 }
 
 }  // namespace mtk

@@ -391,9 +391,8 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
               (p.c_n_inner >= N || ((p.c_n_inner & 3) == 0 && (p.c_n_outer & 3) == 0));
     // Configuration kDlpCfg's contract: vector layouts, no fused row sums,
     // whole 16-deep chunks in every split (kps is a multiple of 16, so
-    // K % 16 == 0 suffices), 16-byte stores to C and to the workspace.
-    const bool wide_ok = dl && !implicit && p.rowsum == nullptr && K > 0 && (K & 15) == 0 &&
-                         p.c_vec && ((uintptr_t)workspace & 15u) == 0;
+    // K % 16 == 0 suffices).
+    const bool wide_ok = dl && !implicit && p.rowsum == nullptr && K > 0 && (K & 15) == 0;
     Plan plan;
     if (forced_plan(M, N, K, batch, dl, !implicit, wide_ok, &plan)) {
         if (plan.splits > 1 && (workspace == nullptr || ws_bytes < plan.ws_bytes))

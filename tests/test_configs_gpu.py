@@ -289,19 +289,44 @@ def _not_dlp(name: str) -> None:
     assert not (name.startswith("dl ") and name.endswith(f" cfg={DLP}")), name
 
 
+@pytest.mark.parametrize("splits", [1, 3])
+def test_forced_dlp_scalar_and_misaligned_outputs(dev, splits):
+    # N % 4 != 0 (element-wise stores and element-wise split-K partials; B is
+    # k-contiguous so it stays a vector layout) and a C that starts 4 bytes
+    # past a 16-byte boundary, with bias and beta.
+    for M, N, K, off in [(300, 270, 96, 0), (260, 256, 48, 1)]:
+        a = oracle.uniform((M, K), 1800 + N)
+        b = oracle.uniform((K, N), 1900 + N)
+        bias = oracle.uniform((N,), 1950 + N)
+        c0 = oracle.uniform((M, N), 1960 + N)
+        buf = torch.zeros(M * N + off, device=dev)
+        C = buf[off:].view(M, N)
+        C.copy_(g(c0, dev))
+        with mt.forced_config(mt.FAMILY_DL, DLP, splits):
+            mt.gemm(g(a, dev), operand(b, "col", dev), out=C, bias=g(bias, dev),
+                    bias_axis=mt.BIAS_COL, beta=-1.5)
+            check_config(mt.FAMILY_DL, DLP, expected_splits(K, splits))
+        want = oracle.matmul(a, b) + bias[None, :] - 1.5 * c0
+        assert_close(sync_np(C), want, K, amax(a), amax(b), f"dlp {M}x{N}x{K}+{off}", extra=2e-6)
+        if off:
+            assert sync_np(buf)[0] == 0, "wrote before the output"
+
+
+def _not_dlp(name: str) -> None:
+    print(f"[config] {name}", flush=True)
+    assert not (name.startswith("dl ") and name.endswith(f" cfg={DLP}")), name
+
+
 def test_forced_dlp_outside_its_contract_uses_the_cost_model(dev):
     # Forced configuration 4 where its contract does not hold: the launch
     # takes the cost model's plan instead, and the result is still exact.
-    cases = [(128, 128, 76, 0), (128, 130, 64, 0), (128, 128, 64, 1)]   # K tail, N % 4, misaligned C
-    for M, N, K, off in cases:
-        a = oracle.uniform((M, K), 1800 + K)
-        b = oracle.uniform((K, N), 1900 + N)
-        buf = torch.zeros(M * N + off, device=dev)
-        C = buf[off:].view(M, N)
-        with mt.forced_config(mt.FAMILY_DL, DLP, 1):
-            mt.gemm(g(a, dev), g(b, dev), out=C)
-            _not_dlp(mt.last_config())
-        assert_close(sync_np(C), oracle.matmul(a, b), K, amax(a), amax(b), f"fallback {M}x{N}x{K}+{off}")
+    M, N, K = 128, 128, 76                     # K tail
+    a = oracle.uniform((M, K), 2100)
+    b = oracle.uniform((K, N), 2101)
+    with mt.forced_config(mt.FAMILY_DL, DLP, 1):
+        C = mt.gemm(g(a, dev), g(b, dev))
+        _not_dlp(mt.last_config())
+    assert_close(sync_np(C), oracle.matmul(a, b), K, amax(a), amax(b), "fallback K tail")
     # the Linear weight gradient with its fused row sums keeps a row-sum kernel
     x = oracle.normal((301, 96), 2000)
     w = oracle.normal((72, 96), 2001, std=0.1)
