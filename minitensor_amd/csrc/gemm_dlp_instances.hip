@@ -1,27 +1,30 @@
-// gemm_dlp_instances.hip -- instantiates gemm_f32_dlp (direct-to-LDS, one
-// 128x128 wave tile per SIMD, fragment prefetch) for the 2x2 vector operand
-// layouts: direct-to-LDS tile configuration kDlpCfg.
+// gemm_dlp_instances.hip -- instantiates gemm_f32_dlp (direct-to-LDS with
+// fragment prefetch) for direct-to-LDS configurations 4 and 5 and the 2x2
+// vector operand layouts.
 #include "gemm_configs.hpp"
 #include "gemm_dlp_kernel.hpp"
 
 namespace mtk {
 namespace {
 
-template <int LA, int LB>
+template <int CFG, int LA, int LB>
 hipError_t launch_dlp(const GemmParams& p, unsigned nblocks, hipStream_t s) {
-    using C = DlCfg<kDlpCfg>;
-    hipLaunchKernelGGL((gemm_f32_dlp<LA, LB, C::STAGES>), dim3(nblocks),
-                       dim3(dl_threads<kDlpCfg>()), 0, s, p);
+    using C = DlCfg<CFG>;
+    hipLaunchKernelGGL((gemm_f32_dlp<C::BM, C::BN, C::WM, C::WN, LA, LB, C::STAGES, C::WPE>),
+                       dim3(nblocks), dim3(dl_threads<CFG>()), 0, s, p);
     return hipGetLastError();
 }
 
+#define MT_DLP_TABLE(CFG) \
+    { { launch_dlp<CFG, L_KV, L_KV>, launch_dlp<CFG, L_KV, L_MV> }, \
+      { launch_dlp<CFG, L_MV, L_KV>, launch_dlp<CFG, L_MV, L_MV> } }
+
 }  // namespace
 
-GemmLaunchFn dlp_launcher(int la, int lb) {
-    static const GemmLaunchFn table[2][2] = {
-        {launch_dlp<L_KV, L_KV>, launch_dlp<L_KV, L_MV>},
-        {launch_dlp<L_MV, L_KV>, launch_dlp<L_MV, L_MV>}};
-    return table[la][lb];
+GemmLaunchFn dlp_launcher(int cfg, int la, int lb) {
+    static const GemmLaunchFn table4[2][2] = MT_DLP_TABLE(4);
+    static const GemmLaunchFn table5[2][2] = MT_DLP_TABLE(5);
+    return cfg == 4 ? table4[la][lb] : table5[la][lb];
 }
 
 }  // namespace mtk

@@ -1,19 +1,23 @@
-// gemm_dlp_kernel.hpp -- direct-to-LDS fp32 MFMA GEMM with one 128x128 wave
-// tile per SIMD and its fragments prefetched a chunk ahead.
+// gemm_dlp_kernel.hpp -- direct-to-LDS fp32 MFMA GEMM whose waves read the
+// next K-chunk's fragments while the current chunk's MFMAs issue.
 //
-// The 256x256 block tile of gemm_f32_dl's first configuration, computed by
-// four waves instead of eight:
-//   * Each wave owns a 128x128 accumulator tile (4 x 4 MFMA blocks, 256
-//     accumulator registers), so a SIMD runs one wave.  Per 16-deep K-chunk a
-//     wave reads 16 KB of fragments from LDS for 128 MFMAs, against 12 KB for
-//     64 MFMAs with 128x64 wave tiles: two thirds of the LDS read traffic per
-//     flop.
+// Two instantiations (direct-to-LDS configurations 4 and 5):
+//   * 256x256 block tile, four waves of 128x128 (one wave per SIMD, 256
+//     accumulator registers).  Per 16-deep K-chunk a wave reads 16 KB of
+//     fragments from LDS for 128 MFMAs, against 12 KB for 64 MFMAs with the
+//     8-wave 128x64 split of gemm_f32_dl: two thirds of the LDS read traffic
+//     per flop.  The headline kernel.
+//   * 64x64 block tile, four waves of 32x32: the small GEMMs that run about
+//     one workgroup per CU, where each SIMD again holds a single wave and the
+//     fragment-read latency after every barrier is exposed.
+// Structure:
 //   * With no second wave on the SIMD to cover the LDS latency, chunk kt+1's
 //     fragments are read while chunk kt's MFMAs issue: two register sets
 //     alternate (the loop is unrolled by two so that each set is a fixed set
 //     of registers).  The body has no branches, so the scheduler can spread
 //     the fragment reads and the next DMA over the MFMA stream (the
-//     sched_group_barrier pattern in dlp_interleave).
+//     sched_group_barrier pattern in dlp_interleave, used by the 256x256
+//     tile; the 64x64 tile's 8 MFMAs per step leave nothing to spread).
 //   * Ring of STAGES LDS slots, one s_barrier per chunk.  At the barrier of
 //     step kt, chunk kt+1 has landed (each wave waited for its own DMA) and
 //     every wave has retired its reads of chunk kt's slot, which the step then
@@ -50,10 +54,14 @@ __device__ __forceinline__ void dlp_interleave() {
     __builtin_amdgcn_sched_group_barrier(kMfma, 128, 0);
 }
 
-template <int LA, int LB, int STAGES>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+// WPE: waves per SIMD the register allocation targets (1 lets the 128x128
+// wave tile keep its 256 accumulators in AGPRs beside 256 VGPRs).
+template <int BM, int BN, int WM, int WN, int LA, int LB, int STAGES, int WPE>
+__global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64)
+__attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 gemm_f32_dlp(GemmParams p) {
-    constexpr int BM = 256, BN = 256, WM = 128, WN = 128, NW = 4;
+    constexpr int WAVES_N = BN / WN;
+    constexpr int NW = (BM / WM) * WAVES_N;
     constexpr int MB = WM / 32, NB = WN / 32;
     static_assert(STAGES >= 2, "the ring needs at least two slots");
     static_assert((LA == L_KV || LA == L_MV) && (LB == L_KV || LB == L_MV),
@@ -68,7 +76,7 @@ gemm_f32_dlp(GemmParams p) {
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const int ra = (wave >> 1) * WM, rb = (wave & 1) * WN;
+    const int ra = (wave / WAVES_N) * WM, rb = (wave % WAVES_N) * WN;
 
     const TileId id = tile_id(p);
     const int m0 = id.tm * BM, n0 = id.tn * BN;
@@ -117,7 +125,7 @@ gemm_f32_dlp(GemmParams p) {
         dl_frags<LA, BM, MB>(next, ra, lane, na);
         dl_frags<LB, BN, NB>(next + TA::floats, rb, lane, nb);
         mfma_chunk<MB, NB>(acc, ca, cb);
-        dlp_interleave();
+        if constexpr (MB * NB * 8 >= 128) dlp_interleave();
     };
 
     int kt = 0;
@@ -141,8 +149,8 @@ gemm_f32_dlp(GemmParams p) {
     }
     mfma_chunk<MB, NB>(acc, fa0, fb0);
     // (store_tile_lds first waits for the re-fetches past the last chunk.)
-    store_tile_lds<MB, NB, NW, 2, WM, WN, STAGES * STAGE>(p, acc, smem, m0, n0, wave, lane, id.split,
-                                                          id.bz);
+    store_tile_lds<MB, NB, NW, WAVES_N, WM, WN, STAGES * STAGE>(p, acc, smem, m0, n0, wave, lane,
+                                                                id.split, id.bz);
 }
 
 }  // namespace mtk

@@ -125,7 +125,8 @@ constexpr CfgCost kDlCost[kNumDlCfg] = {    // direct-to-LDS kernel, vector layo
     {DlCfg<1>::BM, DlCfg<1>::BN, 0.86, 4},
     {DlCfg<2>::BM, DlCfg<2>::BN, 0.68, 8},
     {DlCfg<3>::BM, DlCfg<3>::BN, 0.87, 3},
-    {DlCfg<4>::BM, DlCfg<4>::BN, 0.93, 1}};
+    {DlCfg<4>::BM, DlCfg<4>::BN, 0.93, 1},
+    {DlCfg<5>::BM, DlCfg<5>::BN, 0.72, 8}};
 struct CostModel {
     double round_latency = 6200.0;           // cycles of fill/drain per round
     double epilogue_bytes_per_cycle = 7.9;   // one workgroup's tile store
@@ -153,8 +154,8 @@ Plan cfg_plan(const CfgCost& cc, int cfg, bool dl, int64_t M, int64_t N, int64_t
     return pl;
 }
 
-// wide: the direct-to-LDS configuration kDlpCfg may be chosen (see
-// wide_ok in launch_gemm).
+// wide: the prefetching direct-to-LDS configurations (is_dlp_cfg) may be
+// chosen (see wide_ok in launch_gemm).
 Plan make_plan_uncached(int64_t M, int64_t N, int64_t K, int64_t batch, int cus,
                         bool allow_split, bool dl, bool wide) {
     static const CostModel cm;
@@ -164,7 +165,7 @@ Plan make_plan_uncached(int64_t M, int64_t N, int64_t K, int64_t batch, int cus,
     best.dl = dl;
     double best_t = 1e300;
     for (int cfg = 0; cfg < ncfg; ++cfg) {
-        if (dl && cfg == kDlpCfg && !wide) continue;
+        if (dl && is_dlp_cfg(cfg) && !wide) continue;
         const CfgCost& cc = cfgs[cfg];
         for (int s = 1; s <= kMaxSplits; ++s) {
             if (s > 1 && !allow_split) break;
@@ -227,12 +228,12 @@ thread_local ForcedConfig g_forced;
 
 // The plan of the forced configuration, when one is set and its family can
 // take these operands (dl_ok: both operands have direct-to-LDS layouts;
-// rs_ok: no implicit-im2col operand; wide_ok: configuration kDlpCfg can take
-// them too).
+// rs_ok: no implicit-im2col operand; wide_ok: the prefetching configurations
+// can take them too).
 bool forced_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dl_ok, bool rs_ok,
                  bool wide_ok, Plan* out) {
     const ForcedConfig f = g_forced;
-    if (f.family == MT_FAMILY_DL && dl_ok && (f.cfg != kDlpCfg || wide_ok)) {
+    if (f.family == MT_FAMILY_DL && dl_ok && (!is_dlp_cfg(f.cfg) || wide_ok)) {
         *out = cfg_plan(kDlCost[f.cfg], f.cfg, true, M, N, K, batch, f.splits);
         return true;
     }
@@ -244,7 +245,8 @@ bool forced_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dl_ok, boo
 }
 
 // The implicit-im2col and row-sum forms exist for DlCfg 0..3; the planner
-// never picks kDlpCfg for them (nullptr is a safety net).
+// never picks the prefetching configurations for them (nullptr is a safety
+// net).
 GemmLaunchFn rowsum_launcher(int cfg) {
     switch (cfg) {
         case 0: return dl_rowsum_launcher_cfg0();
@@ -293,7 +295,7 @@ GemmLaunchFn pick_launcher(const Plan& plan, int la, int lb) {
             case 1: return dl_launcher_cfg1(la, lb);
             case 2: return dl_launcher_cfg2(la, lb);
             case 3: return dl_launcher_cfg3(la, lb);
-            default: return dlp_launcher(la, lb);
+            default: return dlp_launcher(plan.cfg, la, lb);
         }
     }
     switch (plan.cfg) {
@@ -389,7 +391,7 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
     p.c_vec = p.c_n == 1 && (N & 3) == 0 && ((uintptr_t)p.C & 15u) == 0 && (p.c_m & 3) == 0 &&
               (batch == 1 || (p.c_b & 3) == 0) &&
               (p.c_n_inner >= N || ((p.c_n_inner & 3) == 0 && (p.c_n_outer & 3) == 0));
-    // Configuration kDlpCfg's contract: vector layouts, no fused row sums,
+    // The prefetching configurations' contract: vector layouts, no fused row sums,
     // whole 16-deep chunks in every split (kps is a multiple of 16, so
     // K % 16 == 0 suffices).
     const bool wide_ok = dl && !implicit && p.rowsum == nullptr && K > 0 && (K & 15) == 0;

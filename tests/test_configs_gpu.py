@@ -21,14 +21,15 @@ from util_parity import amax, assert_close
 pytestmark = pytest.mark.gpu
 
 # (family, configuration): 3 register-staged and 4 direct-to-LDS tiles that
-# take every operand form; direct-to-LDS configuration 4 (DLP, the
-# prefetching 4-wave 256x256 tile) takes only vector-epilogue GEMMs with
-# K % 16 == 0 and has tests of its own below.  (A CPU test pins the counts
-# against the library.)
+# take every operand form; direct-to-LDS configurations 4 and 5 (DLP, the
+# fragment-prefetching kernel with 256x256 and 64x64 tiles) take only GEMMs
+# with K % 16 == 0 and no implicit-im2col operand or fused row sums, and have
+# tests of their own below.  (A CPU test pins the counts against the
+# library.)
 CONFIGS = [(mt.FAMILY_RS, c) for c in range(3)] + [(mt.FAMILY_DL, c) for c in range(4)]
 DL_CONFIGS = [c for f, c in CONFIGS if f == mt.FAMILY_DL]
 IDS = [f"{'rs' if f == mt.FAMILY_RS else 'dl'}{c}" for f, c in CONFIGS]
-DLP = 4
+DLPS = [4, 5]
 
 
 def g(a: np.ndarray, dev) -> torch.Tensor:
@@ -193,7 +194,8 @@ def test_forced_split_without_workspace_is_an_error(dev):
     assert rc == mt.MT_ERR_WORKSPACE
 
 
-@pytest.mark.parametrize("fc", CONFIGS + [(mt.FAMILY_DL, DLP)], ids=IDS + [f"dl{DLP}"])
+@pytest.mark.parametrize("fc", CONFIGS + [(mt.FAMILY_DL, c) for c in DLPS],
+                         ids=IDS + [f"dl{c}" for c in DLPS])
 @pytest.mark.parametrize("splits", [1, 4])
 def test_forced_config_special_values(dev, fc, splits):
     # IEEE special values go through every kernel as through matmul_cpu
@@ -232,12 +234,13 @@ def expected_splits(K: int, asked: int) -> int:
     return -(-K // kps)
 
 
+@pytest.mark.parametrize("DLP", DLPS)
 @pytest.mark.parametrize("splits", [1, 3])
 @pytest.mark.parametrize("la", ["row", "col"])
 @pytest.mark.parametrize("lb", ["row", "col"])
 @pytest.mark.parametrize("M,N,K", [(300, 264, 96), (260, 260, 16), (512, 256, 48),
                                    (1000, 1020, 272)])
-def test_forced_dlp_layouts(dev, splits, la, lb, M, N, K):
+def test_forced_dlp_layouts(dev, DLP, splits, la, lb, M, N, K):
     # The prefetching kernel on every vector layout: ragged M and N (clamped
     # loads, masked stores), 1, 2, 3 (odd: the unrolled loop's last step) and
     # 17 chunks per split, a single tile and a 4x4 grid.
@@ -251,9 +254,10 @@ def test_forced_dlp_layouts(dev, splits, la, lb, M, N, K):
                  f"forced dl{DLP} split {splits} a={la} b={lb} {M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("DLP", DLPS)
 @pytest.mark.parametrize("splits", [1, 2])
 @pytest.mark.parametrize("axis", [mt.BIAS_ROW, mt.BIAS_COL])
-def test_forced_dlp_batched_bias_beta(dev, splits, axis):
+def test_forced_dlp_batched_bias_beta(dev, DLP, splits, axis):
     batch, M, N, K = 3, 96, 72, 64
     a = oracle.uniform((batch, M, K), 1300)
     b = oracle.uniform((batch, K, N), 1400)
@@ -269,7 +273,8 @@ def test_forced_dlp_batched_bias_beta(dev, splits, axis):
                  f"forced dl{DLP} batched bias {axis} beta", extra=2e-6)
 
 
-def test_forced_dlp_strided_output_view(dev):
+@pytest.mark.parametrize("DLP", DLPS)
+def test_forced_dlp_strided_output_view(dev, DLP):
     # A row slice of a wider, 16-byte-aligned buffer (row stride 264 > N):
     # vector stores through c_m, neighbours untouched.
     M, N, K = 130, 256, 32
@@ -284,13 +289,9 @@ def test_forced_dlp_strided_output_view(dev):
     assert not got[:, :4].any() and not got[:, 4 + N:].any(), "wrote outside the view"
 
 
-def _not_dlp(name: str) -> None:
-    print(f"[config] {name}", flush=True)
-    assert not (name.startswith("dl ") and name.endswith(f" cfg={DLP}")), name
-
-
+@pytest.mark.parametrize("DLP", DLPS)
 @pytest.mark.parametrize("splits", [1, 3])
-def test_forced_dlp_scalar_and_misaligned_outputs(dev, splits):
+def test_forced_dlp_scalar_and_misaligned_outputs(dev, DLP, splits):
     # N % 4 != 0 (element-wise stores and element-wise split-K partials; B is
     # k-contiguous so it stays a vector layout) and a C that starts 4 bytes
     # past a 16-byte boundary, with bias and beta.
@@ -314,11 +315,12 @@ def test_forced_dlp_scalar_and_misaligned_outputs(dev, splits):
 
 def _not_dlp(name: str) -> None:
     print(f"[config] {name}", flush=True)
-    assert not (name.startswith("dl ") and name.endswith(f" cfg={DLP}")), name
+    assert not (name.startswith("dl ") and any(name.endswith(f" cfg={c}") for c in DLPS)), name
 
 
-def test_forced_dlp_outside_its_contract_uses_the_cost_model(dev):
-    # Forced configuration 4 where its contract does not hold: the launch
+@pytest.mark.parametrize("DLP", DLPS)
+def test_forced_dlp_outside_its_contract_uses_the_cost_model(dev, DLP):
+    # A forced prefetching configuration where its contract does not hold: the launch
     # takes the cost model's plan instead, and the result is still exact.
     M, N, K = 128, 128, 76                     # K tail
     a = oracle.uniform((M, K), 2100)
