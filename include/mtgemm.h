@@ -203,7 +203,7 @@ int mt_gemm_config_count(int family);
  * thread whose operands that family takes; the others keep the cost model.
  * (Direct-to-LDS configurations 4 and 5, the fragment-prefetching kernel with
  * 256x256 and 64x64 tiles, take only GEMMs without implicit-im2col operands
- * or fused row sums, with K % 16 == 0.)
+ * or fused row sums.)
  * MT_FAMILY_AUTO clears it.  While it is set, workspace queries include its
  * split-K partials and a launch given less returns MT_ERR_WORKSPACE.
  * Returns MT_ERR_INVALID for an unknown family, configuration or split count. */

@@ -55,10 +55,17 @@ struct DlTile {
 // XOR-ing the group with (r/4)%4 makes the 16 rows cover all 64 banks once.
 __device__ __forceinline__ int kswz(int r) { return (r >> 2) & 3; }
 
+// Zero source for lanes whose 16 bytes fall in the padding, beyond N, or past
+// the end of the K range: the DMA writes every lane, so those lanes read 16
+// bytes of zeros.
+static __device__ const float __attribute__((aligned(16))) dl_zero_page[4] = {0.f, 0.f, 0.f,
+                                                                              0.f};
+
 template <int L, int BMN, int NW>
 struct DlLoader {
     using T = DlTile<L, BMN, NW>;
     const float* src[T::per_wave];   // this lane's source for each instruction, chunk 0
+    int kofs[T::per_wave];            // k of this lane's 16 bytes within a chunk
     int64_t kstep;                    // elements between consecutive K-chunks
 
     // X points at element (0, 0) of the operand (batch applied); mn0/k0 are the
@@ -75,11 +82,13 @@ struct DlLoader {
                 const int g = (lane & 3) ^ kswz(r);       // k-group that lands in slot lane&3
                 const int64_t row = min((int64_t)mn0 + r, (int64_t)MN - 1);
                 src[j] = X + row * s_mn + (int64_t)(k0 + g * 4) * s_k;
+                kofs[j] = g * 4;
             } else {
                 const int e = q * 256 + lane * 4;         // float index within [16][BMN]
                 const int kr = e / BMN, mn = e - kr * BMN;
                 const int64_t col = min((int64_t)mn0 + mn, (int64_t)MN - 4);
                 src[j] = X + (int64_t)(k0 + kr) * s_k + col;
+                kofs[j] = kr;
             }
         }
     }
@@ -91,6 +100,22 @@ struct DlLoader {
             const int q = j * NW + wave;
             __builtin_amdgcn_global_load_lds(
                 (const void __attribute__((address_space(1)))*)(src[j] + chunk * kstep),
+                (void __attribute__((address_space(3)))*)(tile + q * 256), 16, 0, 0);
+        }
+    }
+
+    // As issue(), for a chunk that may reach past the end of the K range
+    // (klen elements from the k0 given to init): lanes whose 16 bytes start at
+    // or past klen load zeros.  A lane's 16 bytes never straddle the end: an
+    // L_KV operand has K % 4 == 0 and splits start at multiples of 16, and an
+    // L_MV lane reads one k.
+    __device__ __forceinline__ void issue_bounded(float* tile, int chunk, int wave, int klen) const {
+#pragma unroll
+        for (int j = 0; j < T::per_wave; ++j) {
+            const int q = j * NW + wave;
+            const float* s = chunk * 16 + kofs[j] < klen ? src[j] + chunk * kstep : dl_zero_page;
+            __builtin_amdgcn_global_load_lds(
+                (const void __attribute__((address_space(1)))*)s,
                 (void __attribute__((address_space(3)))*)(tile + q * 256), 16, 0, 0);
         }
     }
@@ -130,11 +155,6 @@ struct DlTail {
         }
     }
 };
-
-// Zero source for gather lanes that fall in the padding or beyond N: the DMA
-// writes every lane, so those lanes read 16 bytes of zeros.
-static __device__ const float __attribute__((aligned(16))) dl_zero_page[4] = {0.f, 0.f, 0.f,
-                                                                              0.f};
 
 // Implicit im2col of a channels-last input as the B operand, in the
 // k-contiguous tile layout of L_KV ([BMN][16], k-groups swizzled).  Lane

@@ -1,30 +1,31 @@
 // gemm_dlp_instances.hip -- instantiates gemm_f32_dlp (direct-to-LDS with
-// fragment prefetch) for direct-to-LDS configurations 4 and 5 and the 2x2
-// vector operand layouts.
+// fragment prefetch) for direct-to-LDS configurations 4 and 5, with and
+// without a partial last K-chunk, and the 2x2 vector operand layouts.
 #include "gemm_configs.hpp"
 #include "gemm_dlp_kernel.hpp"
 
 namespace mtk {
 namespace {
 
-template <int CFG, int LA, int LB>
+template <int CFG, bool TAIL, int LA, int LB>
 hipError_t launch_dlp(const GemmParams& p, unsigned nblocks, hipStream_t s) {
     using C = DlCfg<CFG>;
-    hipLaunchKernelGGL((gemm_f32_dlp<C::BM, C::BN, C::WM, C::WN, LA, LB, C::STAGES, C::WPE>),
+    hipLaunchKernelGGL((gemm_f32_dlp<C::BM, C::BN, C::WM, C::WN, LA, LB, C::STAGES, C::WPE, TAIL>),
                        dim3(nblocks), dim3(dl_threads<CFG>()), 0, s, p);
     return hipGetLastError();
 }
 
-#define MT_DLP_TABLE(CFG) \
-    { { launch_dlp<CFG, L_KV, L_KV>, launch_dlp<CFG, L_KV, L_MV> }, \
-      { launch_dlp<CFG, L_MV, L_KV>, launch_dlp<CFG, L_MV, L_MV> } }
+#define MT_DLP_TABLE(CFG, TAIL) \
+    { { launch_dlp<CFG, TAIL, L_KV, L_KV>, launch_dlp<CFG, TAIL, L_KV, L_MV> }, \
+      { launch_dlp<CFG, TAIL, L_MV, L_KV>, launch_dlp<CFG, TAIL, L_MV, L_MV> } }
 
 }  // namespace
 
-GemmLaunchFn dlp_launcher(int cfg, int la, int lb) {
-    static const GemmLaunchFn table4[2][2] = MT_DLP_TABLE(4);
-    static const GemmLaunchFn table5[2][2] = MT_DLP_TABLE(5);
-    return cfg == 4 ? table4[la][lb] : table5[la][lb];
+GemmLaunchFn dlp_launcher(int cfg, bool tail, int la, int lb) {
+    static const GemmLaunchFn table[2][2][2][2] = {
+        {MT_DLP_TABLE(4, false), MT_DLP_TABLE(4, true)},
+        {MT_DLP_TABLE(5, false), MT_DLP_TABLE(5, true)}};
+    return table[cfg - 4][tail][la][lb];
 }
 
 }  // namespace mtk

@@ -24,10 +24,14 @@
 //     refills with chunk kt+STAGES.  Refills past the last chunk re-fetch the
 //     last chunk (always in bounds) into slots nobody reads again, so the DMA
 //     count per step, and hence every vmcnt, is the same on every step.
+//   * TAIL: a K range that is not a multiple of 16 ends in a partial chunk,
+//     fetched by the same DMA with the lanes past the end reading a zero page
+//     (DlLoader::issue_bounded), so the loop has no tail step.  A separate
+//     instantiation: the bounds test costs the whole-chunk case about 4 %.
 //   * The epilogue is store_tile_lds, as in gemm_f32_dl.
 // Host contract (checked in the dispatcher): operand layouts L_KV / L_MV and
-// every split's K range a whole number (>= 1) of 16-deep chunks.  Rows or
-// columns beyond M or N read clamped, valid rows, as in gemm_f32_dl.
+// a non-empty K range.  Rows or columns beyond M or N read clamped, valid
+// rows, as in gemm_f32_dl.
 #pragma once
 
 #include "gemm_dl_kernel.hpp"
@@ -56,7 +60,7 @@ __device__ __forceinline__ void dlp_interleave() {
 
 // WPE: waves per SIMD the register allocation targets (1 lets the 128x128
 // wave tile keep its 256 accumulators in AGPRs beside 256 VGPRs).
-template <int BM, int BN, int WM, int WN, int LA, int LB, int STAGES, int WPE>
+template <int BM, int BN, int WM, int WN, int LA, int LB, int STAGES, int WPE, bool TAIL>
 __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64)
 __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 gemm_f32_dlp(GemmParams p) {
@@ -82,7 +86,8 @@ gemm_f32_dlp(GemmParams p) {
     const int m0 = id.tm * BM, n0 = id.tn * BN;
     const int k_begin = id.split * p.k_per_split;
     const int k_end = min(p.K, k_begin + p.k_per_split);
-    const int nk = (k_end - k_begin) >> 4;   // >= 1 by the host contract
+    const int klen = k_end - k_begin;        // >= 1 by the host contract
+    const int nk = TAIL ? (klen + 15) >> 4 : klen >> 4;   // host: !TAIL => klen % 16 == 0
     const float* Ab = p.A + (int64_t)id.bz * p.a_b;
     const float* Bb = p.B + (int64_t)id.bz * p.b_b;
 
@@ -98,11 +103,19 @@ gemm_f32_dlp(GemmParams p) {
     DlLoader<LB, BN, NW> lb;
     la.init(Ab, p.a_mn, p.a_k, p.M, m0, k_begin, wave, lane);
     lb.init(Bb, p.b_mn, p.b_k, p.N, n0, k_begin, wave, lane);
+    auto issue = [&](float* slot, int chunk) {
+        if constexpr (TAIL) {
+            la.issue_bounded(slot, chunk, wave, klen);
+            lb.issue_bounded(slot + TA::floats, chunk, wave, klen);
+        } else {
+            la.issue(slot, chunk, wave);
+            lb.issue(slot + TA::floats, chunk, wave);
+        }
+    };
 #pragma unroll
     for (int c = 0; c < STAGES; ++c) {
         const int cc = min(c, nk - 1);
-        la.issue(smem + c * STAGE, cc, wave);
-        lb.issue(smem + c * STAGE + TA::floats, cc, wave);
+        issue(smem + c * STAGE, cc);
     }
     // chunk 0 landed (own DMA), then everyone's
     __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(LOADS * (STAGES - 1)));
@@ -119,8 +132,7 @@ gemm_f32_dlp(GemmParams p) {
         __builtin_amdgcn_s_barrier();
         float* const refill = smem + (kt % STAGES) * STAGE;
         const int cn = min(kt + STAGES, nk - 1);
-        la.issue(refill, cn, wave);
-        lb.issue(refill + TA::floats, cn, wave);
+        issue(refill, cn);
         const float* const next = smem + ((kt + 1) % STAGES) * STAGE;
         dl_frags<LA, BM, MB>(next, ra, lane, na);
         dl_frags<LB, BN, NB>(next + TA::floats, rb, lane, nb);

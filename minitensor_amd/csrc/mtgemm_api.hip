@@ -288,14 +288,14 @@ size_t plan_ws(int64_t M, int64_t N, int64_t K, int64_t batch, int cus) {
     return ws;
 }
 
-GemmLaunchFn pick_launcher(const Plan& plan, int la, int lb) {
+GemmLaunchFn pick_launcher(const Plan& plan, int la, int lb, bool ktail) {
     if (plan.dl) {
         switch (plan.cfg) {
             case 0: return dl_launcher_cfg0(la, lb);
             case 1: return dl_launcher_cfg1(la, lb);
             case 2: return dl_launcher_cfg2(la, lb);
             case 3: return dl_launcher_cfg3(la, lb);
-            default: return dlp_launcher(plan.cfg, la, lb);
+            default: return dlp_launcher(plan.cfg, ktail, la, lb);
         }
     }
     switch (plan.cfg) {
@@ -391,10 +391,9 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
     p.c_vec = p.c_n == 1 && (N & 3) == 0 && ((uintptr_t)p.C & 15u) == 0 && (p.c_m & 3) == 0 &&
               (batch == 1 || (p.c_b & 3) == 0) &&
               (p.c_n_inner >= N || ((p.c_n_inner & 3) == 0 && (p.c_n_outer & 3) == 0));
-    // The prefetching configurations' contract: vector layouts, no fused row sums,
-    // whole 16-deep chunks in every split (kps is a multiple of 16, so
-    // K % 16 == 0 suffices).
-    const bool wide_ok = dl && !implicit && p.rowsum == nullptr && K > 0 && (K & 15) == 0;
+    // The prefetching configurations' contract: vector layouts, no fused row
+    // sums, a non-empty K range.
+    const bool wide_ok = dl && !implicit && p.rowsum == nullptr && K > 0;
     Plan plan;
     if (forced_plan(M, N, K, batch, dl, !implicit, wide_ok, &plan)) {
         if (plan.splits > 1 && (workspace == nullptr || ws_bytes < plan.ws_bytes))
@@ -427,7 +426,7 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
     GemmLaunchFn fn = lb == L_IM          ? conv_launcher(plan.cfg)
                       : lb == L_IMW         ? convw_launcher(plan.cfg)
                       : p.rowsum != nullptr ? rowsum_launcher(plan.cfg)
-                                            : pick_launcher(plan, la, lb);
+                                            : pick_launcher(plan, la, lb, (K & 15) != 0);
     if (fn == nullptr) return MT_ERR_UNSUPPORTED;
     hipError_t e = fn(p, (unsigned)nblocks, stream);
     if (e == hipErrorStreamCaptureUnsupported) e = hipSuccess;
