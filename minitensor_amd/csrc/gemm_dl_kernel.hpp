@@ -113,7 +113,8 @@ struct DlLoader {
 #pragma unroll
         for (int j = 0; j < T::per_wave; ++j) {
             const int q = j * NW + wave;
-            const float* s = chunk * 16 + kofs[j] < klen ? src[j] + chunk * kstep : dl_zero_page;
+            // chunk * 16 < klen for every chunk issued, so this cannot overflow
+            const float* s = kofs[j] < klen - chunk * 16 ? src[j] + chunk * kstep : dl_zero_page;
             __builtin_amdgcn_global_load_lds(
                 (const void __attribute__((address_space(1)))*)s,
                 (void __attribute__((address_space(3)))*)(tile + q * 256), 16, 0, 0);
