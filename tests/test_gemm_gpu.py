@@ -365,10 +365,12 @@ def test_split_k_vector_reduce_bias_beta(dev, axis):
 
 # ---- maximum sizes: outputs past 2^31 elements (64-bit addressing) ---------------
 
-@pytest.mark.parametrize("path", ["dl", "rs"])
-def test_output_beyond_2pow31_elements(dev, path):
+@pytest.mark.parametrize("path,forced", [("dl", None), ("dl", 4), ("dl", 5), ("rs", None)],
+                         ids=["dl", "dl4", "dl5", "rs"])
+def test_output_beyond_2pow31_elements(dev, path, forced):
     # C[40000, 60000] = 2.4e9 elements (9.6 GB): rows past 35791 start beyond
     # 2^31, so any 32-bit element index in a kernel or epilogue would alias.
+    # The cost model's pick, and the two prefetching configurations forced.
     M, N, K = 40000, 60000, 32
     a = oracle.uniform((M, K), 91)
     b = oracle.uniform((K, N), 92)
@@ -377,11 +379,17 @@ def test_output_beyond_2pow31_elements(dev, path):
         buf = torch.empty(M * K + 1, device=dev)
         buf[1:].copy_(A.reshape(-1))
         A = buf[1:].view(M, K)
-    C = mt.gemm(A, to_gpu(b, dev))
+    if forced is None:
+        C = mt.gemm(A, to_gpu(b, dev))
+    else:
+        with mt.forced_config(mt.FAMILY_DL, forced, 1):
+            C = mt.gemm(A, to_gpu(b, dev))
     torch.cuda.synchronize()
     cfg = mt.last_config()
     print(f"[config] {cfg}", flush=True)
     assert cfg.startswith(path + " "), cfg
+    if forced is not None:
+        assert cfg.endswith(f" cfg={forced}"), cfg
     rows = np.array([0, 1, 35790, 35791, 35792, 39998, 39999], np.int64)
     got = C[torch.from_numpy(rows).to(dev)].cpu().numpy()
     assert_close(got, oracle.matmul(a[rows], b), K, amax(a), amax(b), f"{path} rows past 2^31")
@@ -389,14 +397,21 @@ def test_output_beyond_2pow31_elements(dev, path):
     torch.cuda.empty_cache()
 
 
-def test_batched_output_beyond_2pow31_elements(dev):
+@pytest.mark.parametrize("forced", [None, 4])
+def test_batched_output_beyond_2pow31_elements(dev, forced):
     # 3 x [32768, 32768]: batch 2 starts at element 2^31 of C.
     Bt, M, N, K = 3, 32768, 32768, 16
     a = oracle.uniform((Bt, M, K), 93)
     b = oracle.uniform((Bt, K, N), 94)
-    C = mt.gemm(to_gpu(a, dev), to_gpu(b, dev))
+    if forced is None:
+        C = mt.gemm(to_gpu(a, dev), to_gpu(b, dev))
+    else:
+        with mt.forced_config(mt.FAMILY_DL, forced, 1):
+            C = mt.gemm(to_gpu(a, dev), to_gpu(b, dev))
     torch.cuda.synchronize()
     print(f"[config] {mt.last_config()}", flush=True)
+    if forced is not None:
+        assert mt.last_config().endswith(f" cfg={forced}"), mt.last_config()
     for bz in (0, 2):
         rows = np.array([0, 17, M - 1], np.int64)
         got = C[bz, torch.from_numpy(rows).to(dev)].cpu().numpy()
