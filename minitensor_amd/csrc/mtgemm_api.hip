@@ -115,7 +115,9 @@ struct CfgCost {
 // launch.  The constants are fitted (log-time error plus selection regret) to
 // the measured times of every configuration and split factor on 29 shapes --
 // the benchmark shapes, square, ragged, tall, wide, skinny, batched and
-// convolution GEMMs -- on one MI355X.
+// convolution GEMMs -- on one MI355X.  The efficiencies of the prefetching
+// configurations 4 and 5 come from same-box comparisons with configurations
+// 0 and 2, which have the same tiles.
 constexpr CfgCost kRsCost[kNumCfg] = {      // register-staged kernel, any layout
     {TileCfg<0>::BM, TileCfg<0>::BN, 0.86, 1},
     {TileCfg<1>::BM, TileCfg<1>::BN, 0.75, 2},
