@@ -38,10 +38,11 @@
 
 namespace mtk {
 
-// Spread one step's instructions over its 128 MFMAs: the DMA of the refill
-// (up to 8 wave instructions) first, one per MFMA, then the fragment reads of
-// the next chunk (up to 40 LDS instructions), one per two MFMAs.  Groups
-// without instructions of their kind stay empty.
+// Spread the instructions that follow a step's barrier over its NM MFMAs:
+// the DMA of the refill (up to 8 wave instructions) first, one per MFMA, then
+// the fragment reads of the next chunk (up to 40 LDS instructions), one per
+// one or two MFMAs.  Groups without instructions of their kind stay empty.
+template <int NM>
 __device__ __forceinline__ void dlp_interleave() {
     constexpr int kMfma = 0x008, kVmemRead = 0x020, kDsRead = 0x100;
     __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
@@ -53,9 +54,22 @@ __device__ __forceinline__ void dlp_interleave() {
 #pragma unroll
     for (int g = 0; g < 40; ++g) {
         __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kMfma, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(kMfma, NM >= 100 ? 2 : 1, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(kMfma, 128, 0);
+    __builtin_amdgcn_sched_group_barrier(kMfma, NM, 0);
+}
+
+// The MFMAs of k-steps S0..S1-1 of one chunk.
+template <int MB, int NB, int S0, int S1>
+__device__ __forceinline__ void mfma_steps(f32x16 (&acc)[MB][NB], const float (&fa)[MB][8],
+                                           const float (&fb)[NB][8]) {
+#pragma unroll
+    for (int s = S0; s < S1; ++s)
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+            for (int j = 0; j < NB; ++j)
+                acc[i][j] = mfma_32x32x2(fa[i][s], fb[j][s], acc[i][j]);
 }
 
 // WPE: waves per SIMD the register allocation targets (1 lets the 128x128
@@ -125,9 +139,18 @@ gemm_f32_dlp(GemmParams p) {
     dl_frags<LB, BN, NB>(smem + TA::floats, rb, lane, fb0);
 
     // Step kt: multiply chunk kt (registers ca/cb) while reading chunk kt+1
-    // into na/nb and refilling chunk kt's slot with chunk kt+STAGES.
+    // into na/nb and refilling chunk kt's slot with chunk kt+STAGES.  The
+    // barrier guards only the refill and the reads, so with the 128x128 wave
+    // tile the first PRE k-steps of MFMAs issue before it: the MFMA pipe has
+    // work queued while the waves synchronize (about 1 % at 4096^3).
+    constexpr int PRE = MB * NB * 8 >= 128 ? 2 : 0;
     auto step = [&](int kt, const float (&ca)[MB][8], const float (&cb)[NB][8],
                     float (&na)[MB][8], float (&nb)[NB][8]) {
+        if constexpr (PRE > 0) {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));   // ca/cb landed
+            mfma_steps<MB, NB, 0, PRE>(acc, ca, cb);
+            __builtin_amdgcn_sched_barrier(0);
+        }
         __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(LOADS * (STAGES - 2)));
         __builtin_amdgcn_s_barrier();
         float* const refill = smem + (kt % STAGES) * STAGE;
@@ -136,8 +159,8 @@ gemm_f32_dlp(GemmParams p) {
         const float* const next = smem + ((kt + 1) % STAGES) * STAGE;
         dl_frags<LA, BM, MB>(next, ra, lane, na);
         dl_frags<LB, BN, NB>(next + TA::floats, rb, lane, nb);
-        mfma_chunk<MB, NB>(acc, ca, cb);
-        if constexpr (MB * NB * 8 >= 128) dlp_interleave();
+        mfma_steps<MB, NB, PRE, 8>(acc, ca, cb);
+        if constexpr (MB * NB * 8 >= 128) dlp_interleave<(8 - PRE) * MB * NB>();
     };
 
     int kt = 0;
