@@ -140,10 +140,10 @@ gemm_f32_dlp(GemmParams p) {
 
     // Step kt: multiply chunk kt (registers ca/cb) while reading chunk kt+1
     // into na/nb and refilling chunk kt's slot with chunk kt+STAGES.  The
-    // barrier guards only the refill and the reads, so with the 128x128 wave
-    // tile the first PRE k-steps of MFMAs issue before it: the MFMA pipe has
-    // work queued while the waves synchronize (about 1 % at 4096^3).
-    constexpr int PRE = MB * NB * 8 >= 128 ? 2 : 0;
+    // barrier guards only the refill and the reads, so the first PRE k-steps
+    // of MFMAs issue before it: the MFMA pipe has work queued while the waves
+    // synchronize (about 1 % at 4096^3, 3-9 % for the 64x64 tile).
+    constexpr int PRE = 2;
     auto step = [&](int kt, const float (&ca)[MB][8], const float (&cb)[NB][8],
                     float (&na)[MB][8], float (&nb)[NB][8]) {
         if constexpr (PRE > 0) {
