@@ -47,14 +47,16 @@ template <> struct DlCfg<2> { static constexpr int BM = 64, BN = 64, WM = 32, WN
 // 8 waves of 64x64; 2 x 24 KB ring.  Fills the chip where M is about 256
 // (e.g. convolutions with 256 output channels: 49 tiles x split 5 = 245).
 template <> struct DlCfg<3> { static constexpr int BM = 256, BN = 128, WM = 64, WN = 64, STAGES = 2; };
-// Configurations 4 and 5 are the fragment-prefetching kernel gemm_f32_dlp
+// Configurations 4-6 are the fragment-prefetching kernel gemm_f32_dlp
 // (gemm_dlp_kernel.hpp): vector layouts only, no implicit-im2col or row-sum
-// form.  4: 4 waves of 128x128 (one per SIMD);
-// 5: 4 waves of 32x32.  WPE: waves per SIMD its registers are sized for.
+// form.  4: 4 waves of 128x128 (one per SIMD); 5: 4 waves of 32x32; 6: 8 waves
+// of 64x32 (two per SIMD), the 128x128 tile for K ranges of 512 and more.
+// WPE: waves per SIMD its registers are sized for.
 template <> struct DlCfg<4> { static constexpr int BM = 256, BN = 256, WM = 128, WN = 128, STAGES = 2, WPE = 1; };
 template <> struct DlCfg<5> { static constexpr int BM = 64, BN = 64, WM = 32, WN = 32, STAGES = 2, WPE = 8; };
+template <> struct DlCfg<6> { static constexpr int BM = 128, BN = 128, WM = 64, WN = 32, STAGES = 2, WPE = 2; };
 
-constexpr int kNumDlCfg = 6;
+constexpr int kNumDlCfg = 7;
 constexpr int kDlpFirstCfg = 4;   // configurations kDlpFirstCfg.. are gemm_f32_dlp
 constexpr bool is_dlp_cfg(int cfg) { return cfg >= kDlpFirstCfg; }
 
@@ -68,7 +70,7 @@ GemmLaunchFn dl_launcher_cfg0(int la, int lb);
 GemmLaunchFn dl_launcher_cfg1(int la, int lb);
 GemmLaunchFn dl_launcher_cfg2(int la, int lb);
 GemmLaunchFn dl_launcher_cfg3(int la, int lb);
-// Configurations 4, 5 (gemm_f32_dlp); la, lb in {L_KV, L_MV}; tail: K is
+// Configurations 4-6 (gemm_f32_dlp); la, lb in {L_KV, L_MV}; tail: K is
 // not a multiple of 16.
 GemmLaunchFn dlp_launcher(int cfg, bool tail, int la, int lb);
 // Implicit-im2col convolution: A = weights (L_KV), B = L_IM (GemmParams::cv).

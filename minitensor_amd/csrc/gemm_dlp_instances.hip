@@ -1,5 +1,5 @@
 // gemm_dlp_instances.hip -- instantiates gemm_f32_dlp (direct-to-LDS with
-// fragment prefetch) for direct-to-LDS configurations 4 and 5, with and
+// fragment prefetch) for direct-to-LDS configurations 4-6, with and
 // without a partial last K-chunk, and the 2x2 vector operand layouts.
 #include "gemm_configs.hpp"
 #include "gemm_dlp_kernel.hpp"
@@ -22,9 +22,10 @@ hipError_t launch_dlp(const GemmParams& p, unsigned nblocks, hipStream_t s) {
 }  // namespace
 
 GemmLaunchFn dlp_launcher(int cfg, bool tail, int la, int lb) {
-    static const GemmLaunchFn table[2][2][2][2] = {
+    static const GemmLaunchFn table[3][2][2][2] = {
         {MT_DLP_TABLE(4, false), MT_DLP_TABLE(4, true)},
-        {MT_DLP_TABLE(5, false), MT_DLP_TABLE(5, true)}};
+        {MT_DLP_TABLE(5, false), MT_DLP_TABLE(5, true)},
+        {MT_DLP_TABLE(6, false), MT_DLP_TABLE(6, true)}};
     return table[cfg - 4][tail][la][lb];
 }
 

@@ -116,8 +116,8 @@ struct CfgCost {
 // the measured times of every configuration and split factor on 29 shapes --
 // the benchmark shapes, square, ragged, tall, wide, skinny, batched and
 // convolution GEMMs -- on one MI355X.  The efficiencies of the prefetching
-// configurations 4 and 5 come from same-box comparisons with configurations
-// 0 and 2, which have the same tiles.
+// configurations 4-6 come from same-box comparisons with configurations 0, 2
+// and 1, which have the same tiles.
 constexpr CfgCost kRsCost[kNumCfg] = {      // register-staged kernel, any layout
     {TileCfg<0>::BM, TileCfg<0>::BN, 0.86, 1},
     {TileCfg<1>::BM, TileCfg<1>::BN, 0.75, 2},
@@ -128,7 +128,12 @@ constexpr CfgCost kDlCost[kNumDlCfg] = {    // direct-to-LDS kernel, vector layo
     {DlCfg<2>::BM, DlCfg<2>::BN, 0.68, 8},
     {DlCfg<3>::BM, DlCfg<3>::BN, 0.87, 3},
     {DlCfg<4>::BM, DlCfg<4>::BN, 0.93, 1},
-    {DlCfg<5>::BM, DlCfg<5>::BN, 0.72, 8}};
+    {DlCfg<5>::BM, DlCfg<5>::BN, 0.72, 8},
+    {DlCfg<6>::BM, DlCfg<6>::BN, 0.90, 3}};
+// Configuration 6 pays off only over long K ranges (short ones, such as the
+// 64-deep batched GEMM of the benchmark, run up to 20 % slower than
+// configuration 1): the planner offers it for K per split >= kDlp6MinK.
+constexpr int kDlp6MinK = 512;
 struct CostModel {
     double round_latency = 6200.0;           // cycles of fill/drain per round
     double epilogue_bytes_per_cycle = 7.9;   // one workgroup's tile store
@@ -173,6 +178,7 @@ Plan make_plan_uncached(int64_t M, int64_t N, int64_t K, int64_t batch, int cus,
             if (s > 1 && !allow_split) break;
             const Plan pl = cfg_plan(cc, cfg, dl, M, N, K, batch, s);
             if (s > 1 && pl.kps < 64) break;
+            if (dl && cfg == 6 && std::min<int64_t>(pl.kps, K) < kDlp6MinK) break;
             if (pl.splits != s) continue;
             const int64_t wgs = (int64_t)pl.tiles_m * pl.tiles_n * batch * pl.splits;
             if (wgs * 512 >= ((int64_t)1 << 32)) continue;

@@ -21,15 +21,15 @@ from util_parity import amax, assert_close
 pytestmark = pytest.mark.gpu
 
 # (family, configuration): 3 register-staged and 4 direct-to-LDS tiles that
-# take every operand form; direct-to-LDS configurations 4 and 5 (DLP, the
-# fragment-prefetching kernel with 256x256 and 64x64 tiles) take only GEMMs
+# take every operand form; direct-to-LDS configurations 4-6 (DLP, the
+# fragment-prefetching kernel with 256x256, 64x64 and 128x128 tiles) take only GEMMs
 # with K % 16 == 0 and no implicit-im2col operand or fused row sums, and have
 # tests of their own below.  (A CPU test pins the counts against the
 # library.)
 CONFIGS = [(mt.FAMILY_RS, c) for c in range(3)] + [(mt.FAMILY_DL, c) for c in range(4)]
 DL_CONFIGS = [c for f, c in CONFIGS if f == mt.FAMILY_DL]
 IDS = [f"{'rs' if f == mt.FAMILY_RS else 'dl'}{c}" for f, c in CONFIGS]
-DLPS = [4, 5]
+DLPS = [4, 5, 6]
 
 
 def g(a: np.ndarray, dev) -> torch.Tensor:
