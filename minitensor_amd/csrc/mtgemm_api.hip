@@ -127,7 +127,7 @@ constexpr CfgCost kDlCost[kNumDlCfg] = {    // direct-to-LDS kernel, vector layo
     {DlCfg<1>::BM, DlCfg<1>::BN, 0.86, 4},
     {DlCfg<2>::BM, DlCfg<2>::BN, 0.68, 8},
     {DlCfg<3>::BM, DlCfg<3>::BN, 0.87, 3},
-    {DlCfg<4>::BM, DlCfg<4>::BN, 0.93, 1},
+    {DlCfg<4>::BM, DlCfg<4>::BN, 0.98, 1},
     {DlCfg<5>::BM, DlCfg<5>::BN, 0.72, 8},
     {DlCfg<6>::BM, DlCfg<6>::BN, 0.90, 3}};
 // Configuration 6 pays off only over long K ranges (short ones, such as the
