@@ -202,8 +202,9 @@ int mt_gemm_config_count(int family);
  * (1..64; fewer when K is short), on every later GEMM launch of the calling
  * thread whose operands that family takes; the others keep the cost model.
  * (Direct-to-LDS configurations 4-6, the fragment-prefetching kernel with
- * 256x256, 64x64 and 128x128 tiles, take only GEMMs without implicit-im2col
- * operands or fused row sums.)
+ * 256x256, 64x64 and 128x128 tiles, take the convolution weight gradient's
+ * implicit operand but not the forward convolution's implicit im2col
+ * operand or fused row sums.)
  * MT_FAMILY_AUTO clears it.  While it is set, workspace queries include its
  * split-K partials and a launch given less returns MT_ERR_WORKSPACE.
  * Returns MT_ERR_INVALID for an unknown family, configuration or split count. */

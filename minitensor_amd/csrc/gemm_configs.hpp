@@ -48,8 +48,8 @@ template <> struct DlCfg<2> { static constexpr int BM = 64, BN = 64, WM = 32, WN
 // (e.g. convolutions with 256 output channels: 49 tiles x split 5 = 245).
 template <> struct DlCfg<3> { static constexpr int BM = 256, BN = 128, WM = 64, WN = 64, STAGES = 2; };
 // Configurations 4-6 are the fragment-prefetching kernel gemm_f32_dlp
-// (gemm_dlp_kernel.hpp): vector layouts only, no implicit-im2col or row-sum
-// form.  4: 4 waves of 128x128 (one per SIMD); 5: 4 waves of 32x32; 6: 8 waves
+// (gemm_dlp_kernel.hpp): vector layouts and the weight-gradient operand
+// L_IMW; no implicit-im2col (L_IM) or row-sum form.  4: 4 waves of 128x128 (one per SIMD); 5: 4 waves of 32x32; 6: 8 waves
 // of 64x32 (two per SIMD), the 128x128 tile for K ranges of 512 and more.
 // WPE: waves per SIMD its registers are sized for.
 template <> struct DlCfg<4> { static constexpr int BM = 256, BN = 256, WM = 128, WN = 128, STAGES = 2, WPE = 1; };
@@ -73,6 +73,8 @@ GemmLaunchFn dl_launcher_cfg3(int la, int lb);
 // Configurations 4-6 (gemm_f32_dlp); la, lb in {L_KV, L_MV}; tail: K is
 // not a multiple of 16.
 GemmLaunchFn dlp_launcher(int cfg, bool tail, int la, int lb);
+// Configurations 4-6 for the convolution weight gradient (A L_KV, B L_IMW).
+GemmLaunchFn dlp_convw_launcher(int cfg, bool tail);
 // Implicit-im2col convolution: A = weights (L_KV), B = L_IM (GemmParams::cv).
 GemmLaunchFn dl_conv_launcher_cfg0();
 GemmLaunchFn dl_conv_launcher_cfg1();

@@ -1,6 +1,7 @@
 // gemm_dlp_instances.hip -- instantiates gemm_f32_dlp (direct-to-LDS with
 // fragment prefetch) for direct-to-LDS configurations 4-6, with and
-// without a partial last K-chunk, and the 2x2 vector operand layouts.
+// without a partial last K-chunk, for the 2x2 vector operand layouts and the
+// convolution weight gradient (A = dY k-contiguous, B = L_IMW).
 #include "gemm_configs.hpp"
 #include "gemm_dlp_kernel.hpp"
 
@@ -20,6 +21,14 @@ hipError_t launch_dlp(const GemmParams& p, unsigned nblocks, hipStream_t s) {
       { launch_dlp<CFG, TAIL, L_MV, L_KV>, launch_dlp<CFG, TAIL, L_MV, L_MV> } }
 
 }  // namespace
+
+GemmLaunchFn dlp_convw_launcher(int cfg, bool tail) {
+    static const GemmLaunchFn table[3][2] = {
+        {launch_dlp<4, false, L_KV, L_IMW>, launch_dlp<4, true, L_KV, L_IMW>},
+        {launch_dlp<5, false, L_KV, L_IMW>, launch_dlp<5, true, L_KV, L_IMW>},
+        {launch_dlp<6, false, L_KV, L_IMW>, launch_dlp<6, true, L_KV, L_IMW>}};
+    return table[cfg - 4][tail];
+}
 
 GemmLaunchFn dlp_launcher(int cfg, bool tail, int la, int lb) {
     static const GemmLaunchFn table[3][2][2][2] = {

@@ -1,7 +1,7 @@
 // gemm_dlp_kernel.hpp -- direct-to-LDS fp32 MFMA GEMM whose waves read the
 // next K-chunk's fragments while the current chunk's MFMAs issue.
 //
-// Two instantiations (direct-to-LDS configurations 4 and 5):
+// Three tile shapes (direct-to-LDS configurations 4, 5 and 6):
 //   * 256x256 block tile, four waves of 128x128 (one wave per SIMD, 256
 //     accumulator registers).  Per 16-deep K-chunk a wave reads 16 KB of
 //     fragments from LDS for 128 MFMAs, against 12 KB for 64 MFMAs with the
@@ -10,6 +10,8 @@
 //   * 64x64 block tile, four waves of 32x32: the small GEMMs that run about
 //     one workgroup per CU, where each SIMD again holds a single wave and the
 //     fragment-read latency after every barrier is exposed.
+//   * 128x128 block tile, eight waves of 64x32 (two per SIMD), for K ranges
+//     of at least 512 per split.
 // Structure:
 //   * With no second wave on the SIMD to cover the LDS latency, chunk kt+1's
 //     fragments are read while chunk kt's MFMAs issue: two register sets
@@ -29,8 +31,9 @@
 //     (DlLoader::issue_bounded), so the loop has no tail step.  A separate
 //     instantiation: the bounds test costs the whole-chunk case about 4 %.
 //   * The epilogue is store_tile_lds, as in gemm_f32_dl.
-// Host contract (checked in the dispatcher): operand layouts L_KV / L_MV and
-// a non-empty K range.  Rows or columns beyond M or N read clamped, valid
+// Host contract (checked in the dispatcher): operand layouts L_KV / L_MV (B
+// also the implicit im2col-transpose operand L_IMW of the convolution weight
+// gradient) and a non-empty K range.  Rows or columns beyond M or N read clamped, valid
 // rows, as in gemm_f32_dl.
 #pragma once
 
@@ -82,8 +85,10 @@ gemm_f32_dlp(GemmParams p) {
     constexpr int NW = (BM / WM) * WAVES_N;
     constexpr int MB = WM / 32, NB = WN / 32;
     static_assert(STAGES >= 2, "the ring needs at least two slots");
-    static_assert((LA == L_KV || LA == L_MV) && (LB == L_KV || LB == L_MV),
-                  "vector operand layouts only");
+    static_assert((LA == L_KV || LA == L_MV) && (LB == L_KV || LB == L_MV || LB == L_IMW),
+                  "vector operand layouts or the implicit im2col-transpose operand");
+    constexpr bool imw = (LB == L_IMW);
+    constexpr int LBF = imw ? L_MV : LB;     // LDS layout of B's tile
     using TA = DlTile<LA, BM, NW>;
     using TB = DlTile<LB, BN, NW>;
     constexpr int STAGE = TA::floats + TB::floats;
@@ -114,17 +119,16 @@ gemm_f32_dlp(GemmParams p) {
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     DlLoader<LA, BM, NW> la;
-    DlLoader<LB, BN, NW> lb;
+    std::conditional_t<imw, DlImwLoader<BN, NW>, DlLoader<LB, BN, NW>> lb;
     la.init(Ab, p.a_mn, p.a_k, p.M, m0, k_begin, wave, lane);
-    lb.init(Bb, p.b_mn, p.b_k, p.N, n0, k_begin, wave, lane);
+    if constexpr (imw) lb.init(p, Bb, n0, k_begin, k_end, wave, lane);
+    else lb.init(Bb, p.b_mn, p.b_k, p.N, n0, k_begin, wave, lane);
+    // (The implicit operand's loader tests k < k_end itself, on every chunk.)
     auto issue = [&](float* slot, int chunk) {
-        if constexpr (TAIL) {
-            la.issue_bounded(slot, chunk, wave, klen);
-            lb.issue_bounded(slot + TA::floats, chunk, wave, klen);
-        } else {
-            la.issue(slot, chunk, wave);
-            lb.issue(slot + TA::floats, chunk, wave);
-        }
+        if constexpr (TAIL) la.issue_bounded(slot, chunk, wave, klen);
+        else la.issue(slot, chunk, wave);
+        if constexpr (TAIL && !imw) lb.issue_bounded(slot + TA::floats, chunk, wave, klen);
+        else lb.issue(slot + TA::floats, chunk, wave);
     };
 #pragma unroll
     for (int c = 0; c < STAGES; ++c) {
@@ -136,7 +140,7 @@ gemm_f32_dlp(GemmParams p) {
     __builtin_amdgcn_s_barrier();
     float fa0[MB][8], fb0[NB][8], fa1[MB][8], fb1[NB][8];
     dl_frags<LA, BM, MB>(smem, ra, lane, fa0);
-    dl_frags<LB, BN, NB>(smem + TA::floats, rb, lane, fb0);
+    dl_frags<LBF, BN, NB>(smem + TA::floats, rb, lane, fb0);
 
     // Step kt: multiply chunk kt (registers ca/cb) while reading chunk kt+1
     // into na/nb and refilling chunk kt's slot with chunk kt+STAGES.  The
@@ -158,7 +162,7 @@ gemm_f32_dlp(GemmParams p) {
         issue(refill, cn);
         const float* const next = smem + ((kt + 1) % STAGES) * STAGE;
         dl_frags<LA, BM, MB>(next, ra, lane, na);
-        dl_frags<LB, BN, NB>(next + TA::floats, rb, lane, nb);
+        dl_frags<LBF, BN, NB>(next + TA::floats, rb, lane, nb);
         mfma_steps<MB, NB, PRE, 8>(acc, ca, cb);
         if constexpr (MB * NB * 8 >= 128) dlp_interleave<(8 - PRE) * MB * NB>();
     };

@@ -252,9 +252,9 @@ bool forced_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dl_ok, boo
     return false;
 }
 
-// The implicit-im2col and row-sum forms exist for DlCfg 0..3; the planner
-// never picks the prefetching configurations for them (nullptr is a safety
-// net).
+// The implicit-im2col (L_IM) and row-sum forms exist for DlCfg 0..3 only; the
+// planner never picks the prefetching configurations for them (nullptr is a
+// safety net).  The weight-gradient operand (L_IMW) exists for all.
 GemmLaunchFn rowsum_launcher(int cfg) {
     switch (cfg) {
         case 0: return dl_rowsum_launcher_cfg0();
@@ -265,13 +265,13 @@ GemmLaunchFn rowsum_launcher(int cfg) {
     }
 }
 
-GemmLaunchFn convw_launcher(int cfg) {
+GemmLaunchFn convw_launcher(int cfg, bool ktail) {
     switch (cfg) {
         case 0: return dl_convw_launcher_cfg0();
         case 1: return dl_convw_launcher_cfg1();
         case 2: return dl_convw_launcher_cfg2();
         case 3: return dl_convw_launcher_cfg3();
-        default: return nullptr;
+        default: return dlp_convw_launcher(cfg, ktail);
     }
 }
 
@@ -399,9 +399,10 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
     p.c_vec = p.c_n == 1 && (N & 3) == 0 && ((uintptr_t)p.C & 15u) == 0 && (p.c_m & 3) == 0 &&
               (batch == 1 || (p.c_b & 3) == 0) &&
               (p.c_n_inner >= N || ((p.c_n_inner & 3) == 0 && (p.c_n_outer & 3) == 0));
-    // The prefetching configurations' contract: vector layouts, no fused row
+    // The prefetching configurations' contract: vector layouts or the
+    // weight-gradient operand (not the implicit-im2col one), no fused row
     // sums, a non-empty K range.
-    const bool wide_ok = dl && !implicit && p.rowsum == nullptr && K > 0;
+    const bool wide_ok = dl && lb != L_IM && p.rowsum == nullptr && K > 0;
     Plan plan;
     if (forced_plan(M, N, K, batch, dl, !implicit, wide_ok, &plan)) {
         if (plan.splits > 1 && (workspace == nullptr || ws_bytes < plan.ws_bytes))
@@ -432,7 +433,7 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
                   plan.cfg);
 
     GemmLaunchFn fn = lb == L_IM          ? conv_launcher(plan.cfg)
-                      : lb == L_IMW         ? convw_launcher(plan.cfg)
+                      : lb == L_IMW         ? convw_launcher(plan.cfg, (K & 15) != 0)
                       : p.rowsum != nullptr ? rowsum_launcher(plan.cfg)
                                             : pick_launcher(plan, la, lb, (K & 15) != 0);
     if (fn == nullptr) return MT_ERR_UNSUPPORTED;

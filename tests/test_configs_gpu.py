@@ -163,7 +163,7 @@ def test_forced_dl_implicit_conv(dev, cfg, splits):
                  f"forced dl{cfg} implicit conv", extra=1e-5)
 
 
-@pytest.mark.parametrize("cfg", DL_CONFIGS)
+@pytest.mark.parametrize("cfg", DL_CONFIGS + DLPS)
 @pytest.mark.parametrize("splits", [1, 3])
 def test_forced_dl_implicit_conv_weight_grad(dev, cfg, splits):
     # Implicit dW (B = im2colᵀ of channels-last x, columns scattered to OIHW),
@@ -337,3 +337,14 @@ def test_forced_dlp_outside_its_contract_uses_the_cost_model(dev, DLP):
     _, wdw, wdb = oracle.linear_backward(dy, x, w)
     assert_close(sync_np(dw), wdw, 301, amax(dy), amax(x), "dlp fallback dW")
     assert_close(sync_np(db), wdb, 301, amax(dy), 1.0, "dlp fallback db")
+    # ... and the implicit-im2col convolution forward keeps gemm_f32_dl
+    n, c, h, wd, co, k = 2, 32, 9, 10, 40, 3
+    xc = oracle.normal((n, c, h, wd), 2003)
+    wc = oracle.normal((co, c, k, k), 2004)
+    with mt.forced_config(mt.FAMILY_DL, DLP, 1):
+        out = mt.conv2d(g(xc, dev), g(wc, dev), None, 1, 1)
+        name = mt.last_config()
+        _not_dlp(name)
+    assert "im2col" in name, name
+    assert_close(sync_np(out), oracle.conv2d(xc, wc, None, 1, 1), c * k * k, amax(xc), amax(wc),
+                 "dlp fallback implicit conv")
