@@ -117,3 +117,78 @@ def test_random_gemm_auto_plan(dev, case):
     if wide is not None:
         w = wide.cpu().numpy()
         assert not w[:, :lead].any() and not w[:, lead + N:].any(), "wrote outside the window"
+
+
+# ---- batched ------------------------------------------------------------------
+# 24 seeded batched GEMMs (the reference's bmm, include/TensorOps.hpp:933-991,
+# restated as ora_bmm): batch 1-12, each operand dense, per-batch transposed
+# (a permuted view), every second batch of a larger stack, or one matrix
+# expanded over the batch (stride 0); the output fresh or every second batch
+# of a larger stack, with a bias or beta*C now and then.
+
+def _batched(a: np.ndarray, kind: str, dev) -> torch.Tensor:
+    nb, rows, cols = a.shape
+    if kind == "dense":
+        return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    if kind == "trans":
+        return torch.from_numpy(np.ascontiguousarray(a.transpose(0, 2, 1))).to(dev).permute(0, 2, 1)
+    if kind == "step":
+        big = np.zeros((2 * nb, rows, cols), np.float32)
+        big[::2] = a
+        return torch.from_numpy(big).to(dev)[::2]
+    # "expand": every batch is a[0]
+    return torch.from_numpy(np.ascontiguousarray(a[0])).to(dev).expand(nb, rows, cols)
+
+
+BCASES = []
+_brng = np.random.default_rng(20261203)
+for _i in range(24):
+    _r = _round4 if _i % 2 else (lambda x: x)
+    _ka = str(_brng.choice(["dense", "trans", "step", "expand"], p=[0.4, 0.3, 0.15, 0.15]))
+    _kb = str(_brng.choice(["dense", "trans", "step", "expand"], p=[0.4, 0.3, 0.15, 0.15]))
+    if _ka == "expand" and _kb == "expand":
+        _kb = "dense"
+    BCASES.append(dict(batch=int(_brng.integers(1, 13)), M=_r(int(_brng.integers(1, 400))),
+                       N=_r(int(_brng.integers(1, 400))), K=_r(int(_brng.integers(1, 700))),
+                       la=_ka, lb=_kb, out=str(_brng.choice(["fresh", "step"])),
+                       bias=str(_brng.choice(["none", "none", "row", "col"])),
+                       beta=float(_brng.choice([0.0, 0.0, 0.5])), seed=3000 + 10 * _i))
+
+
+@pytest.mark.parametrize("case", BCASES, ids=[f"b{i}" for i in range(len(BCASES))])
+def test_random_batched_auto_plan(dev, case):
+    nb, M, N, K = case["batch"], case["M"], case["N"], case["K"]
+    a = oracle.uniform((nb, M, K), case["seed"])
+    b = oracle.uniform((nb, K, N), case["seed"] + 1)
+    if case["la"] == "expand":
+        a = np.broadcast_to(a[:1], a.shape).copy()
+    if case["lb"] == "expand":
+        b = np.broadcast_to(b[:1], b.shape).copy()
+    A, B = _batched(a, case["la"], dev), _batched(b, case["lb"], dev)
+    c0 = oracle.uniform((nb, M, N), case["seed"] + 2)
+    if case["out"] == "step":
+        big = torch.zeros(2 * nb, M, N, device=dev)
+        C = big[::2]
+    else:
+        big, C = None, torch.empty(nb, M, N, device=dev)
+    beta = case["beta"]
+    if beta != 0.0:
+        C.copy_(torch.from_numpy(c0).to(dev))
+    kw, bias = {}, None
+    if case["bias"] != "none":
+        bias = oracle.uniform((M if case["bias"] == "row" else N,), case["seed"] + 3)
+        kw = dict(bias=torch.from_numpy(bias).to(dev),
+                  bias_axis=mt.BIAS_ROW if case["bias"] == "row" else mt.BIAS_COL)
+    mt.gemm(A, B, out=C, beta=beta, **kw)
+    torch.cuda.synchronize()
+    print(f"[case] {case} -> {mt.last_config()}", flush=True)
+    want = oracle.bmm(a, b).astype(np.float64)
+    if bias is not None:
+        want = want + (bias[None, :, None] if case["bias"] == "row" else bias[None, None, :])
+    if beta != 0.0:
+        want = want + beta * c0
+    extra = 2e-6 * (1.0 + abs(beta)) if (bias is not None or beta != 0.0) else 0.0
+    assert_close(C.cpu().numpy(), want, K, amax(a), amax(b),
+                 f"random bmm {nb}x{M}x{N}x{K} a={case['la']} b={case['lb']}", extra=extra)
+    if big is not None:
+        assert not big[1::2].cpu().numpy().any(), "wrote into the skipped batches"
