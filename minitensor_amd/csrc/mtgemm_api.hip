@@ -331,7 +331,28 @@ int check_gemm(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C,
     return MT_OK;
 }
 
-// Sum split-K partials in split order, then apply bias and beta: deterministic.
+// Split-K partials are summed in split order, then bias and beta are applied:
+// deterministic.  Up to kReduceBatch partial loads (and the loads of the bias
+// and of beta*C) are issued before the first add: a loop bounded by the
+// runtime split count would wait for each load before issuing the next.
+constexpr int kReduceBatch = 8;
+
+template <class T>
+__device__ __forceinline__ T sum_partials(const float* src, int64_t split_stride, int splits,
+                                          T v) {
+    for (int s0 = 0; s0 < splits; s0 += kReduceBatch) {
+        T t[kReduceBatch];
+#pragma unroll
+        for (int j = 0; j < kReduceBatch; ++j)
+            if (s0 + j < splits)
+                t[j] = *reinterpret_cast<const T*>(src + (int64_t)(s0 + j) * split_stride);
+#pragma unroll
+        for (int j = 0; j < kReduceBatch; ++j)
+            if (s0 + j < splits) v += t[j];
+    }
+    return v;
+}
+
 // Scalar form, for outputs that do not take 16-byte stores.
 __global__ void __launch_bounds__(256) splitk_reduce_f32(GemmParams p) {
     const int64_t MN = (int64_t)p.M * p.N;
@@ -342,12 +363,14 @@ __global__ void __launch_bounds__(256) splitk_reduce_f32(GemmParams p) {
         const int64_t mn = e - bz * MN;
         const int m = (int)(mn / p.N);
         const int n = (int)(mn - (int64_t)m * p.N);
-        float v = 0.f;
-        for (int s = 0; s < p.splits; ++s) v += p.ws[((int64_t)s * p.batch + bz) * MN + mn];
-        if (p.bias_axis == 1) v += p.bias[(int64_t)m * p.bias_stride];
-        else if (p.bias_axis == 2) v += p.bias[(int64_t)n * p.bias_stride];
+        const float b = p.bias_axis == 1   ? p.bias[(int64_t)m * p.bias_stride]
+                        : p.bias_axis == 2 ? p.bias[(int64_t)n * p.bias_stride]
+                                           : 0.f;
         float* dst = p.C + bz * p.c_b + (int64_t)m * p.c_m + col_offset(p, n);
-        if (p.beta != 0.f) v += p.beta * *dst;
+        const float old = p.beta != 0.f ? *dst : 0.f;
+        float v = sum_partials<float>(p.ws + bz * MN + mn, p.batch * MN, p.splits, 0.f);
+        if (p.bias_axis != 0) v += b;
+        if (p.beta != 0.f) v += p.beta * old;
         *dst = v;
     }
 }
@@ -359,6 +382,7 @@ __global__ void __launch_bounds__(256) splitk_reduce_f32(GemmParams p) {
 __global__ void __launch_bounds__(256) splitk_reduce_vec_f32(GemmParams p) {
     const int64_t MN = (int64_t)p.M * p.N;
     const int64_t rows = (int64_t)p.M * p.batch;
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
     for (int64_t row = blockIdx.y; row < rows; row += gridDim.y) {
         const int bz = (int)(row / p.M);
         const int m = (int)(row - (int64_t)bz * p.M);
@@ -367,21 +391,22 @@ __global__ void __launch_bounds__(256) splitk_reduce_vec_f32(GemmParams p) {
         float* crow = p.C + (int64_t)bz * p.c_b + (int64_t)m * p.c_m;
         for (int n = (blockIdx.x * blockDim.x + threadIdx.x) * 4; n < p.N;
              n += gridDim.x * blockDim.x * 4) {
-            f32x4 v = {0.f, 0.f, 0.f, 0.f};
-            for (int s = 0; s < p.splits; ++s)
-                v += *reinterpret_cast<const f32x4*>(src + (int64_t)s * p.batch * MN + n);
-            v += brow;
+            f32x4 bcol = zero, old = zero;
             if (p.bias_axis == 2)
-                for (int e = 0; e < 4; ++e) v[e] += p.bias[(int64_t)(n + e) * p.bias_stride];
+                for (int e = 0; e < 4; ++e) bcol[e] = p.bias[(int64_t)(n + e) * p.bias_stride];
+            if (p.beta != 0.f) {
+                if (p.c_vec) old = *reinterpret_cast<const f32x4*>(crow + col_offset(p, n));
+                else
+                    for (int e = 0; e < 4; ++e) old[e] = crow[col_offset(p, n + e)];
+            }
+            f32x4 v = sum_partials<f32x4>(src + n, p.batch * MN, p.splits, zero);
+            v += brow;
+            if (p.bias_axis == 2) v += bcol;
+            if (p.beta != 0.f) v += p.beta * old;
             if (p.c_vec) {
-                f32x4* dst = reinterpret_cast<f32x4*>(crow + col_offset(p, n));
-                if (p.beta != 0.f) v += p.beta * *dst;
-                *dst = v;
+                *reinterpret_cast<f32x4*>(crow + col_offset(p, n)) = v;
             } else {
-                for (int e = 0; e < 4; ++e) {
-                    float* dst = crow + col_offset(p, n + e);
-                    *dst = (p.beta != 0.f ? p.beta * *dst : 0.f) + v[e];
-                }
+                for (int e = 0; e < 4; ++e) crow[col_offset(p, n + e)] = v[e];
             }
         }
     }
