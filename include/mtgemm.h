@@ -50,7 +50,7 @@ typedef struct mt_mat_f32 {
     int64_t offset;
     int64_t rows, cols;
     int64_t row_stride, col_stride;
-    int64_t batch;          /* >= 1 */
+    int64_t batch;          /* >= 0 (0: an empty stack) */
     int64_t batch_stride;   /* 0: the same matrix for every batch entry */
 } mt_mat_f32;
 

@@ -159,7 +159,7 @@ def mat(t: torch.Tensor) -> MatF32:
     else:
         raise ValueError("expected a 2-D or 3-D tensor")
     base = t.untyped_storage().data_ptr()
-    return MatF32(base, t.storage_offset(), rows, cols, rs, cs, max(batch, 1), bs)
+    return MatF32(base, t.storage_offset(), rows, cols, rs, cs, batch, bs)
 
 
 def _stream(stream=None) -> int:

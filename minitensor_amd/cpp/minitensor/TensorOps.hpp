@@ -48,8 +48,7 @@ inline mt_mat_f32 mat(const Tensor<float>& t) {
                           (int64_t)st[0], (int64_t)st[1], 1, 0};
     if (sh.size() == 3)
         return mt_mat_f32{t.data(), (int64_t)t.offset(), (int64_t)sh[1], (int64_t)sh[2],
-                          (int64_t)st[1], (int64_t)st[2], (int64_t)std::max<size_t>(sh[0], 1),
-                          (int64_t)st[0]};
+                          (int64_t)st[1], (int64_t)st[2], (int64_t)sh[0], (int64_t)st[0]};
     throw std::invalid_argument("GEMM operands are 2-D or 3-D");
 }
 

@@ -55,7 +55,7 @@ int device_cu_count() {
 
 bool valid_mat(const mt_mat_f32* X) {
     if (!X) return false;
-    if (X->rows < 0 || X->cols < 0 || X->batch < 1) return false;
+    if (X->rows < 0 || X->cols < 0 || X->batch < 0) return false;
     if (X->row_stride < 0 || X->col_stride < 0 || X->batch_stride < 0 || X->offset < 0) return false;
     if (X->rows >= kMaxDim || X->cols >= kMaxDim || X->batch >= kMaxDim) return false;
     return true;
@@ -321,7 +321,7 @@ int check_gemm(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C,
     *M = A->rows; *N = B->cols; *K = A->cols; *batch = C->batch;
     if ((A->batch != 1 && A->batch != *batch) || (B->batch != 1 && B->batch != *batch))
         return MT_ERR_INVALID;
-    const bool c_empty = (*M == 0 || *N == 0);
+    const bool c_empty = (*M == 0 || *N == 0 || *batch == 0);
     // Two output elements must never share an address.
     if (!c_empty && ((*M > 1 && C->row_stride == 0) || (*N > 1 && C->col_stride == 0) ||
                      (*batch > 1 && C->batch_stride == 0)))
@@ -499,7 +499,7 @@ int run_gemm(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C, int6
         if (ep->bias_axis != MT_BIAS_ROW && ep->bias_axis != MT_BIAS_COL) return MT_ERR_INVALID;
         if (!ep->bias || ep->bias_stride < 0) return MT_ERR_INVALID;
     }
-    if (M == 0 || N == 0) {
+    if (M == 0 || N == 0 || batch == 0) {
         std::snprintf(g_last_config, sizeof g_last_config, "empty");
         return MT_OK;
     }
@@ -538,7 +538,8 @@ int run_gemm(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C, int6
 
 size_t gemm_ws(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C) {
     int64_t M, N, K, batch;
-    if (check_gemm(A, B, C, &M, &N, &K, &batch) != MT_OK || M == 0 || N == 0) return 0;
+    if (check_gemm(A, B, C, &M, &N, &K, &batch) != MT_OK || M == 0 || N == 0 || batch == 0)
+        return 0;
     return plan_ws(M, N, K, batch, device_cu_count());
 }
 

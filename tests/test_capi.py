@@ -52,7 +52,7 @@ BAD = {
     "negative stride": (M(4, 5, rs=-5), M(5, 3), M(4, 3)),
     "negative offset": (M(4, 5, off=-1), M(5, 3), M(4, 3)),
     "batch mismatch": (M(4, 5, batch=3, bs=20), M(5, 3, batch=2, bs=15), M(4, 3, batch=3, bs=12)),
-    "zero batch": (M(4, 5), M(5, 3), M(4, 3, batch=0)),
+    "negative batch": (M(4, 5), M(5, 3), M(4, 3, batch=-1)),
     "C rows alias (stride 0)": (M(4, 5), M(5, 3), M(4, 3, rs=0)),
     "C cols alias (stride 0)": (M(4, 5), M(5, 3), M(4, 3, cs=0)),
     "null C": (M(4, 5), M(5, 3), M(4, 3, base=0)),
@@ -81,6 +81,11 @@ def test_empty_output_is_a_no_op():
     # M == 0 or N == 0: nothing to launch, success (the reference skips the launch too)
     assert mt.lib().mt_gemm_f32(M(0, 5), M(5, 3), M(0, 3), None, None, 0, None) == mt.MT_OK
     assert mt.lib().mt_gemm_f32(M(4, 5), M(5, 0), M(4, 0), None, None, 0, None) == mt.MT_OK
+    # a batch of zero matrices (the reference's bmm loops over no entries)
+    assert mt.lib().mt_gemm_f32(M(4, 5, batch=0, bs=20), M(5, 3, batch=0, bs=15),
+                                M(4, 3, batch=0, bs=12), None, None, 0, None) == mt.MT_OK
+    assert mt.lib().mt_gemm_f32(M(4, 5), M(5, 3), M(4, 3, batch=0, bs=12), None, None, 0,
+                                None) == mt.MT_OK
     assert mt.last_config() == "empty"
 
 
