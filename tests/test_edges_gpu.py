@@ -52,3 +52,34 @@ def test_one_by_one_by_one(dev):
     b = np.array([[-2.0]], np.float32)
     c = mt.matmul(torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev)).cpu().numpy()
     np.testing.assert_array_equal(c, oracle.matmul(a, b))
+
+
+def test_linear_over_zero_rows(dev):
+    # Linear over an empty batch of samples: Y is [0, out]; dX is [0, in],
+    # dW = dYᵀ·X sums over no rows (zeros, plus beta·dW) and so does db.
+    x = torch.empty((0, 6), device=dev)
+    w = torch.from_numpy(oracle.normal((5, 6), 1)).to(dev)
+    b = torch.from_numpy(oracle.normal((5,), 2)).to(dev)
+    y = mt.linear(x, w, b)
+    torch.cuda.synchronize()
+    assert tuple(y.shape) == (0, 5)
+    dy = torch.empty((0, 5), device=dev)
+    dx, dw, db = mt.linear_backward(dy, x, w)
+    torch.cuda.synchronize()
+    assert tuple(dx.shape) == (0, 6)
+    np.testing.assert_array_equal(dw.cpu().numpy(), np.zeros((5, 6), np.float32))
+    np.testing.assert_array_equal(db.cpu().numpy(), np.zeros((5,), np.float32))
+
+
+def test_conv_over_zero_images(dev):
+    x = np.zeros((0, 16, 6, 6), np.float32)
+    wt = oracle.normal((16, 16, 3, 3), 1)
+    X, W = torch.from_numpy(x).to(dev), torch.from_numpy(wt).to(dev)
+    y = mt.conv2d(X, W, torch.zeros(16, device=dev), 1, 1)
+    torch.cuda.synchronize()
+    assert tuple(y.shape) == (0, 16, 6, 6)
+    dx, dw, db = mt.conv2d_backward(X, W, torch.empty((0, 16, 6, 6), device=dev), 1, 1)
+    torch.cuda.synchronize()
+    assert tuple(dx.shape) == (0, 16, 6, 6)
+    np.testing.assert_array_equal(dw.cpu().numpy(), np.zeros_like(wt))
+    np.testing.assert_array_equal(db.cpu().numpy(), np.zeros((16,), np.float32))
