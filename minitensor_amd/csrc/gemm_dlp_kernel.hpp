@@ -146,8 +146,10 @@ gemm_f32_dlp(GemmParams p) {
     // into na/nb and refilling chunk kt's slot with chunk kt+STAGES.  The
     // barrier guards only the refill and the reads, so the first PRE k-steps
     // of MFMAs issue before it: the MFMA pipe has work queued while the waves
-    // synchronize (about 1 % at 4096^3, 3-9 % for the 64x64 tile).
-    constexpr int PRE = 2;
+    // synchronize (about 1 % at 4096^3, 3-9 % for the 64x64 tile).  Three
+    // k-steps for the 64x32 wave tile (8 waves of the 128x128 tile): about
+    // 1 % more at 2048^2 x 1024; equal or slower for the other two.
+    constexpr int PRE = (MB == 2 && NB == 1) ? 3 : 2;
     auto step = [&](int kt, const float (&ca)[MB][8], const float (&cb)[NB][8],
                     float (&na)[MB][8], float (&nb)[NB][8]) {
         if constexpr (PRE > 0) {
