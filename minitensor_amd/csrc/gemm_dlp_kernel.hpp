@@ -18,8 +18,9 @@
 //     alternate (the loop is unrolled by two so that each set is a fixed set
 //     of registers).  The body has no branches, so the scheduler can spread
 //     the fragment reads and the next DMA over the MFMA stream (the
-//     sched_group_barrier pattern in dlp_interleave, used by the 256x256
-//     tile; the 64x64 tile's 8 MFMAs per step leave nothing to spread).
+//     sched_group_barrier patterns in dlp_interleave for the 256x256 tile
+//     and dlp_interleave_reads for the 128x128 one; the 64x64 tile's 8
+//     MFMAs per step do best left to the compiler).
 //   * Ring of STAGES LDS slots, one s_barrier per chunk.  At the barrier of
 //     step kt, chunk kt+1 has landed (each wave waited for its own DMA) and
 //     every wave has retired its reads of chunk kt's slot, which the step then
@@ -60,6 +61,21 @@ __device__ __forceinline__ void dlp_interleave() {
         __builtin_amdgcn_sched_group_barrier(kMfma, NM >= 100 ? 2 : 1, 0);
     }
     __builtin_amdgcn_sched_group_barrier(kMfma, NM, 0);
+}
+
+// The 64x32 wave tile (configuration 6): the refill's DMA first, then one
+// fragment read (up to 24 LDS instructions) per MFMA.  Left to itself the
+// scheduler packs the reads behind the MFMAs: 16 % slower with an
+// n-contiguous B (2048^2 x 1024), 2-4 % with the other layouts.
+template <int LOADS>
+__device__ __forceinline__ void dlp_interleave_reads() {
+    constexpr int kMfma = 0x008, kVmemRead = 0x020, kDsRead = 0x100;
+    __builtin_amdgcn_sched_group_barrier(kVmemRead, LOADS, 0);
+#pragma unroll
+    for (int g = 0; g < 24; ++g) {
+        __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+    }
 }
 
 // The MFMAs of k-steps S0..S1-1 of one chunk.
@@ -167,6 +183,7 @@ gemm_f32_dlp(GemmParams p) {
         dl_frags<LBF, BN, NB>(next + TA::floats, rb, lane, nb);
         mfma_steps<MB, NB, PRE, 8>(acc, ca, cb);
         if constexpr (MB * NB * 8 >= 128) dlp_interleave<(8 - PRE) * MB * NB>();
+        else if constexpr (MB == 2 && NB == 1) dlp_interleave_reads<LOADS>();
     };
 
     int kt = 0;
