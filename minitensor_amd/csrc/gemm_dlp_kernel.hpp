@@ -11,7 +11,7 @@
 //     one workgroup per CU, where each SIMD again holds a single wave and the
 //     fragment-read latency after every barrier is exposed.
 //   * 128x128 block tile, eight waves of 64x32 (two per SIMD), for K ranges
-//     of at least 512 per split.
+//     of at least 512 per split (256 when every workgroup has a CU).
 // Structure:
 //   * With no second wave on the SIMD to cover the LDS latency, chunk kt+1's
 //     fragments are read while chunk kt's MFMAs issue: two register sets

@@ -132,8 +132,12 @@ constexpr CfgCost kDlCost[kNumDlCfg] = {    // direct-to-LDS kernel, vector layo
     {DlCfg<6>::BM, DlCfg<6>::BN, 0.90, 3}};
 // Configuration 6 pays off only over long K ranges (short ones, such as the
 // 64-deep batched GEMM of the benchmark, run up to 20 % slower than
-// configuration 1): the planner offers it for K per split >= kDlp6MinK.
+// configuration 1): the planner offers it for K per split >= kDlp6MinK, or
+// >= kDlp6MinKOneRound when every workgroup gets a CU of its own (about 4 %
+// faster than configuration 1 at 2048^2 x 256; with several rounds the four
+// co-resident workgroups of configuration 1 win).
 constexpr int kDlp6MinK = 512;
+constexpr int kDlp6MinKOneRound = 256;
 struct CostModel {
     double round_latency = 6200.0;           // cycles of fill/drain per round
     double epilogue_bytes_per_cycle = 7.9;   // one workgroup's tile store
@@ -178,9 +182,11 @@ Plan make_plan_uncached(int64_t M, int64_t N, int64_t K, int64_t batch, int cus,
             if (s > 1 && !allow_split) break;
             const Plan pl = cfg_plan(cc, cfg, dl, M, N, K, batch, s);
             if (s > 1 && pl.kps < 64) break;
-            if (dl && cfg == 6 && std::min<int64_t>(pl.kps, K) < kDlp6MinK) break;
+            const int64_t k6 = std::min<int64_t>(pl.kps, K);
+            if (dl && cfg == 6 && k6 < kDlp6MinKOneRound) break;
             if (pl.splits != s) continue;
             const int64_t wgs = (int64_t)pl.tiles_m * pl.tiles_n * batch * pl.splits;
+            if (dl && cfg == 6 && k6 < kDlp6MinK && wgs > cus) continue;
             if (wgs * 512 >= ((int64_t)1 << 32)) continue;
             const double per_cu = std::ceil((double)wgs / cus);
             const double rounds = std::ceil((double)wgs / ((double)cus * cc.occ));
