@@ -3,19 +3,35 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-secondary] [--no-cpu]
 
 Headline (benchmark config 2): one step = one C[4096,4096] = A·B fp32 GEMM,
-A,B ~ U(-1,1), all operands resident in HBM.  `value` is TFLOPS =
-2·4096³ / (mean step time), timed with HIP events on the launch stream over
-exactly K steps bracketed by device synchronisation.  The GEMM is a single
-kernel launch per step, so the roofline figure uses the same events.
+A,B ~ U(-1,1), all operands resident in HBM.  Protocol:
+  1. W untimed warm-up steps;
+  2. an untimed pre-roll of steps for about 200 ms of GPU time -- the length
+     of the reference's adaptive trial window (test/benchmark.cpp:171-181) --
+     so that the timed steps do not run on the clock ramp out of idle;
+  3. exactly K timed steps, a HIP event recorded on the launch stream before
+     the first and after every step.
+`value` is TFLOPS = 2·4096³ / (mean step time), the mean being the span of
+the K steps over K.  min and median of the per-step times are reported
+beside it.  The GEMM is one kernel launch per step, so the roofline's
+`achieved` uses the same events.  After the timed steps, `reference_window`
+repeats the reference's own protocol (one timed call, then 200 ms / that
+time trials) for comparison; it is not `value`.
 
-Secondary lines (the other benchmark configs: ms and TFLOPS, and HBM GB/s for
-the batched one) are reported under "secondary".  Their kernels take 10-100
-us, less than a Python/ctypes call, so `ms` is device time: 20 calls are
-captured into a HIP graph and the graph is replayed between HIP events.
-`ms_eager_python` is the same calls from a Python loop, for comparison.
-The CPU baseline times the reference's own matmul_cpu (oracle/_ref, built
-from the reference headers; the C restatement in oracle/ when that build is
-absent) on a 64-row sample of the same GEMM, single-threaded.
+Secondary lines (the other benchmark configs: ms and TFLOPS, HBM GB/s for
+the batched one) are reported under "secondary".  Their kernels take
+10-100 us, less than a Python/ctypes call, so `ms` is device time: 20 calls
+are captured into a HIP graph and the graph is replayed between HIP events;
+min / median / mean are over the replays.  `ms_eager_python` is the same
+calls from a Python loop.  Config 3 is also timed with B materialised (a
+strided copy into a dense Bᵀ, then the GEMM) to show what the view saves.
+
+CPU baselines (reported baselines only, never the target): the C
+restatement of the reference CPU path in oracle/ (matmul_cpu,
+matmul_cpu_strided, a per-batch matmul_cpu loop for bmm, conv2d_cpu;
+-O2 -ffp-contract=off, bit-exact with the reference's own build), single
+threaded and pinned to one core, on a bounded sample of each workload (rows,
+batch entries or images), best of the stated repetitions, extrapolated
+linearly to the full workload (each sampled unit does the same work).
 Traffic (HBM bytes per launch) is read from the rocprofv3 FETCH_SIZE /
 WRITE_SIZE summary committed under profiles/, or null when absent.
 """
@@ -24,6 +40,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -34,6 +51,7 @@ sys.path.insert(0, str(ROOT))
 PEAK_TFLOPS = 157.3      # MI355X dense fp32 MFMA
 PEAK_HBM_GBS = 8000.0    # MI355X HBM3E
 TRAFFIC_FILE = ROOT / "profiles" / "traffic_gemm_f32_4096.json"
+PREROLL_MS = 200.0
 
 
 def parse():
@@ -52,6 +70,60 @@ def parse():
     return p.parse_args()
 
 
+def _stats(per_ms) -> dict:
+    return {"min": round(min(per_ms), 5), "median": round(statistics.median(per_ms), 5),
+            "mean": round(sum(per_ms) / len(per_ms), 5)}
+
+
+def time_steps(step, steps: int, warmup: int, preroll_ms: float = PREROLL_MS):
+    """Warm-up, ~preroll_ms of untimed steps, then `steps` timed steps with an
+    event after each.  Returns (span ms of the timed steps, per-step ms list,
+    pre-roll step count)."""
+    import torch
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    n_pre = 0
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < preroll_ms:
+        for _ in range(8):   # enqueue a few, then wait, so the queue stays short
+            step()
+        n_pre += 8
+        torch.cuda.synchronize()
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    evs[0].record(stream)
+    for i in range(steps):
+        step()
+        evs[i + 1].record(stream)
+    torch.cuda.synchronize()
+    per = [evs[i].elapsed_time(evs[i + 1]) for i in range(steps)]
+    return evs[0].elapsed_time(evs[-1]), per, n_pre
+
+
+def reference_window(step) -> dict:
+    """The reference's adaptive protocol (test/benchmark.cpp:171-181): one
+    call timed by the host clock around two device syncs, trials = 200 ms /
+    that time, min(5, trials) warm-up calls, then the mean over the trials."""
+    import torch
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    step()
+    torch.cuda.synchronize()
+    one_ms = (time.perf_counter() - t0) * 1e3
+    trials = max(1, int(200.0 / max(one_ms, 0.01)))
+    for _ in range(min(5, trials)):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(trials):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    return {"trials": trials, "ms_mean": round(e0.elapsed_time(e1) / trials, 5)}
+
+
 def time_events(fn, iters: int, warmup: int) -> float:
     """Mean ms per call of fn over `iters` calls, HIP events on the current stream."""
     import torch
@@ -68,10 +140,11 @@ def time_events(fn, iters: int, warmup: int) -> float:
     return start.elapsed_time(stop) / iters
 
 
-def time_graph(fn, calls: int = 20, replays: int = 10) -> float:
-    """Mean device ms per call of fn: `calls` calls captured into one HIP graph,
-    replayed `replays` times between HIP events.  Removes the Python/ctypes
-    launch overhead, which exceeds the kernel time of the small configs."""
+def time_graph(fn, calls: int = 20, replays: int = 10) -> list:
+    """Device ms per call of fn for each replay: `calls` calls captured into
+    one HIP graph, replayed `replays` times with an event around each replay.
+    Removes the Python/ctypes launch overhead, which exceeds the kernel time
+    of the small configs."""
     import torch
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -84,25 +157,25 @@ def time_graph(fn, calls: int = 20, replays: int = 10) -> float:
     with torch.cuda.graph(graph):
         for _ in range(calls):
             fn()
-    graph.replay()
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(replays):
+    for _ in range(3):
         graph.replay()
-    stop.record()
     torch.cuda.synchronize()
-    ms = start.elapsed_time(stop) / (replays * calls)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(replays + 1)]
+    evs[0].record()
+    for i in range(replays):
+        graph.replay()
+        evs[i + 1].record()
+    torch.cuda.synchronize()
+    per = [evs[i].elapsed_time(evs[i + 1]) / calls for i in range(replays)]
     del graph
-    return ms
+    return per
 
 
 SECONDARY = ("c1", "c3", "c4", "c5a", "c5b")
 
 
 def secondary(dev, only=SECONDARY) -> dict:
-    """benchmark configs 1, 3, 4, 5 (ms, TFLOPS; GB/s for the HBM-near batched one)."""
+    """Benchmark configs 1, 3, 4, 5 (ms, TFLOPS; GB/s for the HBM-near batched one)."""
     import ctypes
     import torch
     import minitensor_amd as mt
@@ -119,13 +192,16 @@ def secondary(dev, only=SECONDARY) -> dict:
     out = {}
 
     def both(fn, iters, warmup):
-        """(device ms from graph replay, eager ms of the Python call loop)."""
+        """(per-replay device ms from graph replay, eager ms of the Python call loop)."""
         eager = time_events(fn, iters, warmup)
         return time_graph(fn), eager
 
     def rec(name, times, flops, bytes_=None, cfg=None):
-        ms, eager = times
-        d = {"ms": round(ms, 5), "ms_eager_python": round(eager, 5),
+        per, eager = times
+        st = _stats(per)
+        ms = st["mean"]
+        d = {"ms": ms, "ms_min": st["min"], "ms_median": st["median"],
+             "ms_eager_python": round(eager, 5),
              "tflops": round(flops / ms / 1e9, 2),
              "frac_of_fp32_mfma_peak": round(flops / ms / 1e9 / PEAK_TFLOPS, 4)}
         if bytes_ is not None:
@@ -150,8 +226,17 @@ def secondary(dev, only=SECONDARY) -> dict:
         A, B = n(2048, 1024), n(2048, 1024)
         C = torch.empty(2048, 2048, device=dev)
         ws = ws_for(A, B.t(), C)
+        f3 = 2 * 2048 * 2048 * 1024
         ms = both(lambda: mt.gemm(A, B.t(), out=C, ws=ws), 100, 10)
-        rec("c3a_2048x2048x1024_bT_view", ms, 2 * 2048 * 2048 * 1024, None, mt.last_config())
+        rec("c3a_2048x2048x1024_bT_view", ms, f3, None, mt.last_config())
+        # the same product with Bᵀ materialised first: a strided copy into a
+        # dense [1024,2048] buffer (what contiguous() does), then the GEMM
+        Bt = torch.empty(1024, 2048, device=dev)
+        ws_m = ws_for(A, Bt, C)
+        ms = both(lambda: (mt.axpby(B.t(), Bt), mt.gemm(A, Bt, out=C, ws=ws_m)), 100, 10)
+        rec("c3a_materialised_copy_plus_gemm", ms, f3, None, mt.last_config())
+        ms = both(lambda: mt.gemm(A, Bt, out=C, ws=ws_m), 100, 10)
+        rec("c3a_gemm_on_materialised_copy", ms, f3, None, mt.last_config())
         As = A[128:]
         C2 = torch.empty(1920, 2048, device=dev)
         ms = both(lambda: mt.gemm(As, B.t(), out=C2, ws=ws), 100, 10)
@@ -187,8 +272,9 @@ def secondary(dev, only=SECONDARY) -> dict:
         cb = torch.zeros(256, device=dev)
         d = mt.Conv2dDesc(32, 256, 14, 14, 256, 3, 3, 1, 1)
         cws = mt.workspace(mt.lib().mt_conv2d_workspace_f32(ctypes.byref(d)), dev)
+        fc = 2 * 6272 * 256 * 2304
         ms = both(lambda: mt.conv2d(x, w, cb, 1, 1, ws=cws), 100, 10)
-        rec("c5a_conv3x3_n32_c256_14x14", ms, 2 * 6272 * 256 * 2304,
+        rec("c5a_conv3x3_n32_c256_14x14", ms, fc,
             4 * (x.numel() + w.numel() + cb.numel() + 32 * 256 * 196), mt.last_config())
         # the same layer's backward: dX (implicit, flipped weights) and dW (+ db)
         dy = n(32, 256, 14, 14, std=0.01)
@@ -196,10 +282,10 @@ def secondary(dev, only=SECONDARY) -> dict:
         dwb = torch.empty_like(w)
         ms = both(lambda: mt.conv2d_backward(x, w, dy, 1, 1, need_dw=False, need_db=False,
                                              ws=bws), 100, 10)
-        rec("c5a_conv_backward_dx", ms, 2 * 6272 * 256 * 2304, None, mt.last_config())
+        rec("c5a_conv_backward_dx", ms, fc, None, mt.last_config())
         ms = both(lambda: mt.conv2d_backward(x, w, dy, 1, 1, need_dx=False, ws=bws, dw=dwb),
                   100, 10)
-        rec("c5a_conv_backward_dw_db", ms, 2 * 6272 * 256 * 2304, None, mt.last_config())
+        rec("c5a_conv_backward_dw_db", ms, fc, None, mt.last_config())
 
     if "c5b" in only:  # batched 64 x [512,64]·[64,512]
         A, B = u(64, 512, 64), u(64, 64, 512)
@@ -211,31 +297,23 @@ def secondary(dev, only=SECONDARY) -> dict:
     return out
 
 
-def cpu_baseline() -> dict:
-    """The reference CPU matmul on a bounded row sample of the 4096^3 GEMM, 1 thread."""
-    import numpy as np
-    import oracle
+def attach_cpu(sec: dict, cpu: dict) -> None:
+    """Adds each config's CPU baseline (and the GPU speed-up over it) to its entry."""
+    for name, c in cpu.items():
+        if name in sec:
+            c = dict(c)
+            c["gpu_speedup"] = round(c["ms_full_est"] / sec[name]["ms"], 1)
+            sec[name]["cpu"] = c
 
-    rows = 64
+
+def _pin_one_core():
     try:
         os.sched_setaffinity(0, {sorted(os.sched_getaffinity(0))[0]})
     except (AttributeError, OSError):
         pass
-    a = oracle.uniform((rows, 4096), 42)
-    b = oracle.uniform((4096, 4096), 43)
-    c = np.empty((rows, 4096), np.float32)
-    if oracle.ref_available():
-        kind, fn = "reference", lambda: oracle.ref().ref_matmul_f32(
-            oracle._fp(a), oracle._fp(b), oracle._fp(c), rows, 4096, 4096)
-        what = "reference matmul_cpu (include/TensorOps.hpp:139-160, built from its headers)"
-    else:
-        kind, fn = "port", lambda: oracle.lib().ora_matmul(
-            oracle._fp(a), oracle._fp(b), oracle._fp(c), rows, 4096, 4096)
-        what = "C restatement of the reference matmul_cpu (oracle/oracle.c)"
-    t0 = time.perf_counter()
-    fn()
-    dt = time.perf_counter() - t0
-    flops = 2.0 * rows * 4096 * 4096
+
+
+def _host_desc() -> str:
     cpu_model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -244,11 +322,105 @@ def cpu_baseline() -> dict:
                 break
     except OSError:
         pass
-    return {"value": round(flops / dt / 1e12, 6), "unit": "TFLOPS", "cores": 1, "kind": kind,
-            "sample": f"C[{rows},4096] = A[{rows},4096]·B[4096,4096] ({rows} of the 4096 rows of "
-                      f"the headline GEMM), {what}, -O2 -ffp-contract=off, 1 thread pinned; "
-                      f"{dt:.2f} s; host {cpu_model}, {os.cpu_count()} cpus visible",
-            "seconds": round(dt, 3)}
+    return f"host {cpu_model}, {os.cpu_count()} cpus visible"
+
+
+def _cpu_time(fn, reps: int) -> float:
+    best = float("inf")
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        best = min(best, time.perf_counter() - t0)
+    return best
+
+
+def cpu_baseline() -> dict:
+    """The C restatement of the reference matmul_cpu on a bounded row sample
+    of the 4096^3 GEMM, 1 thread pinned (the headline's CPU baseline)."""
+    import numpy as np
+    import oracle
+
+    rows = 64
+    _pin_one_core()
+    a = oracle.uniform((rows, 4096), 42)
+    b = oracle.uniform((4096, 4096), 43)
+    c = np.empty((rows, 4096), np.float32)
+    dt = _cpu_time(lambda: oracle.lib().ora_matmul(oracle._fp(a), oracle._fp(b), oracle._fp(c),
+                                                    rows, 4096, 4096), 1)
+    flops = 2.0 * rows * 4096 * 4096
+    return {"value": round(flops / dt / 1e12, 6), "unit": "TFLOPS", "cores": 1, "kind": "port",
+            "sample": f"C[{rows},4096] = A[{rows},4096]·B[4096,4096] ({rows} of the 4096 rows "
+                      f"of the headline GEMM), 1 rep, C restatement of the reference "
+                      f"matmul_cpu (oracle/oracle.c, include/TensorOps.hpp:139-160; bit-exact "
+                      f"with the reference's own build), -O2 -ffp-contract=off, 1 thread "
+                      f"pinned; {dt:.2f} s; {_host_desc()}",
+            "seconds": round(dt, 3),
+            "ms_full_est": round(dt * 1e3 * 4096 / rows, 1)}
+
+
+def cpu_config_baselines() -> dict:
+    """CPU baselines of the secondary configs: the oracle's restatement of the
+    reference CPU path on a bounded sample of each workload, best of `reps`,
+    extrapolated linearly to the full workload.  About 15 s in total."""
+    import numpy as np
+    import oracle
+
+    _pin_one_core()
+    out = {}
+
+    def rec(name, secs, scale, reps, sample, path):
+        out[name] = {"ms_full_est": round(secs * 1e3 * scale, 2), "sample_ms": round(secs * 1e3, 2),
+                     "reps": reps, "cores": 1, "kind": "port",
+                     "sample": sample, "path": path}
+
+    a = oracle.uniform((256, 512), 42)
+    b = oracle.uniform((512, 512), 43)
+    rec("c1_256x512x512", _cpu_time(lambda: oracle.matmul(a, b), 3), 1.0, 3,
+        "the whole GEMM", "matmul_cpu (include/TensorOps.hpp:139-160)")
+
+    A = oracle.normal((2048, 1024), 42)
+    B = oracle.normal((2048, 1024), 43)
+    rows = 256
+    rec("c3a_2048x2048x1024_bT_view", _cpu_time(lambda: oracle.matmul(A[:rows], B.T), 3),
+        2048 / rows, 3, f"{rows} of 2048 rows, B as a transpose view",
+        "matmul_cpu_strided (include/TensorOps.hpp:162-189)")
+    rec("c3b_1920x2048x1024_slice_bT_view",
+        _cpu_time(lambda: oracle.matmul(A[128:128 + rows], B.T), 3), 1920 / rows, 3,
+        f"{rows} of 1920 rows of the slice A[128:], B as a transpose view",
+        "matmul_cpu_strided (include/TensorOps.hpp:162-189)")
+
+    X = oracle.normal((256, 2048), 42)
+    W = oracle.normal((1000, 2048), 43, std=(2.0 / 2048) ** 0.5)
+    dY = oracle.normal((256, 1000), 44, std=0.01)
+    t_f = _cpu_time(lambda: oracle.matmul(X[:64], W.T), 3)
+    t_dx = _cpu_time(lambda: oracle.matmul(dY[:64], W), 3)
+    t_dw = _cpu_time(lambda: oracle.matmul(dY.T[:250], X), 3)
+    t_db = _cpu_time(lambda: oracle.colsum(dY), 3)
+    path4 = "matmul_cpu_strided through transpose views (include/Autograd.hpp:117-147)"
+    rec("c4_linear_fwd", t_f, 256 / 64, 3, "64 of 256 rows of Y = X·Wᵀ", path4)
+    rec("c4_linear_dx", t_dx, 256 / 64, 3, "64 of 256 rows of dX = dY·W", path4)
+    rec("c4_linear_dw_db", t_dw, 1000 / 250, 3, "250 of 1000 rows of dW = dYᵀ·X (db: whole)",
+        path4 + " + sum_cpu for db (include/TensorOps.hpp:190-233)")
+    out["c4_linear_dw_db"]["ms_full_est"] = round((t_dw * 1000 / 250 + t_db) * 1e3, 2)
+    rec("c4_linear_fwd_bwd_total", 0.0, 1.0, 3, "sum of the three rows above", path4)
+    out["c4_linear_fwd_bwd_total"]["ms_full_est"] = round(
+        sum(out[k]["ms_full_est"] for k in ("c4_linear_fwd", "c4_linear_dx", "c4_linear_dw_db")),
+        2)
+
+    x = oracle.normal((32, 256, 14, 14), 42)
+    w = oracle.normal((256, 256, 3, 3), 43, std=(2.0 / 2304) ** 0.5)
+    imgs = 4
+    rec("c5a_conv3x3_n32_c256_14x14",
+        _cpu_time(lambda: oracle.conv2d(x[:imgs], w, np.zeros(256, np.float32), 1, 1), 1),
+        32 / imgs, 1, f"{imgs} of 32 images", "conv2d_cpu (include/TensorOps.hpp:235-273)")
+
+    Ab = oracle.uniform((64, 512, 64), 42)
+    Bb = oracle.uniform((64, 64, 512), 43)
+    nb = 16
+    rec("c5b_bmm_64x512x512x64", _cpu_time(lambda: oracle.bmm(Ab[:nb], Bb[:nb]), 3), 64 / nb, 3,
+        f"{nb} of 64 batch entries", "matmul_cpu per batch entry (bmm's loop, "
+        "include/TensorOps.hpp:933-991)")
+    return out
 
 
 def main():
@@ -284,23 +456,16 @@ def main():
     def step():
         mt.gemm(A, B, out=C, ws=ws)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    ev0.record(stream)
-    for _ in range(args.steps):
-        step()
-    ev1.record(stream)
-    torch.cuda.synchronize()
+    span_ms, per_ms, n_pre = time_steps(step, args.steps, args.warmup)
     wall = time.perf_counter() - t0
-    ms = ev0.elapsed_time(ev1) / args.steps
+    ms = span_ms / args.steps
     kernel_cfg = mt.last_config()
     flops = 2.0 * M * N * K
     tflops = flops / ms / 1e9
+    st = _stats(per_ms)
+    ref_win = reference_window(step)
+    ref_win["tflops"] = round(flops / ref_win["ms_mean"] / 1e9, 3)
 
     if args.copy_probe:  # 256 MiB device copy, for FETCH/WRITE_SIZE calibration
         src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
@@ -324,6 +489,10 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 5),
+        "ms_per_step_min": st["min"],
+        "ms_per_step_median": st["median"],
+        "tflops_at_min": round(flops / st["min"] / 1e9, 3),
+        "tflops_at_median": round(flops / st["median"] / 1e9, 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -331,15 +500,19 @@ def main():
         "data": "synthetic (U(-1,1), torch generator seed 42, resident in HBM)",
         "config": {"workload": "benchmark config 2: C[4096,4096] = A[4096,4096]·B[4096,4096] "
                                "fp32 row-major GEMM", "M": M, "N": N, "K": K,
-                   "kernel": kernel_cfg, "wall_s_timed_region": round(wall, 4)},
+                   "kernel": kernel_cfg, "preroll_steps": n_pre,
+                   "wall_s_warmup_preroll_timed": round(wall, 4)},
+        "reference_window": ref_win,
         "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_TFLOPS, 4),
                      "traffic": traffic},
     }
     if not args.no_secondary:
         line["secondary"] = secondary(dev)
-    if not args.no_cpu:
+    if not args.no_cpu:   # after every GPU leg, so the GPU never idles between them
         line["cpu_baseline"] = cpu_baseline()
+        if not args.no_secondary:
+            attach_cpu(line["secondary"], cpu_config_baselines())
     print(json.dumps(line), flush=True)
 
 

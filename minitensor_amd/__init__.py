@@ -167,6 +167,31 @@ def _stream(stream=None) -> int:
     return s.cuda_stream
 
 
+def _on(stream):
+    """Makes `stream` current for the body of an API call, so that the
+    outputs, workspaces and operand copies it allocates belong to the stream
+    its kernels run on (torch's caching allocator recycles a block only after
+    the work queued on its stream), and so that those copies are ordered
+    before the kernels that read them."""
+    return torch.cuda.stream(stream) if stream is not None else contextlib.nullcontext()
+
+
+def _api(fn):
+    """Runs fn under _on(stream) for its `stream` argument, however passed."""
+    import functools
+    import inspect
+
+    sig = inspect.signature(fn)
+    pos = list(sig.parameters).index("stream")
+
+    @functools.wraps(fn)
+    def wrapper(*args, **kwargs):
+        stream = args[pos] if len(args) > pos else kwargs.get("stream")
+        with _on(stream):
+            return fn(*args, **kwargs)
+    return wrapper
+
+
 def workspace(nbytes: int, device) -> Optional[torch.Tensor]:
     if nbytes == 0:
         return None
@@ -177,6 +202,7 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
+@_api
 def gemm(A: torch.Tensor, B: torch.Tensor, out: Optional[torch.Tensor] = None,
          bias: Optional[torch.Tensor] = None, bias_axis: int = BIAS_NONE, beta: float = 0.0,
          ws: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
@@ -231,6 +257,7 @@ def bmm(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
     return gemm(A, B)
 
 
+@_api
 def linear(x: torch.Tensor, w: torch.Tensor, b: Optional[torch.Tensor] = None,
            out: Optional[torch.Tensor] = None, ws: Optional[torch.Tensor] = None,
            stream=None) -> torch.Tensor:
@@ -251,6 +278,7 @@ def linear(x: torch.Tensor, w: torch.Tensor, b: Optional[torch.Tensor] = None,
     return out
 
 
+@_api
 def linear_backward(dy: torch.Tensor, x: torch.Tensor, w: torch.Tensor, need_dx: bool = True,
                     need_dw: bool = True, need_db: bool = True, dx=None, dw=None, db=None,
                     beta_w: float = 0.0, beta_b: float = 0.0, ws=None, stream=None):
@@ -276,6 +304,7 @@ def linear_backward(dy: torch.Tensor, x: torch.Tensor, w: torch.Tensor, need_dx:
     return dx, dw, db
 
 
+@_api
 def colsum(x: torch.Tensor, out: Optional[torch.Tensor] = None, beta: float = 0.0,
            stream=None) -> torch.Tensor:
     _require_gpu(x, out)
@@ -293,6 +322,7 @@ def conv_out_size(inp: int, pad: int, k: int, stride: int) -> int:
     return (inp + 2 * pad - k) // stride + 1
 
 
+@_api
 def conv2d(x: torch.Tensor, w: torch.Tensor, b: Optional[torch.Tensor] = None, stride: int = 1,
            padding: int = 0, ws: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
     """The reference's conv2d forward on NCHW tensors as one fused GEMM.
@@ -321,6 +351,7 @@ def conv2d(x: torch.Tensor, w: torch.Tensor, b: Optional[torch.Tensor] = None, s
     return out
 
 
+@_api
 def conv2d_backward(x: torch.Tensor, w: torch.Tensor, dy: torch.Tensor, stride: int = 1,
                     padding: int = 0, need_dx: bool = True, need_dw: bool = True,
                     need_db: bool = True, ws: Optional[torch.Tensor] = None, stream=None,
@@ -363,6 +394,7 @@ def conv2d_backward(x: torch.Tensor, w: torch.Tensor, dy: torch.Tensor, stride: 
     return dx, dw, db
 
 
+@_api
 def axpby(x: torch.Tensor, y: torch.Tensor, alpha: float = 1.0, beta: float = 0.0,
           stream=None) -> torch.Tensor:
     """y = alpha·x + beta·y in place over 2-D/3-D views (x may have batch 1:

@@ -24,7 +24,6 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "liboracle.so"
 REF_PATH = HERE / "_ref" / "libref.so"
-REF_GPU_PATH = HERE / "_ref" / "libref_gpu.so"
 
 _f = ctypes.POINTER(ctypes.c_float)
 _d = ctypes.POINTER(ctypes.c_double)
@@ -40,9 +39,6 @@ def build() -> None:
     subprocess.run(["make", "-s", "-C", str(HERE), "all"], check=True)
     if Path("/root/reference/include/TensorOps.hpp").exists():
         subprocess.run(["make", "-s", "-C", str(HERE), "ref"], check=True)
-    if Path("/root/reference/src/gpu_ops.cpp").exists():
-        subprocess.run(["make", "-s", "-C", str(HERE), "ref_gpu"], check=True,
-                       stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL)
 
 
 def lib() -> ctypes.CDLL:
@@ -71,40 +67,6 @@ def lib() -> ctypes.CDLL:
 
 def ref_available() -> bool:
     return REF_PATH.exists()
-
-
-_ref_gpu = None
-
-
-def ref_gpu_available() -> bool:
-    return REF_GPU_PATH.exists()
-
-
-def ref_gpu_matmul(a: np.ndarray, b: np.ndarray, which: int = 0, warmup: int = 2,
-                   reps: int = 5):
-    """The reference's own GPU matmul on this GPU (oracle/_ref/libref_gpu.so):
-    which 0 = matmul_gpu on A [M,K]·B [K,N] (src/gpu_ops.cpp:1103-1144);
-    which 1 = matmul_gpu_strided on A·Bᵀ with b holding Bᵀ [N,K] (1199-1223).
-    Returns (C [M,N], ms per call)."""
-    global _ref_gpu
-    if _ref_gpu is None:
-        h = ctypes.CDLL(str(REF_GPU_PATH))
-        h.ref_gpu_matmul_f32.argtypes = [_f, _f, _f, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                         ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                         ctypes.POINTER(ctypes.c_double)]
-        h.ref_gpu_matmul_f32.restype = ctypes.c_int
-        _ref_gpu = h
-    a = np.ascontiguousarray(a, np.float32)
-    b = np.ascontiguousarray(b, np.float32)
-    M, K = a.shape
-    N = b.shape[0] if which == 1 else b.shape[1]
-    c = np.empty((M, N), np.float32)
-    ms = ctypes.c_double(0.0)
-    rc = _ref_gpu.ref_gpu_matmul_f32(_fp(a), _fp(b), _fp(c), M, K, N, which, warmup, reps,
-                                     ctypes.byref(ms))
-    if rc != 0:
-        raise RuntimeError("reference GPU matmul failed")
-    return c, ms.value
 
 
 def ref() -> ctypes.CDLL:

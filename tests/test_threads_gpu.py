@@ -89,3 +89,31 @@ def test_forced_config_is_per_thread(dev):
     print(seen)
     assert seen["forced"].startswith("rs 128x128") and seen["forced"].endswith("cfg=1")
     assert seen["auto"].startswith("dl "), seen["auto"]
+
+
+def test_explicit_stream_without_context(dev):
+    """stream= without a `with torch.cuda.stream(...)` block: the workspace and
+    the output the call allocates belong to that stream, so work queued on
+    the current stream right after the call cannot be handed the workspace
+    while the split-K kernels still use it."""
+    a = oracle.uniform((300, 1000), 31)
+    b = oracle.uniform((1000, 260), 32)
+    A = torch.from_numpy(a).to(dev)
+    B = torch.from_numpy(b).to(dev)
+    torch.cuda.synchronize()
+    want = oracle.matmul(a, b)
+    s = torch.cuda.Stream()
+    outs = []
+    for _ in range(4):
+        with mt.forced_config(mt.FAMILY_DL, 2, 8):   # 64x64 tiles, 8 K splits: partials
+            outs.append(mt.gemm(A, B, stream=s))
+        assert "split=8" in mt.last_config(), mt.last_config()
+        # allocations and writes on the current stream, while s may still run
+        junk = [torch.full((1 << 18,), 7.0, device=dev) for _ in range(16)]
+        del junk
+    s.synchronize()
+    torch.cuda.synchronize()
+    for C in outs:
+        got = C.cpu().numpy()
+        err = float(np.max(np.abs(got.astype(np.float64) - want)))
+        assert err <= oracle.tolerance(1000, 1.0, 1.0), err
