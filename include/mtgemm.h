@@ -194,7 +194,9 @@ const char* mt_last_config(void);
 enum {
     MT_FAMILY_AUTO = 0,  /* the cost model chooses (default)                   */
     MT_FAMILY_RS = 1,    /* register-staged kernel: any operand layout          */
-    MT_FAMILY_DL = 2     /* direct-to-LDS kernel: k- or mn-contiguous operands  */
+    MT_FAMILY_DL = 2,    /* direct-to-LDS kernel: k- or mn-contiguous operands  */
+    MT_FAMILY_KSW = 3    /* wave-split kernel: small tiles, K split across the
+                            waves of a workgroup; any operand layout            */
 };
 /* Number of tile configurations of a family (0 for MT_FAMILY_AUTO). */
 int mt_gemm_config_count(int family);

@@ -409,7 +409,7 @@ def last_config() -> str:
     return lib().mt_last_config().decode()
 
 
-FAMILY_AUTO, FAMILY_RS, FAMILY_DL = 0, 1, 2
+FAMILY_AUTO, FAMILY_RS, FAMILY_DL, FAMILY_KSW = 0, 1, 2, 3
 
 
 def config_count(family: int) -> int:

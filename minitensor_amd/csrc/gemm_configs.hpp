@@ -91,4 +91,19 @@ GemmLaunchFn dl_rowsum_launcher_cfg1();
 GemmLaunchFn dl_rowsum_launcher_cfg2();
 GemmLaunchFn dl_rowsum_launcher_cfg3();
 
+// Wave-split kernel (gemm_ksw_kernel.hpp): tile (32*MB) x (32*NB), W waves
+// splitting the tile's K range, D chunks in flight per wave.  Any operand
+// layout: VA / VB select 16-byte fragment loads for k-contiguous operands
+// (L_KV) or scalar ones (every other layout).
+template <int CFG> struct KswCfg;
+template <> struct KswCfg<0> { static constexpr int MB = 1, NB = 1, W = 4, D = 6; };
+template <> struct KswCfg<1> { static constexpr int MB = 1, NB = 1, W = 8, D = 4; };
+template <> struct KswCfg<2> { static constexpr int MB = 2, NB = 1, W = 4, D = 4; };
+template <> struct KswCfg<3> { static constexpr int MB = 1, NB = 2, W = 4, D = 4; };
+constexpr int kNumKswCfg = 4;
+
+// Configuration cfg of the wave-split kernel; va / vb: A / B is L_KV.
+GemmLaunchFn ksw_launcher(int cfg, bool va, bool vb);
+void ksw_tile(int cfg, int* bm, int* bn);
+
 }  // namespace mtk

@@ -283,6 +283,38 @@ constexpr int stage_blocks() {
     return jp;
 }
 
+// Stores four consecutive output columns n..n+3 of row m (v, the bare sums):
+// C = v + bias + beta*C through col(n), 16-byte when `vec`, element by element
+// otherwise (columns past N skipped); or, for a split-K launch (`part`), the
+// raw partial into the split's workspace slab at `base` (row stride rs).
+__device__ __forceinline__ void store_group4(const GemmParams& p, float* base, int64_t rs,
+                                             bool part, bool vec, int bias_axis, float beta,
+                                             int m, int n, f32x4 v) {
+    float* const row = base + (int64_t)m * rs;
+    const float brow = bias_axis == 1 ? p.bias[(int64_t)m * p.bias_stride] : 0.f;
+    if (vec) {
+        f32x4 o;
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+            o[x] = v[x] + brow;
+            if (bias_axis == 2) o[x] += p.bias[(int64_t)(n + x) * p.bias_stride];
+        }
+        f32x4* const dst = reinterpret_cast<f32x4*>(row + (part ? (int64_t)n : col_offset(p, n)));
+        if (beta != 0.f) o += beta * *dst;
+        *dst = o;
+    } else {
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+            if (n + x >= p.N) break;
+            float o = v[x] + brow;
+            if (bias_axis == 2) o += p.bias[(int64_t)(n + x) * p.bias_stride];
+            float* const dst = row + (part ? (int64_t)(n + x) : col_offset(p, n + x));
+            if (beta != 0.f) o += beta * *dst;
+            *dst = o;
+        }
+    }
+}
+
 // Epilogue of a workgroup of NW waves (wave tiles WM x WN, WAVES_N per tile
 // row) whose first output element is (m0, n0).  `lds` is the kernel's ring of
 // RING floats; the main loop must be finished with it (the first pass waits
@@ -363,30 +395,7 @@ __device__ __forceinline__ void store_tile_lds(const GemmParams& p, const f32x16
                 where(k, &m, &n, &idx);
                 const f32x4 v = sl[idx];
                 if (m >= p.M || n >= p.N) continue;
-                float* const row = base + (int64_t)m * rs;
-                const float brow = bias_axis == 1 ? p.bias[(int64_t)m * p.bias_stride] : 0.f;
-                if (vec) {
-                    f32x4 o;
-#pragma unroll
-                    for (int x = 0; x < 4; ++x) {
-                        o[x] = v[x] + brow;
-                        if (bias_axis == 2) o[x] += p.bias[(int64_t)(n + x) * p.bias_stride];
-                    }
-                    f32x4* const dst =
-                        reinterpret_cast<f32x4*>(row + (part ? (int64_t)n : col_offset(p, n)));
-                    if (beta != 0.f) o += beta * *dst;
-                    *dst = o;
-                } else {
-#pragma unroll
-                    for (int x = 0; x < 4; ++x) {
-                        if (n + x >= p.N) break;
-                        float o = v[x] + brow;
-                        if (bias_axis == 2) o += p.bias[(int64_t)(n + x) * p.bias_stride];
-                        float* const dst = row + (part ? (int64_t)(n + x) : col_offset(p, n + x));
-                        if (beta != 0.f) o += beta * *dst;
-                        *dst = o;
-                    }
-                }
+                store_group4(p, base, rs, part, vec, bias_axis, beta, m, n, v);
             }
         }
 }

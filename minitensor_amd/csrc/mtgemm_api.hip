@@ -87,6 +87,7 @@ const char* layout_name(int l) {
 
 struct Plan {
     bool dl = false;   // direct-to-LDS kernel (both operands in a vector layout)
+    bool ksw = false;  // wave-split kernel (K split across the waves of a workgroup)
     int cfg = 0;       // TileCfg index (register-staged) or DlCfg index (direct-to-LDS)
     int bm = 0, bn = 0;
     int splits = 1;
@@ -130,6 +131,22 @@ constexpr CfgCost kDlCost[kNumDlCfg] = {    // direct-to-LDS kernel, vector layo
     {DlCfg<4>::BM, DlCfg<4>::BN, 0.98, 1},
     {DlCfg<5>::BM, DlCfg<5>::BN, 0.72, 8},
     {DlCfg<6>::BM, DlCfg<6>::BN, 0.90, 3}};
+// Wave-split kernel (configurations of KswCfg): efficiencies from
+// graph-replay timings of every configuration at 1, 2 and 4 K splits on the
+// benchmark's small GEMMs and four neighbouring shapes (one MI355X).  It is
+// L2-bandwidth-bound -- no operand is shared between its waves, about 8 flop
+// per byte read for a 32x32 tile -- so it is offered without split-K only,
+// where the alternative is a split-K plan and its reduction launch: config 1
+// 6.7 vs 9.4 us, the Linear dX GEMM 14.7 vs 18.4 us, 512^3 6.9 vs 11.2 us.
+// (The model prices the split-K reduction from eager timings, above its cost
+// under graph replay; 0.38 for the 32x32 tile keeps the Linear forward GEMM,
+// 17.1 us with split-K against 18.4 us here, on the split-K plan.)
+constexpr CfgCost kKswCost[kNumKswCfg] = {
+    {32 * KswCfg<0>::MB, 32 * KswCfg<0>::NB, 0.38, 8},
+    {32 * KswCfg<1>::MB, 32 * KswCfg<1>::NB, 0.37, 4},
+    {32 * KswCfg<2>::MB, 32 * KswCfg<2>::NB, 0.45, 4},
+    {32 * KswCfg<3>::MB, 32 * KswCfg<3>::NB, 0.45, 4}};
+
 // Configuration 6 pays off only over long K ranges (short ones, such as the
 // 64-deep batched GEMM of the benchmark, run up to 20 % slower than
 // configuration 1): the planner offers it for K per split >= kDlp6MinK, or
@@ -165,10 +182,27 @@ Plan cfg_plan(const CfgCost& cc, int cfg, bool dl, int64_t M, int64_t N, int64_t
     return pl;
 }
 
+// Modelled cycles of one plan (see CostModel).
+double plan_cycles(const CostModel& cm, const CfgCost& cc, const Plan& pl, int64_t M, int64_t N,
+                   int64_t batch, int cus) {
+    const int64_t wgs = (int64_t)pl.tiles_m * pl.tiles_n * batch * pl.splits;
+    const double per_cu = std::ceil((double)wgs / cus);
+    const double rounds = std::ceil((double)wgs / ((double)cus * cc.occ));
+    const double work = (double)cc.bm * cc.bn * (double)std::max<int64_t>(pl.kps, kBK) * 2.0 /
+                        (256.0 * cc.eff);
+    const double epi = (double)cc.bm * cc.bn * 4.0 / cm.epilogue_bytes_per_cycle;
+    double t = per_cu * work + per_cu * epi / cc.occ + rounds * cm.round_latency;
+    if (pl.splits > 1) {
+        const double bytes = (double)(2 * pl.splits + 1) * M * N * batch * 4.0;
+        t += bytes / (cm.bytes_per_cycle) + cm.launch_cycles;
+    }
+    return t;
+}
+
 // wide: the prefetching direct-to-LDS configurations (is_dlp_cfg) may be
-// chosen (see wide_ok in launch_gemm).
+// chosen (see wide_ok in launch_gemm); ksw: the wave-split kernel may be.
 Plan make_plan_uncached(int64_t M, int64_t N, int64_t K, int64_t batch, int cus,
-                        bool allow_split, bool dl, bool wide) {
+                        bool allow_split, bool dl, bool wide, bool ksw) {
     static const CostModel cm;
     const CfgCost* cfgs = dl ? kDlCost : kRsCost;
     const int ncfg = dl ? kNumDlCfg : kNumCfg;
@@ -188,16 +222,20 @@ Plan make_plan_uncached(int64_t M, int64_t N, int64_t K, int64_t batch, int cus,
             const int64_t wgs = (int64_t)pl.tiles_m * pl.tiles_n * batch * pl.splits;
             if (dl && cfg == 6 && k6 < kDlp6MinK && wgs > cus) continue;
             if (wgs * 512 >= ((int64_t)1 << 32)) continue;
-            const double per_cu = std::ceil((double)wgs / cus);
-            const double rounds = std::ceil((double)wgs / ((double)cus * cc.occ));
-            const double work = (double)cc.bm * cc.bn * (double)std::max<int64_t>(pl.kps, kBK) *
-                                2.0 / (256.0 * cc.eff);
-            const double epi = (double)cc.bm * cc.bn * 4.0 / cm.epilogue_bytes_per_cycle;
-            double t = per_cu * work + per_cu * epi / cc.occ + rounds * cm.round_latency;
-            if (pl.splits > 1) {
-                const double bytes = (double)(2 * pl.splits + 1) * M * N * batch * 4.0;
-                t += bytes / (cm.bytes_per_cycle) + cm.launch_cycles;
+            const double t = plan_cycles(cm, cc, pl, M, N, batch, cus);
+            if (t < best_t) {
+                best_t = t;
+                best = pl;
             }
+        }
+    }
+    if (ksw) {
+        for (int cfg = 0; cfg < kNumKswCfg; ++cfg) {
+            Plan pl = cfg_plan(kKswCost[cfg], cfg, false, M, N, K, batch, 1);
+            pl.ksw = true;
+            const int64_t wgs = (int64_t)pl.tiles_m * pl.tiles_n * batch;
+            if (wgs * 512 >= ((int64_t)1 << 32)) continue;
+            const double t = plan_cycles(cm, kKswCost[cfg], pl, M, N, batch, cus);
             if (t < best_t) {
                 best_t = t;
                 best = pl;
@@ -211,11 +249,11 @@ Plan make_plan_uncached(int64_t M, int64_t N, int64_t K, int64_t batch, int cus,
 // for the same few shapes again and again (workspace query, then launch), so
 // each thread keeps its last few plans.
 Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool allow_split,
-               bool dl, bool wide) {
+               bool dl, bool wide, bool ksw) {
     struct Entry {
         int64_t M = -1, N = -1, K = -1, batch = -1;
         int cus = 0;
-        bool allow_split = false, dl = false, wide = false;
+        bool allow_split = false, dl = false, wide = false, ksw = false;
         Plan plan;
     };
     constexpr int kEntries = 8;
@@ -223,12 +261,12 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool all
     thread_local int next = 0;
     for (const Entry& e : cache)
         if (e.M == M && e.N == N && e.K == K && e.batch == batch && e.cus == cus &&
-            e.allow_split == allow_split && e.dl == dl && e.wide == wide)
+            e.allow_split == allow_split && e.dl == dl && e.wide == wide && e.ksw == ksw)
             return e.plan;
     Entry& e = cache[next];
     next = (next + 1) % kEntries;
-    e = Entry{M, N, K, batch, cus, allow_split, dl, wide,
-              make_plan_uncached(M, N, K, batch, cus, allow_split, dl, wide)};
+    e = Entry{M, N, K, batch, cus, allow_split, dl, wide, ksw,
+              make_plan_uncached(M, N, K, batch, cus, allow_split, dl, wide, ksw)};
     return e.plan;
 }
 
@@ -247,6 +285,13 @@ thread_local ForcedConfig g_forced;
 bool forced_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dl_ok, bool rs_ok,
                  bool wide_ok, Plan* out) {
     const ForcedConfig f = g_forced;
+    if (f.family == MT_FAMILY_KSW && rs_ok) {
+        int bm, bn;
+        ksw_tile(f.cfg, &bm, &bn);
+        *out = cfg_plan(CfgCost{bm, bn, 1.0, 1}, f.cfg, false, M, N, K, batch, f.splits);
+        out->ksw = true;
+        return true;
+    }
     if (f.family == MT_FAMILY_DL && dl_ok && (!is_dlp_cfg(f.cfg) || wide_ok)) {
         *out = cfg_plan(kDlCost[f.cfg], f.cfg, true, M, N, K, batch, f.splits);
         return true;
@@ -294,15 +339,18 @@ GemmLaunchFn conv_launcher(int cfg) {
 // Workspace that covers the plan of either kernel family (for sizes queried
 // before the operand pointers, and hence the layouts, are known).
 size_t plan_ws(int64_t M, int64_t N, int64_t K, int64_t batch, int cus) {
-    size_t ws = std::max({make_plan(M, N, K, batch, cus, true, false, false).ws_bytes,
-                          make_plan(M, N, K, batch, cus, true, true, false).ws_bytes,
-                          make_plan(M, N, K, batch, cus, true, true, true).ws_bytes});
+    size_t ws = 0;
+    for (bool dl : {false, true})
+        for (bool wide : {false, true})
+            for (bool ksw : {false, true})
+                ws = std::max(ws, make_plan(M, N, K, batch, cus, true, dl, wide, ksw).ws_bytes);
     Plan forced;
     if (forced_plan(M, N, K, batch, true, true, true, &forced)) ws = std::max(ws, forced.ws_bytes);
     return ws;
 }
 
 GemmLaunchFn pick_launcher(const Plan& plan, int la, int lb, bool ktail) {
+    if (plan.ksw) return ksw_launcher(plan.cfg, la == L_KV, lb == L_KV);
     if (plan.dl) {
         switch (plan.cfg) {
             case 0: return dl_launcher_cfg0(la, lb);
@@ -439,9 +487,12 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
         if (plan.splits > 1 && (workspace == nullptr || ws_bytes < plan.ws_bytes))
             return MT_ERR_WORKSPACE;
     } else {
-        plan = make_plan(M, N, K, batch, device_cu_count(), true, dl, wide_ok);
+        // the wave-split kernel takes every operand form but the implicit
+        // convolution operands and the fused row sums
+        const bool ksw_ok = !implicit && p.rowsum == nullptr;
+        plan = make_plan(M, N, K, batch, device_cu_count(), true, dl, wide_ok, ksw_ok);
         if (plan.splits > 1 && (workspace == nullptr || ws_bytes < plan.ws_bytes))
-            plan = make_plan(M, N, K, batch, device_cu_count(), false, dl, wide_ok);
+            plan = make_plan(M, N, K, batch, device_cu_count(), false, dl, wide_ok, ksw_ok);
     }
     // Row sums of A are fused only into a direct-to-LDS launch of two
     // mn-contiguous operands without split-K (the caller sees p.rowsum cleared
@@ -459,7 +510,8 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
     const int64_t nblocks = (int64_t)plan.tiles_m * plan.tiles_n * plan.splits * batch;
     if (nblocks >= ((int64_t)1 << 31)) return MT_ERR_UNSUPPORTED;
     std::snprintf(g_last_config, sizeof g_last_config,
-                  "%s %dx%d a=%s b=%s split=%d wgs=%lld cfg=%d", plan.dl ? "dl" : "rs", plan.bm,
+                  "%s %dx%d a=%s b=%s split=%d wgs=%lld cfg=%d",
+                  plan.ksw ? "ksw" : plan.dl ? "dl" : "rs", plan.bm,
                   plan.bn, layout_name(la), layout_name(lb), plan.splits, (long long)nblocks,
                   plan.cfg);
 
@@ -1247,7 +1299,10 @@ int mt_version(void) { return MTGEMM_VERSION; }
 const char* mt_last_config(void) { return g_last_config; }
 
 int mt_gemm_config_count(int family) {
-    return family == MT_FAMILY_RS ? kNumCfg : family == MT_FAMILY_DL ? kNumDlCfg : 0;
+    return family == MT_FAMILY_RS    ? kNumCfg
+           : family == MT_FAMILY_DL  ? kNumDlCfg
+           : family == MT_FAMILY_KSW ? kNumKswCfg
+                                     : 0;
 }
 
 int mt_gemm_force_config(int family, int cfg, int splits) {
@@ -1255,7 +1310,7 @@ int mt_gemm_force_config(int family, int cfg, int splits) {
         g_forced = ForcedConfig{};
         return MT_OK;
     }
-    if ((family != MT_FAMILY_RS && family != MT_FAMILY_DL) || cfg < 0 ||
+    if ((family != MT_FAMILY_RS && family != MT_FAMILY_DL && family != MT_FAMILY_KSW) || cfg < 0 ||
         cfg >= mt_gemm_config_count(family) || splits < 1 || splits > kMaxForcedSplits)
         return MT_ERR_INVALID;
     g_forced = ForcedConfig{family, cfg, splits};

@@ -245,6 +245,13 @@ def _views(a, b, ta, tb, dev):
     return A, B
 
 
+# Vector-layout operands go to the direct-to-LDS kernel or, for small output
+# tile counts, to the wave-split kernel; the cost model picks.  (Every
+# configuration of both is also forced on these layouts in
+# test_configs_gpu.py and test_ksw_gpu.py.)
+VECTOR_PATHS = ("dl ", "ksw ")
+
+
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
 @pytest.mark.parametrize("M,N,K", [(260, 132, 1000), (64, 64, 20), (516, 4, 36), (8, 1028, 4)])
 def test_dl_layouts_and_tails(dev, ta, tb, M, N, K):
@@ -252,7 +259,7 @@ def test_dl_layouts_and_tails(dev, ta, tb, M, N, K):
     b = oracle.uniform((K, N), 200 + N)
     A, B = _views(a, b, ta, tb, dev)
     c = run(A, B)
-    assert mt.last_config().startswith("dl "), mt.last_config()
+    assert mt.last_config().startswith(VECTOR_PATHS), mt.last_config()
     assert_close(c, oracle.matmul(a, b), K, amax(a), amax(b), f"dl {M}x{N}x{K} ta={ta} tb={tb}")
 
 
@@ -263,7 +270,7 @@ def test_dl_split_k_and_edges(dev, M, N, K):
     b = oracle.uniform((K, N), 400 + K)
     A, B = to_gpu(a, dev), to_gpu(b, dev)
     c = run(A, B)
-    assert mt.last_config().startswith("dl "), mt.last_config()
+    assert mt.last_config().startswith(VECTOR_PATHS), mt.last_config()
     assert_close(c, oracle.matmul(a, b), K, amax(a), amax(b), f"dl {M}x{N}x{K}")
     np.testing.assert_array_equal(c, run(A, B))   # deterministic, also under split-K
 
@@ -275,7 +282,7 @@ def test_dl_batched_transposed(dev):
     B = to_gpu(b, dev).transpose(1, 2)
     c = mt.gemm(A, B)
     torch.cuda.synchronize()
-    assert mt.last_config().startswith("dl "), mt.last_config()
+    assert mt.last_config().startswith(VECTOR_PATHS), mt.last_config()
     want = oracle.bmm(a, np.ascontiguousarray(b.transpose(0, 2, 1)))
     assert_close(c.cpu().numpy(), want, 100, amax(a), amax(b), "dl batched Bᵀ")
 
@@ -290,7 +297,7 @@ def test_dl_bias_and_beta(dev, axis):
     mt.gemm(to_gpu(a, dev), to_gpu(b, dev), out=C, beta=1.0, bias=to_gpu(bias, dev),
             bias_axis=axis)
     torch.cuda.synchronize()
-    assert mt.last_config().startswith("dl "), mt.last_config()
+    assert mt.last_config().startswith(VECTOR_PATHS), mt.last_config()
     want = oracle.matmul(a, b) + c0 + (bias[:, None] if axis == mt.BIAS_ROW else bias[None, :])
     assert_close(C.cpu().numpy(), want, 300, amax(a), amax(b), f"dl bias {axis} + beta",
                  extra=1e-6)
@@ -365,12 +372,14 @@ def test_split_k_vector_reduce_bias_beta(dev, axis):
 
 # ---- maximum sizes: outputs past 2^31 elements (64-bit addressing) ---------------
 
-@pytest.mark.parametrize("path,forced", [("dl", None), ("dl", 4), ("dl", 5), ("rs", None)],
-                         ids=["dl", "dl4", "dl5", "rs"])
+@pytest.mark.parametrize("path,forced", [("dl", None), ("dl", 4), ("dl", 5), ("rs", None),
+                                         ("ksw", 0)],
+                         ids=["dl", "dl4", "dl5", "rs", "ksw0"])
 def test_output_beyond_2pow31_elements(dev, path, forced):
     # C[40000, 60000] = 2.4e9 elements (9.6 GB): rows past 35791 start beyond
     # 2^31, so any 32-bit element index in a kernel or epilogue would alias.
-    # The cost model's pick, and the two prefetching configurations forced.
+    # The cost model's pick, the two prefetching configurations and the
+    # wave-split kernel forced.
     M, N, K = 40000, 60000, 32
     a = oracle.uniform((M, K), 91)
     b = oracle.uniform((K, N), 92)
@@ -382,7 +391,8 @@ def test_output_beyond_2pow31_elements(dev, path, forced):
     if forced is None:
         C = mt.gemm(A, to_gpu(b, dev))
     else:
-        with mt.forced_config(mt.FAMILY_DL, forced, 1):
+        family = mt.FAMILY_KSW if path == "ksw" else mt.FAMILY_DL
+        with mt.forced_config(family, forced, 1):
             C = mt.gemm(A, to_gpu(b, dev))
     torch.cuda.synchronize()
     cfg = mt.last_config()

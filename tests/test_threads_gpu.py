@@ -88,7 +88,7 @@ def test_forced_config_is_per_thread(dev):
     torch.cuda.synchronize()
     print(seen)
     assert seen["forced"].startswith("rs 128x128") and seen["forced"].endswith("cfg=1")
-    assert seen["auto"].startswith("dl "), seen["auto"]
+    assert not seen["auto"].startswith("rs "), seen["auto"]
 
 
 def test_explicit_stream_without_context(dev):
