@@ -40,7 +40,9 @@ typedef enum mt_status {
     MT_ERR_INVALID = -1,     /* bad shape / stride / pointer argument        */
     MT_ERR_WORKSPACE = -2,   /* workspace missing or smaller than required   */
     MT_ERR_HIP = -3,         /* a HIP runtime call or kernel launch failed   */
-    MT_ERR_UNSUPPORTED = -4  /* valid request this build does not implement  */
+    MT_ERR_UNSUPPORTED = -4, /* valid request this build does not implement  */
+    MT_ERR_SCRATCH_LIMIT = -5 /* mt_gemm_noalloc_f32: the problem needs more
+                                 scratch than MT_NOALLOC_SCRATCH_BYTES        */
 } mt_status;
 
 /* A (possibly batched) strided fp32 matrix view.
@@ -82,6 +84,25 @@ int mt_gemm_f32(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C,
 
 /* Workspace bytes mt_gemm_f32 needs for these operands (0 if none). */
 size_t mt_gemm_workspace_f32(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C);
+
+/* mt_gemm_f32 without a workspace argument.  No counterpart in the reference;
+ * it is for callers that cannot allocate device memory: code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  Its scratch
+ * (split-K partials) is a static device buffer of MT_NOALLOC_SCRATCH_BYTES
+ * that the library holds on each GPU it runs on until the process ends.
+ *   - Same plan and the same results, bit for bit, as mt_gemm_f32 with a
+ *     workspace of mt_gemm_workspace_f32 bytes.
+ *   - A problem whose mt_gemm_workspace_f32 exceeds MT_NOALLOC_SCRATCH_BYTES
+ *     returns MT_ERR_SCRATCH_LIMIT and launches nothing.
+ *   - Allocates nothing and calls no allocating routine; the first call on
+ *     each GPU looks up that GPU's copy of the buffer (hipGetSymbolAddress).
+ *   - Every call on a GPU uses that GPU's one buffer: calls that may overlap
+ *     on one GPU (other streams, other threads) race, and the caller must
+ *     serialise them.  Nothing in the buffer needs to start at zero: a split-K
+ *     launch writes every partial before it sums them. */
+#define MT_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int mt_gemm_noalloc_f32(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C,
+                        const mt_epilogue_f32* ep, void* stream);
 
 /* out[c] = beta*out[c] + sum_r X[r][c]: the bias gradient of Linear.
  * Replaces the reference's unbroadcast -> sum_gpu(dY, 0, keepdims) path

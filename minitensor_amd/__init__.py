@@ -33,6 +33,8 @@ MT_ERR_INVALID = -1
 MT_ERR_WORKSPACE = -2
 MT_ERR_HIP = -3
 MT_ERR_UNSUPPORTED = -4
+MT_ERR_SCRATCH_LIMIT = -5
+NOALLOC_SCRATCH_BYTES = 32 << 20   # MT_NOALLOC_SCRATCH_BYTES
 
 BIAS_NONE, BIAS_ROW, BIAS_COL = 0, 1, 2
 
@@ -69,6 +71,8 @@ _SIGS = {
     "mt_gemm_f32": (ctypes.c_int, [_P(MatF32), _P(MatF32), _P(MatF32), _P(EpilogueF32),
                                    ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "mt_gemm_workspace_f32": (ctypes.c_size_t, [_P(MatF32), _P(MatF32), _P(MatF32)]),
+    "mt_gemm_noalloc_f32": (ctypes.c_int, [_P(MatF32), _P(MatF32), _P(MatF32), _P(EpilogueF32),
+                                           ctypes.c_void_p]),
     "mt_colsum_f32": (ctypes.c_int, [_P(MatF32), ctypes.c_void_p, ctypes.c_int64, ctypes.c_float,
                                      ctypes.c_void_p]),
     "mt_linear_forward_f32": (ctypes.c_int, [_P(MatF32), _P(MatF32), ctypes.c_void_p,

@@ -16,6 +16,7 @@
 
 #include <atomic>
 #include <cmath>
+#include <mutex>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
@@ -24,6 +25,13 @@
 #include "mtgemm.h"
 
 using namespace mtk;
+
+// Scratch of mt_gemm_noalloc_f32 (split-K partials), one copy per GPU, part of
+// this code object and so loaded with the library: nothing is allocated for
+// it at call time.  Host code must never use this name as a device address
+// (on the host it is only a stand-in): kernels get the address that
+// hipGetSymbolAddress returns for the current device (noalloc_scratch).
+static __device__ __align__(256) unsigned char scratch[MT_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -594,6 +602,26 @@ int run_gemm(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C, int6
     return rc;
 }
 
+// Device address of the current GPU's copy of `scratch`, looked up on the
+// first call on that GPU (with that GPU current) and kept per GPU.
+constexpr int kMaxDevices = 64;
+struct NoallocScratch {
+    std::once_flag once;
+    void* ptr = nullptr;
+    hipError_t err = hipSuccess;
+};
+NoallocScratch g_noalloc[kMaxDevices];
+
+int noalloc_scratch(void** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return MT_ERR_HIP;
+    NoallocScratch& sc = g_noalloc[dev];
+    std::call_once(sc.once, [&sc] { sc.err = hipGetSymbolAddress(&sc.ptr, HIP_SYMBOL(scratch)); });
+    if (sc.err != hipSuccess || sc.ptr == nullptr) return MT_ERR_HIP;
+    *out = sc.ptr;
+    return MT_OK;
+}
+
 size_t gemm_ws(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C) {
     int64_t M, N, K, batch;
     if (check_gemm(A, B, C, &M, &N, &K, &batch) != MT_OK || M == 0 || N == 0 || batch == 0)
@@ -977,6 +1005,24 @@ size_t mt_gemm_workspace_f32(const mt_mat_f32* A, const mt_mat_f32* B, const mt_
     return gemm_ws(A, B, C);
 }
 
+int mt_gemm_noalloc_f32(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C,
+                        const mt_epilogue_f32* ep, void* stream) {
+    int64_t M, N, K, batch;
+    const int rc = check_gemm(A, B, C, &M, &N, &K, &batch);
+    if (rc != MT_OK) return rc;
+    // The workspace mt_gemm_f32 would be given covers the plan it picks, so
+    // with at least that much scratch the plan (and every bit of C) is the same.
+    const size_t need = gemm_ws(A, B, C);
+    if (need > MT_NOALLOC_SCRATCH_BYTES) return MT_ERR_SCRATCH_LIMIT;
+    void* ws = nullptr;
+    if (need > 0) {
+        const int r = noalloc_scratch(&ws);
+        if (r != MT_OK) return r;
+    }
+    return run_gemm(A, B, C, 0, 0, ep, ws, need > 0 ? MT_NOALLOC_SCRATCH_BYTES : 0,
+                    static_cast<hipStream_t>(stream));
+}
+
 int mt_colsum_f32(const mt_mat_f32* X, float* out, int64_t out_stride, float beta, void* stream) {
     if (!valid_mat(X) || X->batch != 1 || out_stride < 0) return MT_ERR_INVALID;
     if (X->cols == 0) return MT_OK;
@@ -1290,6 +1336,9 @@ const char* mt_strerror(int status) {
         case MT_ERR_WORKSPACE: return "workspace missing or too small";
         case MT_ERR_HIP: return "HIP runtime error";
         case MT_ERR_UNSUPPORTED: return "unsupported request";
+        case MT_ERR_SCRATCH_LIMIT:
+            return "problem needs more scratch than mt_gemm_noalloc_f32's static buffer "
+                   "(MT_NOALLOC_SCRATCH_BYTES); use mt_gemm_f32 with a workspace";
         default: return "unknown status";
     }
 }
