@@ -133,13 +133,14 @@ int mt_linear_backward_f32(const mt_mat_f32* dY, const mt_mat_f32* X, const mt_m
  * (include/TensorOps.hpp:17-20).  Weight and output are dense (element
  * offsets applied by the caller).  The GEMM is C[c_out, n*h_out*w_out] =
  * W[c_out, c_in*kh*kw] · col[c_in*kh*kw, n*h_out*w_out] with the row bias fused
- * and the output scattered straight into NCHW.  When c_in*kh*kw % 4 == 0 and
- * the weight is 16-byte aligned, col is never formed: the kernel gathers it
- * from the input (implicit GEMM) and the workspace only holds split-K
- * partials; otherwise an im2col pass fills a column buffer in the workspace
- * first (mt_conv2d_workspace_f32 reports the size of whichever path the
- * geometry takes; a misaligned weight then needs the column buffer too and
- * the call returns MT_ERR_WORKSPACE if it is missing).  Replaces conv2d_gpu +
+ * and the output scattered straight into NCHW.  When c_in % 16 == 0, col is
+ * never formed: the input is copied to channels-last in the workspace (unless
+ * it already is channels-last), the weights to OHWI, and the GEMM kernel
+ * gathers the im2col operand from that copy (implicit GEMM); the workspace
+ * holds the two copies and any split-K partials.  Otherwise an im2col pass
+ * fills a column buffer in the workspace first.  mt_conv2d_workspace_f32
+ * reports the size of whichever path the geometry takes; a workspace that is
+ * missing or too small returns MT_ERR_WORKSPACE.  Replaces conv2d_gpu +
  * im2col_kernel + batched_sgemm_kernel_v2 (reference src/gpu_ops.cpp:2237-2325,
  * 1748-1825, 683-859; declared include/TensorOps.hpp:708). */
 typedef struct mt_conv2d_desc {

@@ -73,17 +73,37 @@ void matmul_into(const Tensor<T>& a, const Tensor<T>& b, Tensor<T>& out) {
     else matmul_cpu_strided(a, b, out);
 }
 
-// out = conv2d(input, weight) for stride 1; the padding is the one that gives
-// out's spatial size ((H_out - H + kh - 1) / 2 on each side).
+// out = conv2d(input, weight) into out's shape.  The registry's binary
+// signature carries no stride or padding (include/Dispatch.hpp:21-22), so they
+// are inferred from the shapes: stride 1 with the padding that gives out's
+// size, else the "same" padding (kh-1)/2 of ResNet-style layers with the
+// smallest stride that gives it.  Any other shape throws std::invalid_argument.
 template <typename T>
 void conv2d_into(const Tensor<T>& input, const Tensor<T>& weight, Tensor<T>& out) {
     if (input.shape().size() != 4 || weight.shape().size() != 4 || out.shape().size() != 4)
         throw std::invalid_argument("conv2d expects NCHW input and OIHW weight.");
-    const long H = (long)input.shape()[2], kh = (long)weight.shape()[2], Ho = (long)out.shape()[2];
-    const long twice = Ho - H + kh - 1;
-    if (twice < 0 || twice % 2) throw std::invalid_argument("conv2d: output size needs stride != 1");
-    const size_t pad = (size_t)(twice / 2);
-    Tensor<T> r = conv2d(input, weight, Tensor<T>(), 1, pad);
+    const size_t H = input.shape()[2], W = input.shape()[3];
+    const size_t kh = weight.shape()[2], kw = weight.shape()[3];
+    const size_t Ho = out.shape()[2], Wo = out.shape()[3];
+    auto fits = [&](size_t s, size_t p) {
+        return safe_out_size(H, p, kh, s) == Ho && safe_out_size(W, p, kw, s) == Wo;
+    };
+    size_t stride = 0, pad = 0;
+    const long twice = (long)Ho - (long)H + (long)kh - 1;
+    if (twice >= 0 && twice % 2 == 0 && fits(1, (size_t)twice / 2)) {
+        stride = 1;
+        pad = (size_t)twice / 2;
+    } else {
+        pad = (kh - 1) / 2;
+        for (size_t s = 2; s <= std::max(H, W) + 2 * pad; ++s)
+            if (fits(s, pad)) {
+                stride = s;
+                break;
+            }
+    }
+    if (stride == 0)
+        throw std::invalid_argument("conv2d: no stride and padding give the output shape");
+    Tensor<T> r = conv2d(input, weight, Tensor<T>(), stride, pad);
     if (r.shape() != out.shape()) throw std::invalid_argument("conv2d: output shape mismatch");
     copy_strided(r, out);
 }

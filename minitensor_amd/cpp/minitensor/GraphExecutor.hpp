@@ -65,13 +65,14 @@ public:
         if (state_ == State::NeedsCapture) {
             load(x, y);
             GPU_CHECK(hipStreamSynchronize(stream_));
-            capture();
+            capture();   // on an exception: state_ is NeedsWarmup again
             state_ = State::GraphReady;
         }
         return replay(x, y);
     }
 
     bool captured() const { return state_ == State::GraphReady; }
+    hipStream_t stream() const { return stream_; }
     size_t capture_allocations() const { return reservation_.fresh_allocations(); }
 
 private:
@@ -83,12 +84,24 @@ private:
         copy_gpu_strided(y, y_);
     }
 
+    // If the step throws while it is being captured, the capture is ended and
+    // its partial graph destroyed, the reservation stops pinning this
+    // thread's allocations, and the executor starts over with an eager
+    // warm-up step on the next call; the exception propagates.
     void capture() {
-        reservation_.start();
         GPU_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeRelaxed));
-        {
+        reservation_.start();
+        try {
             ActiveStreamGuard g(stream_);
             out_ = step_(x_, y_);
+        } catch (...) {
+            hipGraph_t partial = nullptr;
+            (void)hipStreamEndCapture(stream_, &partial);
+            if (partial) (void)hipGraphDestroy(partial);
+            (void)hipGetLastError();
+            reservation_.stop();
+            state_ = State::NeedsWarmup;
+            throw;
         }
         const hipError_t e = hipStreamEndCapture(stream_, &graph_);
         reservation_.stop();

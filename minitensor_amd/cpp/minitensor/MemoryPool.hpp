@@ -44,6 +44,8 @@ public:
             if (active() == this) active() = nullptr;
         }
         size_t blocks() const { return blocks_.size(); }
+        // Whether a Reservation is pinning this thread's allocations now.
+        static bool active_on_this_thread() { return active() != nullptr; }
         size_t fresh_allocations() const { return fresh_; }  // blocks that needed a new malloc
 
     private:

@@ -13,9 +13,15 @@
 // handed to the kernels by descriptor, never copied, and the offset is always
 // applied (the reference's contiguous GPU path drops it).
 // GPU launchers keep the reference's names and signatures
-// (include/TensorOps.hpp:697-728): matmul_gpu, matmul_gpu_strided,
-// matmul_gpu_v2, matmul_gpu_bk16, conv2d_gpu, conv2d_backward_{input,weight,bias}_gpu,
-// fill_gpu, copy_gpu_strided.
+// (include/TensorOps.hpp:697-728) for the GEMM path and what it needs:
+// matmul_gpu, matmul_gpu_strided, matmul_gpu_v2, matmul_gpu_bk16 (A, B, C&);
+// sum_gpu(input, axis, keepdims) -> Tensor; conv2d_gpu, conv2d_gpu_strided,
+// conv2d_backward_{input,weight,bias}_gpu; fill_gpu(T*, T, size_t);
+// copy_gpu_strided(const Tensor<T> src, T* dst).  (Additions: a beta argument
+// defaulting to 0 on the backward weight/bias launchers, for gradient
+// accumulation, and a Tensor-to-Tensor copy_gpu_strided overload.)  The
+// reference's other launchers (elementwise, pooling, losses, optimizers,
+// batch norm) are outside this backend.
 #pragma once
 
 #include <cmath>
@@ -93,17 +99,18 @@ inline std::vector<Dim> collapse(const std::vector<size_t>& shape, const std::ve
 }
 
 // Y = alpha·X + beta·Y over same-shape GPU views (X may broadcast), in slabs
-// of at most three dims per mt_axpby_f32 launch.
-inline void axpby(const Tensor<float>& X, float alpha, Tensor<float>& Y, float beta) {
-    if (X.shape() != Y.shape()) throw std::invalid_argument("axpby: shape mismatch");
-    auto dims = collapse(Y.shape(), X.strides(), Y.strides());
+// of at most three dims per mt_axpby_f32 launch.  Y is given as raw device
+// memory: element i of Y is ybase[yoff + Σ idx·ystrides].
+inline void axpby_raw(const Tensor<float>& X, float alpha, float* ybase, size_t yoff,
+                      const std::vector<size_t>& ystrides, float beta) {
+    auto dims = collapse(X.shape(), X.strides(), ystrides);
     if (dims.empty()) dims.push_back({1, 0, 0});
     while (dims.size() < 3) dims.insert(dims.begin(), Dim{1, 0, 0});
     const size_t outer = dims.size() - 3;
     size_t n_outer = 1;
     for (size_t i = 0; i < outer; ++i) n_outer *= dims[i].n;
     for (size_t o = 0; o < n_outer; ++o) {
-        size_t xo = X.offset(), yo = Y.offset(), rem = o;
+        size_t xo = X.offset(), yo = yoff, rem = o;
         for (size_t i = outer; i-- > 0;) {
             const size_t c = rem % dims[i].n;
             rem /= dims[i].n;
@@ -115,11 +122,16 @@ inline void axpby(const Tensor<float>& X, float alpha, Tensor<float>& Y, float b
         const Dim& c = dims[outer + 2];
         mt_mat_f32 mx{X.data(), (int64_t)xo, (int64_t)r.n, (int64_t)c.n, (int64_t)r.xs,
                       (int64_t)c.xs, (int64_t)b.n, (int64_t)b.xs};
-        mt_mat_f32 my{Y.data(), (int64_t)yo, (int64_t)r.n, (int64_t)c.n, (int64_t)r.ys,
+        mt_mat_f32 my{ybase, (int64_t)yo, (int64_t)r.n, (int64_t)c.n, (int64_t)r.ys,
                       (int64_t)c.ys, (int64_t)b.n, (int64_t)b.ys};
         if (b.n > 1 && b.xs == 0) mx.batch = 1;  // broadcast over the batch dim
         mt_check_status(mt_axpby_f32(&mx, alpha, &my, beta, active_stream()), "axpby");
     }
+}
+
+inline void axpby(const Tensor<float>& X, float alpha, Tensor<float>& Y, float beta) {
+    if (X.shape() != Y.shape()) throw std::invalid_argument("axpby: shape mismatch");
+    axpby_raw(X, alpha, Y.data(), Y.offset(), Y.strides(), beta);
 }
 
 template <typename T>
@@ -244,33 +256,41 @@ void conv2d_backward_weight_cpu(const Tensor<T>& go, const Tensor<T>& in, Tensor
     const size_t N = in.shape()[0], Ci = in.shape()[1], H = in.shape()[2], W = in.shape()[3];
     const size_t Co = gw.shape()[0], kh = gw.shape()[2], kw = gw.shape()[3];
     const size_t Ho = go.shape()[2], Wo = go.shape()[3];
+    // per image: a partial sum over the output positions, added to the
+    // gradient image by image -- the reference's order (include/TensorOps.hpp:356-394)
     for (size_t co = 0; co < Co; ++co)
         for (size_t ci = 0; ci < Ci; ++ci)
             for (size_t r = 0; r < kh; ++r)
-                for (size_t s = 0; s < kw; ++s) {
-                    T v = 0;
-                    for (size_t n = 0; n < N; ++n)
+                for (size_t s = 0; s < kw; ++s) gw.data()[at4(gw, co, ci, r, s)] = T(0);
+    for (size_t n = 0; n < N; ++n)
+        for (size_t co = 0; co < Co; ++co)
+            for (size_t ci = 0; ci < Ci; ++ci)
+                for (size_t r = 0; r < kh; ++r)
+                    for (size_t s = 0; s < kw; ++s) {
+                        T v = 0;
                         for (size_t oy = 0; oy < Ho; ++oy)
                             for (size_t ox = 0; ox < Wo; ++ox) {
                                 const long iy = (long)(oy * stride + r) - (long)pad;
                                 const long ix = (long)(ox * stride + s) - (long)pad;
                                 if (iy < 0 || iy >= (long)H || ix < 0 || ix >= (long)W) continue;
-                                v += go.data()[at4(go, n, co, oy, ox)] * in.data()[at4(in, n, ci, iy, ix)];
+                                v += in.data()[at4(in, n, ci, iy, ix)] * go.data()[at4(go, n, co, oy, ox)];
                             }
-                    gw.data()[at4(gw, co, ci, r, s)] = v;
-                }
+                        gw.data()[at4(gw, co, ci, r, s)] += v;
+                    }
 }
 
 template <typename T>
 void conv2d_backward_bias_cpu(const Tensor<T>& go, Tensor<T>& gb) {
     const size_t N = go.shape()[0], Co = go.shape()[1], Ho = go.shape()[2], Wo = go.shape()[3];
-    for (size_t co = 0; co < Co; ++co) {
-        T v = 0;
-        for (size_t n = 0; n < N; ++n)
+    // per image, then added: the reference's order (include/TensorOps.hpp:396-415)
+    for (size_t co = 0; co < Co; ++co) gb.data()[gb.offset() + co * gb.strides()[0]] = T(0);
+    for (size_t n = 0; n < N; ++n)
+        for (size_t co = 0; co < Co; ++co) {
+            T v = 0;
             for (size_t y = 0; y < Ho; ++y)
                 for (size_t x = 0; x < Wo; ++x) v += go.data()[at4(go, n, co, y, x)];
-        gb.data()[gb.offset() + co * gb.strides()[0]] = v;
-    }
+            gb.data()[gb.offset() + co * gb.strides()[0]] += v;
+        }
 }
 
 // ======================================================================
@@ -305,6 +325,16 @@ void fill_gpu(T* data, T val, size_t n) {
     mt_check_status(mt_fill_f32(data, (int64_t)n, val, active_stream()), "fill_gpu");
 }
 
+// The reference's launcher (include/TensorOps.hpp:717): src (any strides)
+// into dense row-major memory at dst.
+template <typename T>
+void copy_gpu_strided(const Tensor<T> src, T* dst) {
+    mt_detail::require_float_gpu<T>();
+    if (src.total_elements() == 0) return;
+    mt_detail::axpby_raw(src, 1.f, dst, 0, contiguous_strides(src.shape()), 0.f);
+}
+
+// src into dst, both any strides (dst's shape = src's).
 template <typename T>
 void copy_gpu_strided(const Tensor<T>& src, Tensor<T>& dst) {
     mt_detail::require_float_gpu<T>();
@@ -526,55 +556,79 @@ Tensor<T> operator+(const Tensor<T>& A, const Tensor<T>& B) {
     return C;
 }
 
-// Sum over one axis (no autograd node: used by unbroadcast under NoGradGuard).
+// Sum over one axis on the GPU: the reference's launcher
+// (include/TensorOps.hpp:707, src/gpu_ops.cpp:1306-1348), with the same
+// output shape (keepdims: the axis kept with extent 1).  The view is read in
+// place through its strides: one mt_colsum_f32 launch per slab of the
+// remaining dims that does not collapse into a single strided run.
 template <typename T>
-Tensor<T> sum(const Tensor<T>& A, size_t axis, bool keepdims) {
+Tensor<T> sum_gpu(const Tensor<T>& A, size_t axis, bool keepdims) {
+    mt_detail::require_float_gpu<T>();
     if (axis >= A.shape().size()) throw std::out_of_range("sum: axis out of range");
     std::vector<size_t> out_shape = A.shape();
     if (keepdims) out_shape[axis] = 1;
     else out_shape.erase(out_shape.begin() + axis);
     Tensor<T> out(out_shape, A.device());
-    // remaining dims of A in order, as (extent, stride)
-    std::vector<size_t> rshape, rstr;
+    std::vector<size_t> rshape, rstr;   // remaining dims of A in order: (extent, stride)
     for (size_t i = 0; i < A.shape().size(); ++i)
         if (i != axis) { rshape.push_back(A.shape()[i]); rstr.push_back(A.strides()[i]); }
     const size_t R = A.shape()[axis], rs = A.strides()[axis];
     const size_t n_out = numel_of(rshape);
     if (n_out == 0) return out;
-    if (A.device().is_gpu()) {
-        mt_detail::require_float_gpu<T>();
-        auto dims = mt_detail::collapse(rshape, rstr, contiguous_strides(rshape));
-        if (dims.empty()) dims.push_back({1, 0, 0});
-        const mt_detail::Dim inner = dims.back();
-        const size_t n_outer = n_out / inner.n;
-        for (size_t o = 0; o < n_outer; ++o) {
-            size_t xo = A.offset(), yo = 0, rem = o;
-            for (size_t i = dims.size() - 1; i-- > 0;) {
-                const size_t c = rem % dims[i].n;
-                rem /= dims[i].n;
-                xo += c * dims[i].xs;
-                yo += c * dims[i].ys;
-            }
-            mt_mat_f32 x{A.data(), (int64_t)xo, (int64_t)R, (int64_t)inner.n, (int64_t)rs,
-                         (int64_t)inner.xs, 1, 0};
-            mt_check_status(mt_colsum_f32(&x, out.data() + yo, (int64_t)inner.ys, 0.f, active_stream()),
-                            "sum");
+    auto dims = mt_detail::collapse(rshape, rstr, contiguous_strides(rshape));
+    if (dims.empty()) dims.push_back({1, 0, 0});
+    const mt_detail::Dim inner = dims.back();
+    const size_t n_outer = n_out / inner.n;
+    for (size_t o = 0; o < n_outer; ++o) {
+        size_t xo = A.offset(), yo = 0, rem = o;
+        for (size_t i = dims.size() - 1; i-- > 0;) {
+            const size_t c = rem % dims[i].n;
+            rem /= dims[i].n;
+            xo += c * dims[i].xs;
+            yo += c * dims[i].ys;
         }
-    } else {
-        std::vector<size_t> idx(rshape.size(), 0);
-        for (size_t e = 0; e < n_out; ++e) {
-            size_t base = A.offset();
-            for (size_t i = 0; i < rshape.size(); ++i) base += idx[i] * rstr[i];
-            T s = 0;
-            for (size_t j = 0; j < R; ++j) s += A.data()[base + j * rs];
-            out.data()[e] = s;
-            for (size_t i = rshape.size(); i-- > 0;) {
-                if (++idx[i] < rshape[i]) break;
-                idx[i] = 0;
-            }
+        mt_mat_f32 x{A.data(), (int64_t)xo, (int64_t)R, (int64_t)inner.n, (int64_t)rs,
+                     (int64_t)inner.xs, 1, 0};
+        mt_check_status(mt_colsum_f32(&x, out.data() + yo, (int64_t)inner.ys, 0.f, active_stream()),
+                        "sum");
+    }
+    return out;
+}
+
+// Sum over one axis of a CPU tensor, sequential over the reduced axis (the
+// reference's sum_cpu order, include/TensorOps.hpp:190-233).
+template <typename T>
+Tensor<T> sum_cpu(const Tensor<T>& A, size_t axis, bool keepdims) {
+    if (axis >= A.shape().size()) throw std::out_of_range("sum: axis out of range");
+    std::vector<size_t> out_shape = A.shape();
+    if (keepdims) out_shape[axis] = 1;
+    else out_shape.erase(out_shape.begin() + axis);
+    Tensor<T> out(out_shape, A.device());
+    std::vector<size_t> rshape, rstr;
+    for (size_t i = 0; i < A.shape().size(); ++i)
+        if (i != axis) { rshape.push_back(A.shape()[i]); rstr.push_back(A.strides()[i]); }
+    const size_t R = A.shape()[axis], rs = A.strides()[axis];
+    const size_t n_out = numel_of(rshape);
+    std::vector<size_t> idx(rshape.size(), 0);
+    for (size_t e = 0; e < n_out; ++e) {
+        size_t base = A.offset();
+        for (size_t i = 0; i < rshape.size(); ++i) base += idx[i] * rstr[i];
+        T s = 0;
+        for (size_t j = 0; j < R; ++j) s += A.data()[base + j * rs];
+        out.data()[e] = s;
+        for (size_t i = rshape.size(); i-- > 0;) {
+            if (++idx[i] < rshape[i]) break;
+            idx[i] = 0;
         }
     }
     return out;
+}
+
+// Sum over one axis (no autograd node: used by unbroadcast under NoGradGuard),
+// routed by device as the reference's sum (include/TensorOps.hpp:1047-1070).
+template <typename T>
+Tensor<T> sum(const Tensor<T>& A, size_t axis, bool keepdims) {
+    return A.device().is_gpu() ? sum_gpu(A, axis, keepdims) : sum_cpu(A, axis, keepdims);
 }
 
 template <typename T>

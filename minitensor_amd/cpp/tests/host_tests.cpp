@@ -1,17 +1,26 @@
 // host_tests.cpp -- tests of the C++ host layer (Tensor / matmul / bmm / conv2d /
 // F::linear / Linear / Conv2D / Dispatch) on the CPU device and on the GPU.
 //
-//   mt_host_tests --cpu    CPU-device tests (no GPU needed)
-//   mt_host_tests --gpu    GPU tests: known answers and CPU-vs-GPU equivalence
+//   mt_host_tests --cpu [--golden FILE]   CPU-device tests (no GPU needed)
+//   mt_host_tests --gpu [--golden FILE]   GPU tests: known answers and CPU-vs-GPU equivalence
+//
+// FILE is tests/golden/reference_vectors.bin: inputs and outputs of the
+// reference's own CPU code (tests/golden/make_golden.py).  The CPU device is
+// checked against it bit for bit, so the GPU comparisons against the CPU
+// device are anchored to the reference.
 //
 // Known answers are the reference's own tests: test/tensor_test.cpp:258-510,
 // test/engien_test.cpp:80-96, test/spatial_test.cpp:155-230, test/view_test.cpp.
 // Equivalence uses the GEMM parity bound 1e-5·√K·max|A|·max|B|.
 #include <cmath>
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <fstream>
 #include <functional>
+#include <map>
 #include <random>
+#include <stdexcept>
 #include <string>
 #include <vector>
 
@@ -94,6 +103,49 @@ void check_close(const Tensor<float>& got, const Tensor<float>& want, size_t K, 
     const double e = max_err(got, want);
     if (!(e <= bound)) std::printf("  %s: max|err| %.3e > bound %.3e\n", g_cur, e, bound);
     CHECK(e <= bound);
+}
+
+// ---- golden vectors (tests/golden/reference_vectors.bin) ---------------------
+std::string g_golden_path;
+
+std::map<std::string, Tensor<float>>& golden_arrays() {
+    static std::map<std::string, Tensor<float>> arrays;
+    static bool loaded = false;
+    if (loaded) return arrays;
+    loaded = true;
+    if (g_golden_path.empty()) throw std::runtime_error("no --golden file given");
+    std::ifstream f(g_golden_path, std::ios::binary);
+    if (!f) throw std::runtime_error("cannot open " + g_golden_path);
+    char magic[8];
+    f.read(magic, 8);
+    if (!f || std::memcmp(magic, "MTGOLD01", 8) != 0) throw std::runtime_error("bad golden file");
+    uint32_t count = 0;
+    f.read(reinterpret_cast<char*>(&count), 4);
+    for (uint32_t i = 0; i < count && f; ++i) {
+        uint32_t len = 0, nd = 0;
+        f.read(reinterpret_cast<char*>(&len), 4);
+        std::string name(len, '\0');
+        f.read(name.data(), len);
+        f.read(reinterpret_cast<char*>(&nd), 4);
+        std::vector<size_t> shape(nd);
+        for (auto& d : shape) {
+            uint64_t v = 0;
+            f.read(reinterpret_cast<char*>(&v), 8);
+            d = (size_t)v;
+        }
+        Tensor<float> t(shape);
+        f.read(reinterpret_cast<char*>(t.data()), (std::streamsize)(t.total_elements() * 4));
+        arrays[name] = t;
+    }
+    if (!f) throw std::runtime_error("truncated golden file");
+    return arrays;
+}
+
+Tensor<float> gold(const std::string& name) {
+    auto& a = golden_arrays();
+    auto it = a.find(name);
+    if (it == a.end()) throw std::runtime_error("golden array missing: " + name);
+    return it->second;
 }
 
 Tensor<float> mat23() {
@@ -299,6 +351,76 @@ TEST_CPU(cpu_dispatch_registry) {
     w.fill(1);
     dispatch_binary_op(OpType::Conv2D, x, w, y);
     CHECK_EQ_F(y.data()[0], 12); CHECK_EQ_F(y.data()[3], 28);
+}
+
+
+// ---- the CPU device against the reference's own outputs -----------------------
+// tests/golden/make_golden.py ran the reference's CPU code (built from its
+// headers) on these inputs; the CPU device computes in the same order, so
+// every result must match bit for bit.
+TEST_CPU(cpu_golden_matmul_and_views) {
+    CHECK(max_err(matmul(gold("dense_a"), gold("dense_b")), gold("dense_c")) == 0);
+    // A: rows 2..4 of a [5,5] storage (offset 10); B: [5,4] at offset 3
+    Tensor<float> A = gold("offset_a_store").as_strided({3, 5}, {5, 1}, 10);
+    Tensor<float> B = gold("offset_b_store").as_strided({5, 4}, {4, 1}, 3);
+    CHECK(max_err(matmul(A, B), gold("offset_c")) == 0);
+    CHECK(max_err(matmul(gold("bT_a"), gold("bT_bt").transpose(0, 1)), gold("bT_c")) == 0);
+    Tensor<float> row = gold("expand_row").reshape({1, 40}).expand({17, 40});
+    CHECK(max_err(matmul(row, gold("expand_b")), gold("expand_c")) == 0);
+}
+
+TEST_CPU(cpu_golden_conv_forward) {
+    CHECK(max_err(conv2d(gold("conv_x"), gold("conv_w"), gold("conv_b"), 2, 1),
+                  gold("conv_out")) == 0);
+}
+
+TEST_CPU(cpu_golden_linear_forward_backward) {
+    // the reference's Linear: Y = matmul(X, W_ref) + b with W_ref [in,out], b [1,out]
+    Tensor<float> x = gold("lin_x"), w = gold("lin_w_ref");
+    Tensor<float> b = gold("lin_b").reshape({1, w.shape()[1]});
+    for (auto* t : {&x, &w, &b}) t->set_requires_grad(true);
+    Tensor<float> y = matmul(x, w) + b;
+    CHECK(max_err(y, gold("lin_y")) == 0);
+    y.grad() = gold("lin_dy");
+    y.backward();
+    CHECK(max_err(x.grad(), gold("lin_dx")) == 0);
+    CHECK(max_err(w.grad(), gold("lin_dw_ref")) == 0);
+    CHECK(max_err(b.grad().reshape({b.shape()[1]}), gold("lin_db")) == 0);
+}
+
+TEST_CPU(cpu_golden_conv_backward) {
+    // three images: dW and db summed per image, then added, as the reference does
+    for (const char* tag : {"s1", "s2"}) {
+        const std::string k = std::string("cbwd_") + tag + "_";
+        Tensor<float> geom = gold(k + "geom");
+        const size_t st = (size_t)geom.data()[0], pad = (size_t)geom.data()[1];
+        Tensor<float> x = gold(k + "x"), w = gold(k + "w");
+        Tensor<float> b({w.shape()[0]});
+        b.fill(0.f);
+        for (auto* t : {&x, &w, &b}) t->set_requires_grad(true);
+        Tensor<float> y = conv2d(x, w, b, st, pad);
+        y.grad() = gold(k + "dy");
+        y.backward();
+        CHECK(max_err(x.grad(), gold(k + "dx")) == 0);
+        CHECK(max_err(w.grad(), gold(k + "dw")) == 0);
+        CHECK(max_err(b.grad(), gold(k + "db")) == 0);
+    }
+}
+
+TEST_CPU(cpu_dispatch_conv2d_infers_stride) {
+    // OpType::Conv2D gets (input, weight, out) only: stride 1 with the padding
+    // that gives out's size, else the "same" padding (kh-1)/2 with the stride
+    // that does; both against conv2d
+    Tensor<float> x = uniform({2, 3, 11, 10}, 71), w = uniform({4, 3, 3, 3}, 72);
+    for (size_t stride : {1u, 2u, 3u}) {
+        const size_t pad = 1;
+        Tensor<float> want = conv2d(x, w, Tensor<float>(), stride, pad);
+        Tensor<float> out(want.shape());
+        dispatch_binary_op(OpType::Conv2D, x, w, out);
+        CHECK(max_err(out, want) == 0);
+    }
+    Tensor<float> bad({2, 4, 50, 50});
+    CHECK_THROWS(dispatch_binary_op(OpType::Conv2D, x, w, bad), std::invalid_argument);
 }
 
 // =====================================================================
@@ -581,13 +703,125 @@ TEST_GPU(gpu_contiguous_and_dispatch) {
     CHECK_THROWS(matmul(mat23().to(GPU), mat32()), std::invalid_argument);
 }
 
+
+// The reference's modules and launchers by name on the GPU device, each
+// against the CPU device (itself pinned to the reference by the golden tests).
+// Conv2D<float> is the reference's main GPU consumer (test/resnet.cpp,
+// test/mnist.cpp): a ResNet-like 3x3 (implicit GEMM), a strided 3x3 and a
+// c_in = 3 stem layer (explicit im2col), forward and backward.
+TEST_GPU(gpu_conv2d_module_forward_backward) {
+    struct Layer { size_t n, c, h, w, co, k, st, pad; };
+    for (const Layer& L : {Layer{4, 64, 14, 14, 64, 3, 1, 1}, Layer{2, 32, 15, 15, 64, 3, 2, 1},
+                           Layer{2, 3, 32, 32, 16, 7, 2, 3}}) {
+        Conv2D<float> m(L.c, L.co, L.k, L.st, L.pad);        // CPU parameters
+        m.bias_.fill(0.05f);
+        Conv2D<float> mg = m;                                // the same values on the GPU
+        mg.to(GPU);
+        mg.weight_.set_requires_grad(true);
+        mg.bias_.set_requires_grad(true);
+        Tensor<float> x = uniform({L.n, L.c, L.h, L.w}, 80 + (unsigned)L.c);
+        Tensor<float> xg = x.to(GPU);
+        x.set_requires_grad(true);
+        xg.set_requires_grad(true);
+        Tensor<float> y = m.forward(x), yg = mg.forward(xg);
+        CHECK(yg.device().is_gpu());
+        const size_t kg = L.c * L.k * L.k;
+        check_close(yg, y, kg, 1, amax(m.weight_), 1e-6);
+        Tensor<float> dy = uniform(y.shape(), 90 + (unsigned)L.c);
+        y.grad() = dy;
+        yg.grad() = dy.to(GPU);
+        y.backward();
+        yg.backward();
+        const size_t np = L.n * y.shape()[2] * y.shape()[3];
+        check_close(xg.grad(), x.grad(), L.co * L.k * L.k, 1, amax(m.weight_));
+        check_close(mg.weight_.grad(), m.weight_.grad(), np, 1, 1);
+        check_close(mg.bias_.grad(), m.bias_.grad(), np, 1, 1);
+    }
+}
+
+TEST_GPU(gpu_F_conv2d_golden) {
+    Tensor<float> y = F::conv2d(gold("conv_x").to(GPU), gold("conv_w").to(GPU),
+                                gold("conv_b").to(GPU), 2, 1);
+    CHECK(y.device().is_gpu());
+    check_close(y, gold("conv_out"), 27, amax(gold("conv_x")), amax(gold("conv_w")), 1e-6);
+}
+
+TEST_GPU(gpu_matmul_launchers_by_name) {
+    // the reference's benchmark calls these by name (test/benchmark.cpp:225-251)
+    const Tensor<float> a = gold("dense_a").to(GPU), b = gold("dense_b").to(GPU);
+    const Tensor<float> want = gold("dense_c");
+    const float am = amax(gold("dense_a")), bm = amax(gold("dense_b"));
+    Tensor<float> c1({64, 80}, GPU), c2({64, 80}, GPU), c3({64, 80}, GPU), c4({33, 29}, GPU);
+    matmul_gpu<float>(a, b, c1);
+    matmul_gpu_v2<float>(a, b, c2);
+    matmul_gpu_bk16<float>(a, b, c3);
+    matmul_gpu_strided<float>(gold("bT_a").to(GPU), gold("bT_bt").to(GPU).transpose(0, 1), c4);
+    for (Tensor<float>* c : {&c1, &c2, &c3}) check_close(*c, want, 96, am, bm);
+    check_close(c4, gold("bT_c"), 47, 1, 1);
+}
+
+TEST_GPU(gpu_dispatch_conv2d) {
+    // OpType::Conv2D on the GPU: stride 1 and the inferred strides 2 and 3
+    Tensor<float> x = uniform({2, 16, 13, 12}, 73), w = uniform({8, 16, 3, 3}, 74);
+    for (size_t stride : {1u, 2u, 3u}) {
+        Tensor<float> want = conv2d(x, w, Tensor<float>(), stride, 1);
+        Tensor<float> out(want.shape(), GPU);
+        dispatch_binary_op(OpType::Conv2D, x.to(GPU), w.to(GPU), out);
+        check_close(out, want, 144, 1, 1);
+    }
+}
+
+TEST_GPU(gpu_sum_and_copy_launchers_by_name) {
+    // sum_gpu(input, axis, keepdims) and copy_gpu_strided(src, T* dst) with the
+    // reference's signatures (include/TensorOps.hpp:707, 717)
+    Tensor<float> a = uniform({5, 7, 9}, 75);
+    Tensor<float> ag = a.to(GPU).transpose(0, 2);            // a strided view [9,7,5]
+    Tensor<float> ac = a.transpose(0, 2);
+    for (size_t axis = 0; axis < 3; ++axis)
+        for (bool keep : {false, true}) {
+            Tensor<float> got = sum_gpu(ag, axis, keep);
+            Tensor<float> want = sum_cpu(ac, axis, keep);
+            CHECK(got.shape() == want.shape());
+            check_close(got, want, ac.shape()[axis], 1, 1);
+        }
+    Tensor<float> dense({9, 7, 5}, GPU);
+    copy_gpu_strided<float>(ag, dense.data());
+    CHECK(max_err(dense, ac.contiguous()) == 0);
+}
+
+TEST_GPU(gpu_graph_executor_step_throws_during_capture) {
+    // a step that fails while it is being captured: the exception propagates,
+    // the stream leaves capture mode, this thread's allocations are no longer
+    // pinned, and the next step runs eagerly and correctly
+    int calls = 0;
+    Tensor<float> w = uniform({16, 8}, 76).to(GPU);
+    GraphExecutor<float> ex([&](const Tensor<float>& x, const Tensor<float>&) {
+        if (++calls == 2) throw std::runtime_error("step failed");
+        return matmul(x, w);
+    });
+    Tensor<float> x = uniform({4, 16}, 77).to(GPU), y = uniform({4, 8}, 78).to(GPU);
+    ex.step(x, y);                                           // eager warm-up
+    CHECK_THROWS(ex.step(x, y), std::runtime_error);         // the capture throws
+    hipStreamCaptureStatus st = hipStreamCaptureStatusActive;
+    GPU_CHECK(hipStreamIsCapturing(ex.stream(), &st));
+    CHECK(st == hipStreamCaptureStatusNone);
+    CHECK(!MemoryPool::Reservation::active_on_this_thread());
+    CHECK(!ex.captured());
+    Tensor<float> out = ex.step(x, y);                       // eager again
+    GPU_CHECK(hipDeviceSynchronize());
+    check_close(out, matmul(host(x), host(w)), 16, 1, 1);
+    ex.step(x, y);                                           // captures now
+    CHECK(ex.captured());
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
     const bool want_gpu = argc > 1 && std::strcmp(argv[1], "--gpu") == 0;
     const bool want_cpu = argc > 1 && std::strcmp(argv[1], "--cpu") == 0;
+    if (argc > 3 && std::strcmp(argv[2], "--golden") == 0) g_golden_path = argv[3];
     if (!want_gpu && !want_cpu) {
-        std::printf("usage: %s --cpu | --gpu\n", argv[0]);
+        std::printf("usage: %s --cpu | --gpu [--golden FILE]\n", argv[0]);
         return 2;
     }
     int ran = 0;

@@ -1,10 +1,12 @@
 """Write tests/golden/reference_vectors.npz from the reference's own CPU code.
 
 Runs oracle/_ref/libref.so (miniTensor's matmul / conv2d / Linear CPU path
-compiled from its headers by oracle/Makefile) on small seeded inputs and
-stores inputs and outputs as plain arrays (np.savez, no pickles), so the
-oracle and the GPU path can be checked against the reference where the
-reference tree is not available.
+and conv2d's autograd backward, compiled from its headers by oracle/Makefile)
+on small seeded inputs and stores inputs and outputs as plain arrays
+(np.savez, no pickles), plus the same arrays as a raw binary for the C++
+host-layer tests, so the oracle, the host layer's CPU device and the GPU path
+can be checked against the reference where the reference tree is not
+available.
 
     python tests/golden/make_golden.py
 """
@@ -20,6 +22,23 @@ sys.path.insert(0, str(ROOT))
 import oracle  # noqa: E402
 
 OUT = Path(__file__).resolve().parent / "reference_vectors.npz"
+
+
+def write_bin(arrays: dict, path: Path) -> None:
+    """The same arrays in a raw form a C++ test reads without numpy:
+    b"MTGOLD01", count (u32), then per array: name length (u32), name,
+    ndim (u32), dims (u64 each), the float32 data (little-endian)."""
+    with open(path, "wb") as f:
+        f.write(b"MTGOLD01")
+        f.write(np.uint32(len(arrays)).tobytes())
+        for name in sorted(arrays):
+            a = np.ascontiguousarray(arrays[name], dtype=np.float32)
+            nb = name.encode()
+            f.write(np.uint32(len(nb)).tobytes() + nb)
+            f.write(np.uint32(a.ndim).tobytes())
+            f.write(np.asarray(a.shape, dtype=np.uint64).tobytes())
+            f.write(a.astype("<f4").tobytes())
+    print(f"wrote {path} ({path.stat().st_size} bytes)")
 
 
 def main() -> None:
@@ -79,7 +98,26 @@ def main() -> None:
     v.update(lin_x=x, lin_w_ref=w_ref, lin_b=bias, lin_dy=dy, lin_y=y, lin_dx=dx, lin_dw_ref=dw,
              lin_db=db)
 
+    # 7. conv2d backward through the reference's autograd (Conv2DBackward ->
+    #    conv2d_backward_{input,weight,bias}_cpu): three images, so the
+    #    per-image accumulation order of dW and db shows; stride 1 and 2.
+    for tag, (n, c, h, wd, co, k, st, pad) in (("s1", (3, 4, 7, 6, 5, 3, 1, 1)),
+                                                 ("s2", (3, 2, 9, 8, 3, 3, 2, 1))):
+        x = oracle.normal((n, c, h, wd), 57 + st)
+        w = oracle.normal((co, c, k, k), 59 + st, std=(2 / (c * k * k)) ** 0.5)
+        ho, wo = oracle.conv_out(h, pad, k, st), oracle.conv_out(wd, pad, k, st)
+        dy = oracle.normal((n, co, ho, wo), 61 + st, std=0.1)
+        dx = np.empty_like(x)
+        dw = np.empty_like(w)
+        db = np.empty((co,), np.float32)
+        r.ref_conv2d_bwd_f32(fp(x), fp(w), fp(dy), fp(dx), fp(dw), fp(db), n, c, h, wd, co, k, k,
+                             st, pad)
+        v.update({f"cbwd_{tag}_x": x, f"cbwd_{tag}_w": w, f"cbwd_{tag}_dy": dy,
+                  f"cbwd_{tag}_dx": dx, f"cbwd_{tag}_dw": dw, f"cbwd_{tag}_db": db,
+                  f"cbwd_{tag}_geom": np.array([st, pad], np.float32)})
+
     np.savez(OUT, **v)
+    write_bin(v, OUT.with_suffix(".bin"))
     print(f"wrote {OUT} ({OUT.stat().st_size} bytes, {len(v)} arrays)")
 
 

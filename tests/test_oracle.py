@@ -119,6 +119,37 @@ def test_golden_vectors(gold):
     np.testing.assert_array_equal(dx, g["lin_dx"])
     np.testing.assert_array_equal(dw, g["lin_dw_ref"].T)
     np.testing.assert_array_equal(db, g["lin_db"])
+    # conv backward from the reference's autograd, three images (per-image
+    # accumulation of dW and db), stride 1 and 2
+    for tag in ("s1", "s2"):
+        st, pad = (int(v) for v in g[f"cbwd_{tag}_geom"])
+        dx, dw, db = oracle.conv2d_backward(g[f"cbwd_{tag}_x"], g[f"cbwd_{tag}_w"],
+                                            g[f"cbwd_{tag}_dy"], st, pad)
+        np.testing.assert_array_equal(dx, g[f"cbwd_{tag}_dx"])
+        np.testing.assert_array_equal(dw, g[f"cbwd_{tag}_dw"])
+        np.testing.assert_array_equal(db, g[f"cbwd_{tag}_db"])
+
+
+def test_golden_binary_matches_npz(gold):
+    """The raw fixture the C++ host tests read holds the same arrays."""
+    import struct
+    raw = (GOLDEN.with_suffix(".bin")).read_bytes()
+    assert raw[:8] == b"MTGOLD01"
+    (count,) = struct.unpack_from("<I", raw, 8)
+    pos, seen = 12, {}
+    for _ in range(count):
+        (ln,) = struct.unpack_from("<I", raw, pos)
+        name = raw[pos + 4:pos + 4 + ln].decode()
+        pos += 4 + ln
+        (nd,) = struct.unpack_from("<I", raw, pos)
+        dims = struct.unpack_from(f"<{nd}Q", raw, pos + 4)
+        pos += 4 + 8 * nd
+        n = int(np.prod(dims)) if nd else 1
+        seen[name] = np.frombuffer(raw, "<f4", n, pos).reshape(dims)
+        pos += 4 * n
+    assert pos == len(raw) and sorted(seen) == sorted(gold)
+    for k in gold:
+        np.testing.assert_array_equal(seen[k], gold[k])
 
 
 @needs_ref
