@@ -188,8 +188,8 @@ def test_conv_backward_shapes(dev, n, c, h, wd, co, kh, kw, stride, pad):
 def test_config5a_conv_backward_adjoint(dev):
     # benchmark config 5a shape: dX and dW through the GEMM path, checked by the
     # size-independent adjoint identities <dY, conv(x,w)> = <dX, x> = <dW, w>
-    # (fp64 sums over every element), plus 8 sampled dW output channels against
-    # the oracle's conv2d_backward_weight_cpu.
+    # (fp64 sums over every element), plus 8 sampled dW output channels and two
+    # whole dX images against the oracle's conv2d_backward_{weight,input}_cpu.
     x = oracle.normal((32, 256, 14, 14), 42)
     w = oracle.normal((256, 256, 3, 3), 43, std=(2.0 / 2304) ** 0.5)
     dy = oracle.normal((32, 256, 14, 14), 44, std=0.01)
@@ -207,6 +207,12 @@ def test_config5a_conv_backward_adjoint(dev):
     _, wdw, wdb = oracle.conv2d_backward(x, w[ch], dy[:, ch], 1, 1)
     assert_close(dw[ch], wdw, 32 * 196, amax(dy), amax(x), "C5a dW sampled channels")
     assert_close(db, dy.astype(np.float64).sum(axis=(0, 2, 3)), 32 * 196, amax(dy), 1.0, "C5a db")
+    # dX element-wise on two whole images (first and last): an image's input
+    # gradient depends only on its own dY, so the oracle's
+    # conv2d_backward_input_cpu over those images alone is the exact reference
+    imgs = [0, 31]
+    wdx, _, _ = oracle.conv2d_backward(x[imgs], w, dy[imgs], 1, 1)
+    assert_close(dx[imgs], wdx, 256 * 9, amax(dy), amax(w), "C5a dX images 0 and 31")
 
 
 # ---- implicit-GEMM convolution ------------------------------------------------
