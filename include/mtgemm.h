@@ -133,12 +133,17 @@ int mt_linear_backward_f32(const mt_mat_f32* dY, const mt_mat_f32* X, const mt_m
  * (include/TensorOps.hpp:17-20).  Weight and output are dense (element
  * offsets applied by the caller).  The GEMM is C[c_out, n*h_out*w_out] =
  * W[c_out, c_in*kh*kw] · col[c_in*kh*kw, n*h_out*w_out] with the row bias fused
- * and the output scattered straight into NCHW.  When c_in % 16 == 0, col is
- * never formed: the input is copied to channels-last in the workspace (unless
- * it already is channels-last), the weights to OHWI, and the GEMM kernel
- * gathers the im2col operand from that copy (implicit GEMM); the workspace
- * holds the two copies and any split-K partials.  Otherwise an im2col pass
- * fills a column buffer in the workspace first.  mt_conv2d_workspace_f32
+ * and the output scattered straight into NCHW.  col is never formed when
+ *   c_in % 16 == 0: the input is copied to channels-last in the workspace
+ *     (unless it already is channels-last), the weights to OHWI, and the GEMM
+ *     kernel gathers the im2col operand from that copy with 16-byte loads;
+ *   else c_in*kh*kw % 4 == 0: the GEMM kernel gathers the im2col operand
+ *     from the NCHW input itself, 4 bytes per load, with the K order of the
+ *     OIHW weights, which it reads in place (a weight pointer that is not
+ *     16-byte aligned is first copied to the workspace).
+ * (Implicit GEMM; the workspace holds the copies and any split-K partials.)
+ * Otherwise an im2col pass fills a column buffer in the workspace first.
+ * mt_conv2d_workspace_f32
  * reports the size of whichever path the geometry takes; a workspace that is
  * missing or too small returns MT_ERR_WORKSPACE.  Replaces conv2d_gpu +
  * im2col_kernel + batched_sgemm_kernel_v2 (reference src/gpu_ops.cpp:2237-2325,
@@ -170,10 +175,11 @@ int mt_conv2d_fwd_strided_f32(const mt_conv2d_desc* d, const float* input,
  *           the kernel from a channels-last copy of the input (no column
  *           buffer), otherwise im2col fills one first
  *           replaces conv2d_backward_weight_gpu (reference src/gpu_ops.cpp:2623-2713)
- *   input:  stride 1, square kernel, pad <= kh-1, c_out % 16 == 0: the
+ *   input:  stride 1, square kernel, pad <= kh-1, c_out*kh*kw % 4 == 0: the
  *           implicit-GEMM forward convolution of dY with the weights
  *           transposed to [c_in][c_out] and flipped, padding kh-1-pad (no
- *           column buffer); otherwise dcol = Wᵀ · dY, then a deterministic
+ *           column buffer; channels-last when c_out % 16 == 0, else from
+ *           the NCHW dY); otherwise dcol = Wᵀ · dY, then a deterministic
  *           col2im gather into dX
  *           replaces conv2d_backward_input_gpu + fused_backward_input_kernel
  *           (reference src/gpu_ops.cpp:2499-2550, 861-907)

@@ -80,6 +80,11 @@ GemmLaunchFn dl_conv_launcher_cfg0();
 GemmLaunchFn dl_conv_launcher_cfg1();
 GemmLaunchFn dl_conv_launcher_cfg2();
 GemmLaunchFn dl_conv_launcher_cfg3();
+// Implicit-im2col convolution from an NCHW view: A = OIHW weights (L_KV), B = L_IMR.
+GemmLaunchFn dl_convr_launcher_cfg0();
+GemmLaunchFn dl_convr_launcher_cfg1();
+GemmLaunchFn dl_convr_launcher_cfg2();
+GemmLaunchFn dl_convr_launcher_cfg3();
 // Convolution weight gradient: A = dY [c_out][n*h_out*w_out] (L_KV), B = L_IMW.
 GemmLaunchFn dl_convw_launcher_cfg0();
 GemmLaunchFn dl_convw_launcher_cfg1();

@@ -1,7 +1,8 @@
 // gemm_dl_instances.hip -- instantiates gemm_f32_dl for one tile
 // configuration (selected with -DMT_CFG=<n>): the 2x2 vector operand layouts
 // (k-contiguous / mn-contiguous for A and for B), the implicit-im2col
-// convolution (A k-contiguous weights, B = L_IM) and its weight gradient
+// convolution (A k-contiguous weights, B = L_IM from a channels-last input or
+// L_IMR from an NCHW view) and its weight gradient
 // (A = dY as [c_out][n*h_out*w_out], B = L_IMW), and the mn-contiguous pair
 // with fused row sums of A (the Linear dW GEMM with its bias gradient).
 #include "gemm_configs.hpp"
@@ -34,6 +35,7 @@ GemmLaunchFn dl_launcher_cfg0(int la, int lb) {
     return table[la][lb];
 }
 GemmLaunchFn dl_conv_launcher_cfg0() { return launch_dl<0, L_KV, L_IM>; }
+GemmLaunchFn dl_convr_launcher_cfg0() { return launch_dl<0, L_KV, L_IMR>; }
 GemmLaunchFn dl_convw_launcher_cfg0() { return launch_dl<0, L_KV, L_IMW>; }
 GemmLaunchFn dl_rowsum_launcher_cfg0() { return launch_dl<0, L_MV, L_MV, true>; }
 #elif MT_CFG == 1
@@ -42,6 +44,7 @@ GemmLaunchFn dl_launcher_cfg1(int la, int lb) {
     return table[la][lb];
 }
 GemmLaunchFn dl_conv_launcher_cfg1() { return launch_dl<1, L_KV, L_IM>; }
+GemmLaunchFn dl_convr_launcher_cfg1() { return launch_dl<1, L_KV, L_IMR>; }
 GemmLaunchFn dl_convw_launcher_cfg1() { return launch_dl<1, L_KV, L_IMW>; }
 GemmLaunchFn dl_rowsum_launcher_cfg1() { return launch_dl<1, L_MV, L_MV, true>; }
 #elif MT_CFG == 2
@@ -50,6 +53,7 @@ GemmLaunchFn dl_launcher_cfg2(int la, int lb) {
     return table[la][lb];
 }
 GemmLaunchFn dl_conv_launcher_cfg2() { return launch_dl<2, L_KV, L_IM>; }
+GemmLaunchFn dl_convr_launcher_cfg2() { return launch_dl<2, L_KV, L_IMR>; }
 GemmLaunchFn dl_convw_launcher_cfg2() { return launch_dl<2, L_KV, L_IMW>; }
 GemmLaunchFn dl_rowsum_launcher_cfg2() { return launch_dl<2, L_MV, L_MV, true>; }
 #elif MT_CFG == 3
@@ -58,6 +62,7 @@ GemmLaunchFn dl_launcher_cfg3(int la, int lb) {
     return table[la][lb];
 }
 GemmLaunchFn dl_conv_launcher_cfg3() { return launch_dl<3, L_KV, L_IM>; }
+GemmLaunchFn dl_convr_launcher_cfg3() { return launch_dl<3, L_KV, L_IMR>; }
 GemmLaunchFn dl_convw_launcher_cfg3() { return launch_dl<3, L_KV, L_IMW>; }
 GemmLaunchFn dl_rowsum_launcher_cfg3() { return launch_dl<3, L_MV, L_MV, true>; }
 #else

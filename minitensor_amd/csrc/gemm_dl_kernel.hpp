@@ -39,7 +39,7 @@ namespace mtk {
 // instruction.  The implicit-im2col operand uses the k-contiguous tile.
 template <int L, int BMN, int NW>
 struct DlTile {
-    static_assert(L == L_KV || L == L_MV || L == L_IM || L == L_IMW,
+    static_assert(L == L_KV || L == L_MV || L == L_IM || L == L_IMW || L == L_IMR,
                   "direct-to-LDS needs a DMA layout");
     static constexpr bool kc = (L == L_KV || L == L_IM);
     static constexpr int floats = BMN * 16;
@@ -217,6 +217,118 @@ struct DlImLoader {
     }
 };
 
+// Implicit im2col of an NCHW view (any strides) as the B operand (L_IMR), in
+// the K order (ci, r, s) of OIHW weights, so that A is the weight tensor
+// itself.  The tile is the n-contiguous [16][BN] one of L_MV, filled by 4-byte
+// DMA (global_load_lds_dword): one wave instruction moves one k-row of 64
+// consecutive output pixels, which read mostly contiguous runs of an input
+// row.  Each lane keeps the same pixel for all its instructions (NW is a
+// multiple of BN/64), so the per-lane state is that pixel's window; the k-row
+// of an instruction is wave-uniform, so its tap (r, s) and element offset
+// c*sc + r*sh + s*sw are scalar state, stepped by 16 k per chunk with
+// additions (chunks are issued in order 0, 1, 2, ...; issue_tail decodes the
+// partial last chunk).  Per instruction a lane only tests its window against
+// the image and selects its address; a tap in the padding, a pixel past N or
+// (tail) a k past the K range reads the zero page.
+template <int BN, int NW>
+struct DlImrLoader {
+    static constexpr int INSTS = BN * 16 / 64;   // 4-byte DMA instructions per chunk
+    static constexpr int per_wave = INSTS / NW;
+    static_assert(per_wave * NW == INSTS, "instructions must split evenly over the waves");
+    static_assert(NW % (BN / 64) == 0, "a lane keeps one pixel for all its instructions");
+    const float* pix;        // input + img*img_stride + ih0*sh + iw0*sw of the lane's pixel
+    int ih0, iw0;            // the window's top-left input row / column (far negative past N)
+    int kr[per_wave];        // k-row of each instruction within a chunk: wave-uniform
+    int r[per_wave], s[per_wave];   // tap of each instruction's k in the next chunk
+    int64_t off[per_wave];          // c*sc + r*sh + s*sw of that k
+    int k0, k_end, kh, kw, h, w, dr, ds;
+    int64_t sc, sh, sw;
+    int64_t step, carry_s, carry_r;   // offset steps: 16 k; s wraps; r wraps
+
+    __device__ __forceinline__ void decode(int k, int& c_, int& r_, int& s_) const {
+        const int khw = kh * kw;
+        c_ = k / khw;
+        const int tap = k - c_ * khw;
+        r_ = tap / kw;
+        s_ = tap - r_ * kw;
+    }
+
+    __device__ __forceinline__ void init(const GemmParams& p, const float* X, int n0, int kbegin,
+                                         int kend, int wave, int lane) {
+        const ConvGeom& g = p.cv;
+        kh = g.kh; kw = g.kw; h = g.h; w = g.w;
+        sc = g.sc; sh = g.sh; sw = g.sw;
+        k0 = kbegin;
+        k_end = kend;
+        // one chunk (16 k) in mixed radix (c, r, s)
+        const int khw = kh * kw;
+        const int dci = 16 / khw;
+        dr = (16 - dci * khw) / kw;
+        ds = 16 - dci * khw - dr * kw;
+        step = dci * sc + dr * sh + ds * sw;
+        carry_s = sh - kw * sw;
+        carry_r = sc - kh * sh;
+        int n = n0 + 64 * (wave % (BN / 64)) + lane;
+        const bool nok = n < p.N;
+        if (!nok) n = p.N - 1;
+        const int hw = g.ho * g.wo;
+        const int img = n / hw, rem = n - img * hw;
+        const int oh = rem / g.wo, ow = rem - oh * g.wo;
+        ih0 = nok ? oh * g.stride - g.pad : -(1 << 29);
+        iw0 = ow * g.stride - g.pad;
+        pix = X + (int64_t)img * g.img_stride + (int64_t)(oh * g.stride - g.pad) * sh +
+              (int64_t)iw0 * sw;
+#pragma unroll
+        for (int j = 0; j < per_wave; ++j) {
+            kr[j] = (j * NW + wave) / (BN / 64);
+            int c_;
+            decode(k0 + kr[j], c_, r[j], s[j]);
+            off[j] = c_ * sc + r[j] * sh + s[j] * sw;
+        }
+    }
+
+    __device__ __forceinline__ const float* source(int r_, int s_, int64_t o) const {
+        const bool ok = (unsigned)(ih0 + r_) < (unsigned)h && (unsigned)(iw0 + s_) < (unsigned)w;
+        return ok ? pix + o : dl_zero_page;
+    }
+
+    __device__ __forceinline__ static void dma(const float* src, float* dst) {
+        __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1)))*)src,
+                                         (void __attribute__((address_space(3)))*)dst, 4, 0, 0);
+    }
+
+    // Issue the DMA of the next whole chunk in order (every k inside the K
+    // range), then step the taps and offsets by 16 k.
+    __device__ __forceinline__ void issue(float* tile, int /*chunk*/, int wave) {
+#pragma unroll
+        for (int j = 0; j < per_wave; ++j) {
+            dma(source(r[j], s[j], off[j]), tile + (j * NW + wave) * 64);
+            // carries as masks (all-ones when s or r wraps): scalar arithmetic
+            int s2 = s[j] + ds, r2 = r[j] + dr;
+            const int ms = (kw - 1 - s2) >> 31;
+            s2 -= kw & ms;
+            r2 -= ms;
+            const int mr = (kh - 1 - r2) >> 31;
+            r2 -= kh & mr;
+            s[j] = s2; r[j] = r2;
+            off[j] += step + (carry_s & (int64_t)ms) + (carry_r & (int64_t)mr);
+        }
+    }
+
+    // The DMA of chunk `chunk` (the partial last one): k past k_end reads
+    // zeros.  The stepped state is untouched.
+    __device__ __forceinline__ void issue_tail(float* tile, int chunk, int wave) const {
+#pragma unroll
+        for (int j = 0; j < per_wave; ++j) {
+            const int k = k0 + chunk * 16 + kr[j];
+            int c_, r_, s_;
+            decode(k, c_, r_, s_);
+            const float* src = source(r_, s_, c_ * sc + r_ * sh + s_ * sw);
+            dma(k < k_end ? src : dl_zero_page, tile + (j * NW + wave) * 64);
+        }
+    }
+};
+
 // Implicit im2colᵀ of a channels-last input as the B operand of the
 // convolution weight gradient (L_IMW), tile [16][BMN] (n contiguous, the L_MV
 // LDS layout).  A lane of instruction q covers k-row kr = (q*256 + 4*lane) / BMN
@@ -361,8 +473,10 @@ gemm_f32_dl(GemmParams p) {
     static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be 32-aligned");
     using TA = DlTile<LA, BM, NW>;
     using TB = DlTile<LB, BN, NW>;
+    constexpr bool imr = (LB == L_IMR);   // B moved by 4-byte DMA
     constexpr int STAGE = TA::floats + TB::floats;
-    constexpr int LOADS = TA::per_wave + TB::per_wave;   // wave instructions per chunk
+    // DMA instructions per wave per chunk
+    constexpr int LOADS = TA::per_wave + (imr ? DlImrLoader<BN, NW>::per_wave : TB::per_wave);
     static_assert(LOADS * (STAGES - 2) < 64, "vmcnt holds at most 63");
     __shared__ __attribute__((aligned(1024))) float smem[STAGES * STAGE];
 
@@ -380,7 +494,8 @@ gemm_f32_dl(GemmParams p) {
     const int k_end = min(p.K, k_begin + p.k_per_split);
     const int klen = k_end > k_begin ? k_end - k_begin : 0;
     const int nk = klen >> 4;                 // full chunks
-    // The implicit operand has c % 16 == 0, so its K ranges hold whole chunks.
+    // The channels-last implicit operand has c % 16 == 0, so its K ranges
+    // hold whole chunks.
     const bool tail = LB != L_IM && (klen & 15) != 0;
     const float* Ab = p.A + (int64_t)id.bz * p.a_b;
     const float* Bb = p.B + (int64_t)id.bz * p.b_b;
@@ -395,7 +510,7 @@ gemm_f32_dl(GemmParams p) {
 
     constexpr bool im = (LB == L_IM);
     constexpr bool imw = (LB == L_IMW);
-    constexpr int LBF = im ? L_KV : imw ? L_MV : LB;   // LDS layout of B's tile
+    constexpr int LBF = im ? L_KV : (imw || imr) ? L_MV : LB;   // LDS layout of B's tile
     // Fused row sums of A: the waves of the first wave column of the first
     // tile column see every A fragment of their rows exactly once.
     const bool do_rs = RS && id.tn == 0 && wn == 0;
@@ -412,19 +527,24 @@ gemm_f32_dl(GemmParams p) {
 
     DlTail<LA, BM, NT> ta;
     std::conditional_t<imw, DlImwTail<BN, NT>, DlTail<LBF, BN, NT>> tb;
+    DlLoader<LA, BM, NW> la;
+    std::conditional_t<
+        im, DlImLoader<BN, NW>,
+        std::conditional_t<imw, DlImwLoader<BN, NW>,
+                           std::conditional_t<imr, DlImrLoader<BN, NW>, DlLoader<LBF, BN, NW>>>>
+        lb;
+    la.init(Ab, p.a_mn, p.a_k, p.M, m0, k_begin, wave, lane);
+    if constexpr (im || imw || imr) lb.init(p, Bb, n0, k_begin, k_end, wave, lane);
+    else lb.init(Bb, p.b_mn, p.b_k, p.N, n0, k_begin, wave, lane);
     if (tail) {
         const int kt0 = k_begin + nk * 16;
         ta.load(Ab, p.a_mn, p.a_k, p.M, m0, kt0, k_end, t);
-        if constexpr (imw) tb.load(p, Bb, n0, kt0, k_end, t);
+        // (L_IMR: by DMA into the last ring slot, free until the first
+        // loop iteration's barrier; waited for below)
+        if constexpr (imr) lb.issue_tail(smem + (STAGES - 1) * STAGE + TA::floats, nk, wave);
+        else if constexpr (imw) tb.load(p, Bb, n0, kt0, k_end, t);
         else tb.load(Bb, p.b_mn, p.b_k, p.N, n0, kt0, k_end, t);
     }
-
-    DlLoader<LA, BM, NW> la;
-    std::conditional_t<im, DlImLoader<BN, NW>,
-                       std::conditional_t<imw, DlImwLoader<BN, NW>, DlLoader<LBF, BN, NW>>> lb;
-    la.init(Ab, p.a_mn, p.a_k, p.M, m0, k_begin, wave, lane);
-    if constexpr (im || imw) lb.init(p, Bb, n0, k_begin, k_end, wave, lane);
-    else lb.init(Bb, p.b_mn, p.b_k, p.N, n0, k_begin, wave, lane);
 
 #pragma unroll
     for (int c = 0; c < STAGES - 1; ++c)
@@ -437,8 +557,14 @@ gemm_f32_dl(GemmParams p) {
         // Slot STAGES-1 is free until the first loop iteration's barrier.
         float* const st = smem + (STAGES - 1) * STAGE;
         ta.store(st, t);
-        tb.store(st + TA::floats, t);
-        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));
+        if constexpr (imr) {
+            // the tail DMA was issued before the prologue's chunks
+            if (nk >= STAGES - 1) __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(LOADS * (STAGES - 1)));
+            else __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+        } else {
+            tb.store(st + TA::floats, t);
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(63));
+        }
         __builtin_amdgcn_s_barrier();
         float fa[MB][8], fb[NB][8];
         dl_frags<LA, BM, MB>(st, ra, lane, fa);
@@ -446,7 +572,6 @@ gemm_f32_dl(GemmParams p) {
         mfma_chunk<MB, NB>(acc, fa, fb);
         add_rows(fa);
     }
-
     for (int kt = 0; kt < nk; ++kt) {
         // Chunk kt must have landed (own instructions, then everyone's).
         // The barrier also retires every wave's reads of the slot refilled

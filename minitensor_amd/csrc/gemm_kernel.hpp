@@ -56,7 +56,9 @@ enum : int {
     L_KS = 2,  // k-contiguous LDS tile, scalar gathers (any strides)
     L_MS = 3,  // mn-contiguous LDS tile, scalar gathers (any strides)
     L_IM = 4,  // B only, direct-to-LDS kernel: implicit im2col of a channels-last input
-    L_IMW = 5  // B only, direct-to-LDS kernel: implicit im2colᵀ (conv weight gradient)
+    L_IMW = 5, // B only, direct-to-LDS kernel: implicit im2colᵀ (conv weight gradient)
+    L_IMR = 6  // B only, direct-to-LDS kernel: implicit im2col of an NCHW view, K order
+               // (ci, r, s), gathered through registers
 };
 
 // Geometry of an implicit-im2col B operand over a channels-last input
@@ -69,9 +71,13 @@ enum : int {
 //          consecutive channels of one tap);
 // both read xt[img][oh*stride - pad + r][ow*stride - pad + s][ci], zero
 // outside the image.
+//   L_IMR: B(k, n) with k = (ci*kh + r)*kw + s -- the OIHW weights' own K
+//          order, so they need no reorder -- and n as for L_IM, read from an
+//          NCHW view of any strides (img_stride, sc, sh, sw) of the input.
 struct ConvGeom {
     int64_t img_stride;
     int c, h, w, kh, kw, stride, pad, ho, wo;
+    int64_t sc, sh, sw;   // L_IMR: element strides of a channel, a row, a column
 };
 
 struct GemmParams {

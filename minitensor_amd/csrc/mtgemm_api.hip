@@ -88,6 +88,7 @@ const char* layout_name(int l) {
         case L_MV: return "mv";
         case L_IM: return "im2col";
         case L_IMW: return "im2colT";
+        case L_IMR: return "im2col_nchw";
         case L_KS: return "ks";
         default: return "ms";
     }
@@ -334,12 +335,12 @@ GemmLaunchFn convw_launcher(int cfg, bool ktail) {
     }
 }
 
-GemmLaunchFn conv_launcher(int cfg) {
+GemmLaunchFn conv_launcher(int cfg, bool nchw) {
     switch (cfg) {
-        case 0: return dl_conv_launcher_cfg0();
-        case 1: return dl_conv_launcher_cfg1();
-        case 2: return dl_conv_launcher_cfg2();
-        case 3: return dl_conv_launcher_cfg3();
+        case 0: return nchw ? dl_convr_launcher_cfg0() : dl_conv_launcher_cfg0();
+        case 1: return nchw ? dl_convr_launcher_cfg1() : dl_conv_launcher_cfg1();
+        case 2: return nchw ? dl_convr_launcher_cfg2() : dl_conv_launcher_cfg2();
+        case 3: return nchw ? dl_convr_launcher_cfg3() : dl_conv_launcher_cfg3();
         default: return nullptr;
     }
 }
@@ -480,7 +481,7 @@ __global__ void __launch_bounds__(256) splitk_reduce_vec_f32(GemmParams p) {
 int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t ws_bytes,
                 hipStream_t stream) {
     const int64_t M = p.M, N = p.N, K = p.K, batch = p.batch;
-    const bool implicit = lb == L_IM || lb == L_IMW;
+    const bool implicit = lb == L_IM || lb == L_IMW || lb == L_IMR;
     // 16-byte epilogue stores: four consecutive columns must be contiguous,
     // aligned, and (for a scattered output) never straddle a column group.
     p.c_vec = p.c_n == 1 && (N & 3) == 0 && ((uintptr_t)p.C & 15u) == 0 && (p.c_m & 3) == 0 &&
@@ -489,7 +490,7 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
     // The prefetching configurations' contract: vector layouts or the
     // weight-gradient operand (not the implicit-im2col one), no fused row
     // sums, a non-empty K range.
-    const bool wide_ok = dl && lb != L_IM && p.rowsum == nullptr && K > 0;
+    const bool wide_ok = dl && lb != L_IM && lb != L_IMR && p.rowsum == nullptr && K > 0;
     Plan plan;
     if (forced_plan(M, N, K, batch, dl, !implicit, wide_ok, &plan)) {
         if (plan.splits > 1 && (workspace == nullptr || ws_bytes < plan.ws_bytes))
@@ -523,7 +524,7 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
                   plan.bn, layout_name(la), layout_name(lb), plan.splits, (long long)nblocks,
                   plan.cfg);
 
-    GemmLaunchFn fn = lb == L_IM          ? conv_launcher(plan.cfg)
+    GemmLaunchFn fn = lb == L_IM || lb == L_IMR ? conv_launcher(plan.cfg, lb == L_IMR)
                       : lb == L_IMW         ? convw_launcher(plan.cfg, (K & 15) != 0)
                       : p.rowsum != nullptr ? rowsum_launcher(plan.cfg)
                                             : pick_launcher(plan, la, lb, (K & 15) != 0);
@@ -974,6 +975,43 @@ int run_conv_implicit(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, const flo
     return launch_gemm(p, true, L_KV, L_IM, wsp + iw.xt + iw.wt, ws_bytes - iw.xt - iw.wt, s);
 }
 
+// The implicit-GEMM convolution over an NCHW view (L_IMR) reads the OIHW
+// weights as its A operand in 16-byte rows: kg % 4 == 0 (weights that are not
+// 16-byte aligned are first copied to the workspace, nchw_weight_ws bytes).
+bool nchw_implicit(const mt_conv2d_desc* d) {
+    const int64_t kg = d->c_in * d->kh * d->kw;
+    return kg > 0 && (kg & 3) == 0 && d->h * d->w < kMaxDim;
+}
+size_t nchw_weight_ws(const mt_conv2d_desc* d) {
+    return align_up((size_t)d->c_out * d->c_in * d->kh * d->kw * sizeof(float), 256);
+}
+
+// Implicit-GEMM convolution of an NCHW view (any strides): C[c_out, np] =
+// W[c_out, kg] · im2col(x)[kg, np] with k = (ci*kh + r)*kw + s, the weights'
+// own order, so neither operand is copied: the kernel gathers the im2col
+// operand from the view through in_strides.  The workspace holds only split-K
+// partials.  Needs nchw_implicit(d) and a 16-byte-aligned weight.
+int run_conv_nchw(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, const float* input,
+                  const int64_t in_strides[4], const float* weight, const float* bias,
+                  float* output, void* workspace, size_t ws_bytes, hipStream_t s) {
+    const int64_t kg = d->c_in * d->kh * d->kw, hw = Ho * Wo, np = d->n * hw;
+    GemmParams p{};
+    p.A = weight; p.a_mn = kg; p.a_k = 1; p.a_b = 0;
+    p.B = input;
+    p.C = output; p.c_m = hw; p.c_n = 1; p.c_b = 0;
+    p.c_n_inner = hw; p.c_n_outer = d->c_out * hw;
+    p.bias = bias; p.bias_stride = 1; p.bias_axis = bias ? MT_BIAS_ROW : MT_BIAS_NONE;
+    p.beta = 0.f;
+    p.M = (int)d->c_out; p.N = (int)np; p.K = (int)kg; p.batch = 1;
+    ConvGeom& g = p.cv;
+    g.img_stride = in_strides[0];
+    g.sc = in_strides[1]; g.sh = in_strides[2]; g.sw = in_strides[3];
+    g.c = (int)d->c_in; g.h = (int)d->h; g.w = (int)d->w;
+    g.kh = (int)d->kh; g.kw = (int)d->kw; g.stride = (int)d->stride; g.pad = (int)d->pad;
+    g.ho = (int)Ho; g.wo = (int)Wo;
+    return launch_gemm(p, true, L_KV, L_IMR, workspace, ws_bytes, s);
+}
+
 // The implicit weight gradient reads 4 channels of one tap per 16-byte vector
 // (c_in % 4 == 0) and dYt [c_out][np] rows as 16-byte vectors (np % 4 == 0).
 bool implicit_dw(const mt_conv2d_desc* d, int64_t np) {
@@ -984,12 +1022,19 @@ bool implicit_dw(const mt_conv2d_desc* d, int64_t np) {
 // forward convolution of dY (c_out channels, h_out x w_out) with the weights
 // transposed to [c_in][c_out] and flipped in both spatial axes, padding
 // kh - 1 - pad: dX[ci][ih][iw] = sum_{co,r,s} W[co][ci][r][s]·dY[co][ih+pad-r][iw+pad-s].
-// Returns the descriptor of that convolution, or false when it does not apply
-// (or would not take the implicit path).
+// Returns the descriptor of that convolution, or false when it does not apply:
+// it runs on the channels-last kernel when c_out % 16 == 0, else on the NCHW
+// kernel, whose flipped weights (written densely to the workspace) must take
+// 16-byte rows (c_out*kh*kw % 4 == 0).
 bool dx_as_forward(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, mt_conv2d_desc* t) {
     if (d->stride != 1 || d->kh != d->kw || d->pad > d->kh - 1) return false;
     *t = mt_conv2d_desc{d->n, d->c_out, Ho, Wo, d->c_in, d->kh, d->kw, 1, d->kh - 1 - d->pad};
-    return implicit_geometry(t) && Ho * Wo < kMaxDim;
+    return ((d->c_out * d->kh * d->kw) & 3) == 0 && d->c_out > 0 && Ho * Wo < kMaxDim;
+}
+
+// Bytes of the flipped, transposed weights of the implicit dX.
+size_t flipped_ws(const mt_conv2d_desc* d) {
+    return align_up((size_t)d->c_in * d->c_out * d->kh * d->kw * sizeof(float), 256);
 }
 
 }  // namespace
@@ -1097,10 +1142,13 @@ size_t mt_conv2d_workspace_f32(const mt_conv2d_desc* d) {
     const int64_t kg = d->c_in * d->kh * d->kw, np = d->n * Ho * Wo;
     if (np == 0 || d->c_out == 0) return 0;
     const size_t gemm = plan_ws(d->c_out, np, kg, 1, device_cu_count());
-    if (implicit_geometry(d) && d->h * d->w < kMaxDim) {   // no column buffer
+    if (implicit_geometry(d) && d->h * d->w < kMaxDim) {   // channels-last kernel
         const ImplicitWs iw = implicit_ws(d);
         return iw.xt + iw.wt + gemm;
     }
+    // the NCHW-view kernel: split-K partials, and room for an aligned copy of
+    // the weights (used only when the caller's are not 16-byte aligned)
+    if (nchw_implicit(d)) return nchw_weight_ws(d) + gemm;
     return align_up((size_t)kg * np * sizeof(float), 256) + gemm;
 }
 
@@ -1116,6 +1164,10 @@ int mt_conv2d_fwd_strided_f32(const mt_conv2d_desc* d, const float* input,
     if (!output || (kg > 0 && (!input || !weight))) return MT_ERR_INVALID;
     hipStream_t s = static_cast<hipStream_t>(stream);
 
+    // c_in % 16 == 0: the channels-last kernel (16-byte DMA gathers) on a
+    // channels-last copy of the input (the input itself when it is one) and
+    // OHWI weights.  Its gathers beat the NCHW-view kernel's 4-byte ones by
+    // more than the two copies cost (benchmark layer: 84 vs 95 us).
     if (implicit_geometry(d) && d->h * d->w < kMaxDim) {
         const ImplicitWs iw = implicit_ws(d);
         if (!workspace || ws_bytes < iw.xt + iw.wt || ((uintptr_t)workspace & 15u) != 0)
@@ -1126,6 +1178,22 @@ int mt_conv2d_fwd_strided_f32(const mt_conv2d_desc* d, const float* input,
                              d->kh * d->kw, d->c_out, wt, s) != hipSuccess)
             return MT_ERR_HIP;
         return run_conv_implicit(d, Ho, Wo, input, in_strides, bias, output, wsp, ws_bytes, s);
+    }
+    // other channel counts with kg % 4 == 0: the implicit GEMM over the NCHW
+    // view, no copy of either operand and no column buffer
+    if (nchw_implicit(d)) {
+        const size_t wb = nchw_weight_ws(d);
+        if (!workspace || ws_bytes < wb || ((uintptr_t)workspace & 15u) != 0)
+            return MT_ERR_WORKSPACE;
+        char* wsp = static_cast<char*>(workspace);
+        if (((uintptr_t)weight & 15u) != 0) {
+            if (hipMemcpyAsync(wsp, weight, (size_t)d->c_out * kg * sizeof(float),
+                               hipMemcpyDeviceToDevice, s) != hipSuccess)
+                return MT_ERR_HIP;
+            weight = reinterpret_cast<const float*>(wsp);
+        }
+        return run_conv_nchw(d, Ho, Wo, input, in_strides, weight, bias, output, wsp + wb,
+                             ws_bytes - wb, s);
     }
 
     // Explicit im2col into the workspace, then the GEMM on the column buffer.
@@ -1169,10 +1237,13 @@ size_t mt_conv2d_bwd_workspace_f32(const mt_conv2d_desc* d) {
                                   plan_ws(d->c_out, kg, np, 1, cus));
     mt_conv2d_desc t;
     if (dx_as_forward(d, Ho, Wo, &t)) {   // implicit dX (usually smaller than the above)
-        const ImplicitWs iw = implicit_ws(&t);
-        need = std::max(need, iw.xt + iw.wt +
-                                  plan_ws(d->c_in, d->n * d->h * d->w, d->c_out * d->kh * d->kw,
-                                          1, cus));
+        const size_t g = plan_ws(d->c_in, d->n * d->h * d->w, d->c_out * d->kh * d->kw, 1, cus);
+        if (implicit_geometry(&t)) {
+            const ImplicitWs iw = implicit_ws(&t);
+            need = std::max(need, iw.xt + iw.wt + g);
+        } else {
+            need = std::max(need, flipped_ws(d) + g);
+        }
     }
     return need;
 }
@@ -1254,8 +1325,9 @@ int mt_conv2d_bwd_input_f32(const mt_conv2d_desc* d, const float* grad_out, cons
     }
     if (!grad_out || !weight) return MT_ERR_INVALID;
     mt_conv2d_desc t;
-    if (dx_as_forward(d, Ho, Wo, &t)) {
-        // Implicit GEMM of dY with the flipped, transposed weights: no dcol buffer.
+    if (dx_as_forward(d, Ho, Wo, &t) && implicit_geometry(&t)) {
+        // Channels-last implicit GEMM of dY with the weights transposed to
+        // [c_in][c_out] and flipped (OHWI of the dX convolution): no dcol buffer.
         int64_t th, tw;
         if (!conv_dims(&t, &th, &tw) || th != d->h || tw != d->w) return MT_ERR_INVALID;
         const ImplicitWs iw = implicit_ws(&t);
@@ -1270,6 +1342,25 @@ int mt_conv2d_bwd_input_f32(const mt_conv2d_desc* d, const float* grad_out, cons
         const int64_t st[4] = {d->c_out * hw, hw, Wo, 1};   // dense dY
         return run_conv_implicit(&t, d->h, d->w, grad_out, st, nullptr, grad_input, wsp, ws_bytes,
                                  s);
+    }
+    if (dx_as_forward(d, Ho, Wo, &t)) {
+        // Other c_out: the implicit GEMM of dY (NCHW, read in place) with the
+        // flipped, transposed weights in OIHW order: no dcol buffer, no copy of dY.
+        int64_t th, tw;
+        if (!conv_dims(&t, &th, &tw) || th != d->h || tw != d->w) return MT_ERR_INVALID;
+        const size_t fb = flipped_ws(d);
+        if (!workspace || ws_bytes < fb || ((uintptr_t)workspace & 15u) != 0)
+            return MT_ERR_WORKSPACE;
+        char* wsp = static_cast<char*>(workspace);
+        float* wf = reinterpret_cast<float*>(wsp);
+        // wf[ci][co][r'][s'] = W[co][ci][kh-1-r'][kw-1-s'] (OIHW of the dX convolution)
+        const int64_t khw = d->kh * d->kw;
+        if (launch_transpose(weight + (khw - 1), khw, -1, 0, d->c_in * khw, d->c_out, khw,
+                             d->c_out, d->c_in, wf, s) != hipSuccess)
+            return MT_ERR_HIP;
+        const int64_t st[4] = {d->c_out * hw, hw, Wo, 1};   // dense dY
+        return run_conv_nchw(&t, d->h, d->w, grad_out, st, wf, nullptr, grad_input, wsp + fb,
+                             ws_bytes - fb, s);
     }
     const size_t col_b = align_up((size_t)kg * np * sizeof(float), 256);
     const size_t dyt_b = align_up((size_t)d->c_out * np * sizeof(float), 256);

@@ -245,6 +245,58 @@ def test_conv_implicit_shapes(dev, n, c, h, wd, co, kh, kw, stride, pad):
     assert_close(out, want, c * kh * kw, amax(x), amax(w), "implicit conv", extra=1e-5)
 
 
+# The implicit GEMM over an NCHW view (K order (ci, r, s), the OIHW weights
+# read in place): any c_in with c_in*kh*kw % 4 == 0, including K ranges that
+# end in a partial chunk, fewer K than one chunk, rectangular kernels, strides
+# 2 and 3, padding 0 and 2, and output-channel tails; forward and (stride 1,
+# square kernels) the input gradient.
+@pytest.mark.parametrize("n,c,h,wd,co,kh,kw,stride,pad", [
+    (2, 4, 9, 9, 8, 3, 3, 1, 1),       # kg = 36: a partial last chunk
+    (1, 12, 7, 7, 10, 5, 5, 2, 2),     # kg = 300, stride 2
+    (2, 8, 6, 6, 5, 1, 1, 1, 0),       # kg = 8: less than one chunk
+    (1, 20, 11, 9, 7, 3, 2, 1, 1),     # 3x2 kernel
+    (3, 4, 10, 12, 66, 3, 3, 3, 0),    # stride 3, no padding, c_out tail
+])
+def test_conv_nchw_implicit_geometries(dev, n, c, h, wd, co, kh, kw, stride, pad):
+    x = oracle.normal((n, c, h, wd), 400 + c)
+    w = oracle.normal((co, c, kh, kw), 401 + co)
+    b = oracle.normal((co,), 402)
+    out = sync_np(mt.conv2d(g(x, dev), g(w, dev), g(b, dev), stride, pad))
+    cfg = mt.last_config()
+    print(f"[config] {cfg}")
+    assert "b=im2col_nchw" in cfg, cfg
+    assert_close(out, oracle.conv2d(x, w, b, stride, pad), c * kh * kw, amax(x), amax(w),
+                 "NCHW implicit conv", extra=1e-5)
+    if stride == 1 and kh == kw and pad <= kh - 1 and (co * kh * kw) % 4 == 0:
+        ho, wo = oracle.conv_out(h, pad, kh, 1), oracle.conv_out(wd, pad, kw, 1)
+        dy = oracle.normal((n, co, ho, wo), 403)
+        dx, _, _ = mt.conv2d_backward(g(x, dev), g(w, dev), g(dy, dev), 1, pad, need_dw=False,
+                                      need_db=False)
+        cfg = mt.last_config()
+        print(f"[config] dX {cfg}")
+        assert "b=im2col_nchw" in cfg, cfg
+        wdx, _, _ = oracle.conv2d_backward(x, w, dy, 1, pad)
+        assert_close(sync_np(dx), wdx, co * kh * kw, amax(dy), amax(w), "NCHW implicit dX")
+
+
+def test_conv_nchw_unaligned_weight(dev):
+    """Weights that are not 16-byte aligned (a view one float into a buffer)
+    are copied to the workspace the query reserves, then read as A."""
+    n, c, h, wd, co = 2, 4, 9, 10, 12
+    x = oracle.normal((n, c, h, wd), 404)
+    w = oracle.normal((co, c, 3, 3), 405)
+    buf = torch.zeros(w.size + 1, dtype=torch.float32, device=dev)
+    buf[1:] = g(w.reshape(-1), dev)
+    W = buf[1:].view(co, c, 3, 3)
+    assert W.data_ptr() % 16 != 0
+    out = sync_np(mt.conv2d(g(x, dev), W, None, 1, 1))
+    cfg = mt.last_config()
+    print(f"[config] {cfg}")
+    assert "b=im2col_nchw" in cfg, cfg
+    assert_close(out, oracle.conv2d(x, w, None, 1, 1), c * 9, amax(x), amax(w),
+                 "unaligned weight")
+
+
 @pytest.mark.parametrize("view", ["channel_slice", "spatial_crop", "nhwc", "batch_step"])
 @pytest.mark.parametrize("c", [16, 3])   # 16: implicit path; 3 (kg = 27): explicit im2col
 def test_conv_strided_input_views(dev, view, c):
