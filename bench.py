@@ -425,12 +425,17 @@ def cpu_config_baselines() -> dict:
 
 def copy_probe(dev) -> None:
     """Five copies of a 256 MiB tensor (__amd_rocclr_copyBuffer): reads and
-    writes 256 MiB each, the calibration of FETCH_SIZE / WRITE_SIZE."""
+    writes 256 MiB each, the calibration of FETCH_SIZE / WRITE_SIZE.  Then
+    five fills of a 64 MiB tensor: a write-only stream, the reference for
+    store-bound kernels."""
     import torch
     src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
     dst = torch.empty_like(src)
     for _ in range(5):
         dst.copy_(src)
+    out = torch.empty(16 << 20, dtype=torch.float32, device=dev)
+    for _ in range(5):
+        out.fill_(2.0)
     torch.cuda.synchronize()
 
 
