@@ -58,7 +58,7 @@ enum : int {
     L_IM = 4,  // B only, direct-to-LDS kernel: implicit im2col of a channels-last input
     L_IMW = 5, // B only, direct-to-LDS kernel: implicit im2colᵀ (conv weight gradient)
     L_IMR = 6  // B only, direct-to-LDS kernel: implicit im2col of an NCHW view, K order
-               // (ci, r, s), gathered through registers
+               // (ci, r, s), gathered by 4-byte DMA
 };
 
 // Geometry of an implicit-im2col B operand over a channels-last input

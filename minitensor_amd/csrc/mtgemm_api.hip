@@ -877,48 +877,141 @@ hipError_t transpose_dy(const mt_conv2d_desc* d, int64_t hw, const float* dy, fl
                         d->n, hw, s);
 }
 
-// out[b][j][i] = in[b*sb + i*si + (j / jw)*sj1 + (j % jw)*sj0], out dense
-// [B][J][I]: a batched transpose through a 32x33 LDS tile, reads coalesced
-// along j (when sj0 == 1) and writes coalesced along i.  With b = image,
-// i = channel, j = pixel it turns an NCHW view into channels-last; with
-// b = c_out, i = c_in, j = filter tap it turns OIHW weights into OHWI.
-__global__ void __launch_bounds__(256)
-transpose_f32(const float* in, int64_t sb, int64_t si, int64_t sj1, int64_t sj0, int jw, int I,
-              int J, int B, float* out) {
-    __shared__ float tile[32][33];
-    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
-    const int i0 = blockIdx.y * 32, j0 = blockIdx.x * 32;
-    for (int b = blockIdx.z; b < B; b += gridDim.z) {
-        const float* src = in + (int64_t)b * sb;
+// One layout change: out[b][j][i] = in[b*sb + i*si + (j / jw)*sj1 + (j % jw)*sj0],
+// out dense [B][J][I], moved in TI x TJ tiles (2048 elements, 8 per thread)
+// through LDS.  Reads run along j (coalesced when sj0 == 1), or along i when
+// ri is set (si == 1: a batched copy that only reorders the outer
+// dimensions); writes run along i.  With b = image, i = channel, j = pixel it
+// turns an NCHW view into channels-last; with b = c_out, i = c_in, j = filter
+// tap it turns OIHW weights into OHWI.  Tiles are TI x TJ = 32 x 64, or
+// 64 x 32 when J <= 32, or 128 x 16 when J <= 16 (filter taps), so that few
+// threads idle.
+struct TJob {
+    const float* in;
+    float* out;
+    int64_t sb, si, sj1, sj0;
+    int jw, I, J, B;
+    int lti, ltj;      // log2 of the tile's extent along i and j
+    int ti, tj;        // tiles along i and j
+    int ri;            // read along i
+    int64_t blocks;    // ti * tj * B
+};
+
+TJob tjob(const float* in, int64_t sb, int64_t si, int64_t sj1, int64_t sj0, int64_t jw,
+          int64_t I, int64_t J, int64_t B, float* out) {
+    TJob t{};
+    t.in = in; t.out = out;
+    t.sb = sb; t.si = si; t.sj1 = sj1; t.sj0 = sj0;
+    t.jw = (int)jw; t.I = (int)I; t.J = (int)J; t.B = (int)B;
+    t.ltj = J <= 16 ? 4 : J <= 32 ? 5 : 6;
+    t.lti = 11 - t.ltj;
+    t.ti = (int)((I + (1 << t.lti) - 1) >> t.lti);
+    t.tj = (int)((J + (1 << t.ltj) - 1) >> t.ltj);
+    t.ri = si == 1 && sj0 != 1;
+    t.blocks = (I == 0 || J == 0) ? 0 : (int64_t)t.ti * t.tj * B;
+    return t;
+}
+
+// Up to two independent layout changes in one launch (the blocks of job 0,
+// then those of job 1), so that a convolution's input and weight transforms
+// cost one launch.  xcd: the grid is 8 * (ceil(blocks0 / 8) + ceil(blocks1 / 8))
+// and block ids are remapped so that each XCD (which takes every 8th id) runs
+// a contiguous eighth of each job's tiles: neighbouring tiles share the cache
+// lines at their edges, and then share them in one L2.  Otherwise a
+// grid-stride loop over the tiles.
+__global__ void __launch_bounds__(256) transpose_f32(TJob j0, TJob j1, int xcd) {
+    __shared__ float tile[128 * 17];   // [i - i0][j - j0], row pitch TJ + 1
+    const int t = threadIdx.x;
+    const int64_t total = j0.blocks + j1.blocks;
+    int64_t first = blockIdx.x, stride = gridDim.x;
+    if (xcd) {
+        const int64_t per0 = (j0.blocks + 7) >> 3, per1 = (j1.blocks + 7) >> 3;
+        const int64_t x = blockIdx.x & 7, q = blockIdx.x >> 3;
+        first = q < per0 ? (x * per0 + q < j0.blocks ? x * per0 + q : total)
+                         : (x * per1 + q - per0 < j1.blocks ? j0.blocks + x * per1 + q - per0
+                                                             : total);
+        stride = total;
+    }
+    for (int64_t blk = first; blk < total; blk += stride) {
+        const bool second = blk >= j0.blocks;
+        const TJob jb = second ? j1 : j0;
+        int64_t r = second ? blk - j0.blocks : blk;
+        const int per_b = jb.ti * jb.tj;
+        const int b = (int)(r / per_b);
+        r -= (int64_t)b * per_b;
+        const int TI = 1 << jb.lti, TJ = 1 << jb.ltj, pitch = TJ + 1;
+        const int i0 = (int)(r / jb.tj) << jb.lti, jt0 = (int)(r % jb.tj) << jb.ltj;
+        const float* src = jb.in + (int64_t)b * jb.sb;
+        // i-major lanes (consecutive i) for ri reads and for the writes;
+        // j-major lanes (consecutive j) for the other reads
+        const int im_i = t & (TI - 1), im_j = t >> jb.lti, im_step = 256 >> jb.lti;
+        const int jm_j = t & (TJ - 1), jm_i = t >> jb.ltj, jm_step = 256 >> jb.ltj;
+        float v[8];
+        if (!jb.ri) {
+            // this thread's j (and its offset) is fixed; i steps by jm_step
+            const int j = jt0 + jm_j;
+            const bool jok = j < jb.J;
+            const int jh = jok ? j / jb.jw : 0;
+            const float* q = src + (int64_t)(i0 + jm_i) * jb.si + (int64_t)jh * jb.sj1 +
+                             (int64_t)(j - jh * jb.jw) * jb.sj0;
+            const int64_t qstep = (int64_t)jm_step * jb.si;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int i = i0 + ty + 8 * k, j = j0 + tx;
-            float v = 0.f;
-            if (i < I && j < J) {
-                const int jh = j / jw;
-                v = src[(int64_t)i * si + (int64_t)jh * sj1 + (int64_t)(j - jh * jw) * sj0];
+            for (int k = 0; k < 8; ++k)
+                v[k] = jok && i0 + jm_i + k * jm_step < jb.I ? q[k * qstep] : 0.f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) tile[(jm_i + k * jm_step) * pitch + jm_j] = v[k];
+        } else {
+            // this thread's i is fixed (si == 1); j steps by im_step
+            const int i = i0 + im_i;
+            const bool iok = i < jb.I;
+            if (jb.jw == 1) {   // j -> offset j * sj1, no division
+                const float* q = src + i + (int64_t)(jt0 + im_j) * jb.sj1;
+                const int64_t qstep = (int64_t)im_step * jb.sj1;
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    v[k] = iok && jt0 + im_j + k * im_step < jb.J ? q[k * qstep] : 0.f;
+            } else {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const int j = jt0 + im_j + k * im_step;
+                    v[k] = 0.f;
+                    if (iok && j < jb.J) {
+                        const int jh = j / jb.jw;
+                        v[k] = src[i + (int64_t)jh * jb.sj1 + (int64_t)(j - jh * jb.jw) * jb.sj0];
+                    }
+                }
             }
-            tile[ty + 8 * k][tx] = v;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) tile[im_i * pitch + im_j + k * im_step] = v[k];
         }
         __syncthreads();
+        {
+            const int i = i0 + im_i;
+            float* o = jb.out + ((int64_t)b * jb.J + jt0 + im_j) * jb.I + i;
+            const int64_t ostep = (int64_t)im_step * jb.I;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int j = j0 + ty + 8 * k, i = i0 + tx;
-            if (i < I && j < J) out[((int64_t)b * J + j) * I + i] = tile[tx][ty + 8 * k];
+            for (int k = 0; k < 8; ++k)
+                if (i < jb.I && jt0 + im_j + k * im_step < jb.J)
+                    o[k * ostep] = tile[im_i * pitch + im_j + k * im_step];
         }
         __syncthreads();
     }
 }
 
+hipError_t launch_transposes(const TJob& a, const TJob& b, hipStream_t s) {
+    const int64_t total = a.blocks + b.blocks;
+    if (total == 0) return hipSuccess;
+    const int64_t xgrid = 8 * (((a.blocks + 7) >> 3) + ((b.blocks + 7) >> 3));
+    const bool xcd = xgrid <= ((int64_t)1 << 20);
+    const unsigned grid = (unsigned)(xcd ? xgrid : (int64_t)1 << 20);
+    hipLaunchKernelGGL(transpose_f32, dim3(grid), dim3(256), 0, s, a, b, xcd ? 1 : 0);
+    return capture_safe_last_error();
+}
+
 hipError_t launch_transpose(const float* in, int64_t sb, int64_t si, int64_t sj1, int64_t sj0,
                             int64_t jw, int64_t I, int64_t J, int64_t B, float* out,
                             hipStream_t s) {
-    if (I == 0 || J == 0 || B == 0) return hipSuccess;
-    dim3 grid((unsigned)((J + 31) / 32), (unsigned)((I + 31) / 32),
-              (unsigned)std::min<int64_t>(B, 65535));
-    hipLaunchKernelGGL(transpose_f32, grid, dim3(256), 0, s, in, sb, si, sj1, sj0, (int)jw,
-                       (int)I, (int)J, (int)B, out);
-    return capture_safe_last_error();
+    return launch_transposes(tjob(in, sb, si, sj1, sj0, jw, I, J, B, out), TJob{}, s);
 }
 
 // Element strides of a dense NCHW tensor.
@@ -939,26 +1032,27 @@ hipError_t launch_im2col(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, const 
 // Implicit-GEMM convolution: C[c_out, np] = Wt[c_out, kg] · im2col(xt)[kg, np]
 // with k = (r*kw + s)*c_in + ci, the im2col operand gathered by the kernel
 // from a channels-last input xt (the input itself when it already is one,
-// else a transposed copy in the workspace) and Wt the OHWI weights, which the
-// caller has already written at wsp + implicit_ws(d).xt.  Needs
-// implicit_geometry(d) and ws_bytes >= xt + wt.
+// else a transposed copy in the workspace) and Wt the OHWI weights, which
+// wjob writes to wsp + implicit_ws(d).xt in the same launch as the input's
+// transpose.  Needs implicit_geometry(d) and ws_bytes >= xt + wt.
 int run_conv_implicit(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, const float* input,
                       const int64_t in_strides[4], const float* bias, float* output, char* wsp,
-                      size_t ws_bytes, hipStream_t s) {
+                      size_t ws_bytes, const TJob& wjob, hipStream_t s) {
     const ImplicitWs iw = implicit_ws(d);
     const int64_t c = d->c_in, kg = c * d->kh * d->kw, hw = Ho * Wo, np = d->n * hw;
     const bool nhwc = in_strides[1] == 1 && in_strides[3] == c && in_strides[2] == d->w * c &&
                       (in_strides[0] & 3) == 0 && ((uintptr_t)input & 15u) == 0;
     const float* xt = input;
     int64_t img_stride = in_strides[0];
+    TJob xjob{};
     if (!nhwc) {
         float* buf = reinterpret_cast<float*>(wsp);
-        if (launch_transpose(input, in_strides[0], in_strides[1], in_strides[2], in_strides[3],
-                             d->w, c, d->h * d->w, d->n, buf, s) != hipSuccess)
-            return MT_ERR_HIP;
+        xjob = tjob(input, in_strides[0], in_strides[1], in_strides[2], in_strides[3], d->w, c,
+                    d->h * d->w, d->n, buf);
         xt = buf;
         img_stride = d->h * d->w * c;
     }
+    if (launch_transposes(xjob, wjob, s) != hipSuccess) return MT_ERR_HIP;
     GemmParams p{};
     p.A = reinterpret_cast<const float*>(wsp + iw.xt); p.a_mn = kg; p.a_k = 1; p.a_b = 0;
     p.B = xt;
@@ -1174,10 +1268,10 @@ int mt_conv2d_fwd_strided_f32(const mt_conv2d_desc* d, const float* input,
             return MT_ERR_WORKSPACE;
         char* wsp = static_cast<char*>(workspace);
         float* wt = reinterpret_cast<float*>(wsp + iw.xt);      // OIHW -> OHWI
-        if (launch_transpose(weight, kg, d->kh * d->kw, d->kw, 1, d->kw, d->c_in,
-                             d->kh * d->kw, d->c_out, wt, s) != hipSuccess)
-            return MT_ERR_HIP;
-        return run_conv_implicit(d, Ho, Wo, input, in_strides, bias, output, wsp, ws_bytes, s);
+        const TJob wjob = tjob(weight, kg, d->kh * d->kw, d->kw, 1, d->kw, d->c_in,
+                               d->kh * d->kw, d->c_out, wt);
+        return run_conv_implicit(d, Ho, Wo, input, in_strides, bias, output, wsp, ws_bytes, wjob,
+                                 s);
     }
     // other channel counts with kg % 4 == 0: the implicit GEMM over the NCHW
     // view, no copy of either operand and no column buffer
@@ -1272,10 +1366,12 @@ int mt_conv2d_bwd_weight_f32(const mt_conv2d_desc* d, const float* input, const 
         float* dyt = reinterpret_cast<float*>(wsp + xt_b);
         int64_t st[4];
         dense_strides(d, st);
-        if (launch_transpose(input, st[0], st[1], st[2], st[3], d->w, d->c_in, d->h * d->w, d->n,
-                             xt, s) != hipSuccess)
+        // x -> channels-last and dY [n][c_out][hw] -> dYt [c_out][n][hw], one launch
+        if (launch_transposes(tjob(input, st[0], st[1], st[2], st[3], d->w, d->c_in, d->h * d->w,
+                                   d->n, xt),
+                              tjob(grad_out, hw, 1, d->c_out * hw, 0, 1, hw, d->n, d->c_out, dyt),
+                              s) != hipSuccess)
             return MT_ERR_HIP;
-        if (transpose_dy(d, hw, grad_out, dyt, s) != hipSuccess) return MT_ERR_HIP;
         GemmParams p{};
         p.A = dyt; p.a_mn = np; p.a_k = 1; p.a_b = 0;
         p.B = xt;
@@ -1336,12 +1432,11 @@ int mt_conv2d_bwd_input_f32(const mt_conv2d_desc* d, const float* grad_out, cons
         char* wsp = static_cast<char*>(workspace);
         // Wt[ci][r'][s'][co] = W[co][ci][kh-1-r'][kw-1-s'] (negative tap strides)
         const int64_t khw = d->kh * d->kw;
-        if (launch_transpose(weight + (khw - 1), khw, d->c_in * khw, -d->kw, -1, d->kw, d->c_out,
-                             khw, d->c_in, reinterpret_cast<float*>(wsp + iw.xt), s) != hipSuccess)
-            return MT_ERR_HIP;
+        const TJob wjob = tjob(weight + (khw - 1), khw, d->c_in * khw, -d->kw, -1, d->kw,
+                               d->c_out, khw, d->c_in, reinterpret_cast<float*>(wsp + iw.xt));
         const int64_t st[4] = {d->c_out * hw, hw, Wo, 1};   // dense dY
         return run_conv_implicit(&t, d->h, d->w, grad_out, st, nullptr, grad_input, wsp, ws_bytes,
-                                 s);
+                                 wjob, s);
     }
     if (dx_as_forward(d, Ho, Wo, &t)) {
         // Other c_out: the implicit GEMM of dY (NCHW, read in place) with the
