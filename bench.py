@@ -140,11 +140,13 @@ def time_events(fn, iters: int, warmup: int) -> float:
     return start.elapsed_time(stop) / iters
 
 
-def time_graph(fn, calls: int = 20, replays: int = 10) -> list:
+def time_graph(fn, calls: int = 20, replays: int = 10, preroll_ms: float = PREROLL_MS / 2) -> list:
     """Device ms per call of fn for each replay: `calls` calls captured into
-    one HIP graph, replayed `replays` times with an event around each replay.
-    Removes the Python/ctypes launch overhead, which exceeds the kernel time
-    of the small configs."""
+    one HIP graph, replayed `replays` times with an event around each replay,
+    after about preroll_ms of untimed replays (so that every workload is timed
+    at the clocks of sustained work, not on the ramp out of the previous
+    one's host-side set-up).  Removes the Python/ctypes launch overhead, which
+    exceeds the kernel time of the small configs."""
     import torch
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -157,7 +159,14 @@ def time_graph(fn, calls: int = 20, replays: int = 10) -> list:
     with torch.cuda.graph(graph):
         for _ in range(calls):
             fn()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
     for _ in range(3):
+        graph.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    per_replay = max(t0.elapsed_time(t1) / 3, 1e-3)
+    for _ in range(min(int(preroll_ms / per_replay), 5000)):
         graph.replay()
     torch.cuda.synchronize()
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(replays + 1)]
