@@ -140,6 +140,23 @@ constexpr CfgCost kDlCost[kNumDlCfg] = {    // direct-to-LDS kernel, vector layo
     {DlCfg<4>::BM, DlCfg<4>::BN, 0.98, 1},
     {DlCfg<5>::BM, DlCfg<5>::BN, 0.72, 8},
     {DlCfg<6>::BM, DlCfg<6>::BN, 0.90, 3}};
+// The same kernels with the convolution weight gradient's gathered B operand
+// (L_IMW): its 16-byte gathers cost per chunk whatever the tile's height, so
+// the 256-row tile of configuration 3 amortises them over twice the MFMA work
+// of the 128-row ones.  Forced sweeps of every configuration and split on
+// five ResNet-like dW shapes (c_out 64-512, one MI355X): configuration 3 at
+// its best split is 3-4 % faster than the plain table's picks where M >= 256
+// (5a layer: split 14, 86.9 vs 89.4 us at configuration 6 split 7;
+// 512 x 4608 x 1568: 99.7 vs 103.7 us at configuration 1), and the 64-row
+// shapes keep configuration 5.  Only configurations 3 and 6 differ.
+constexpr CfgCost kDlCostImw[kNumDlCfg] = {
+    {DlCfg<0>::BM, DlCfg<0>::BN, 0.90, 1},
+    {DlCfg<1>::BM, DlCfg<1>::BN, 0.86, 4},
+    {DlCfg<2>::BM, DlCfg<2>::BN, 0.68, 8},
+    {DlCfg<3>::BM, DlCfg<3>::BN, 0.93, 3},
+    {DlCfg<4>::BM, DlCfg<4>::BN, 0.98, 1},
+    {DlCfg<5>::BM, DlCfg<5>::BN, 0.72, 8},
+    {DlCfg<6>::BM, DlCfg<6>::BN, 0.86, 3}};
 // Wave-split kernel (configurations of KswCfg): efficiencies from
 // graph-replay timings of every configuration at 1, 2 and 4 K splits on the
 // benchmark's small GEMMs and four neighbouring shapes (one MI355X).  It is
@@ -209,11 +226,12 @@ double plan_cycles(const CostModel& cm, const CfgCost& cc, const Plan& pl, int64
 }
 
 // wide: the prefetching direct-to-LDS configurations (is_dlp_cfg) may be
-// chosen (see wide_ok in launch_gemm); ksw: the wave-split kernel may be.
+// chosen (see wide_ok in launch_gemm); ksw: the wave-split kernel may be;
+// imw: B is the weight-gradient operand (priced by kDlCostImw).
 Plan make_plan_uncached(int64_t M, int64_t N, int64_t K, int64_t batch, int cus,
-                        bool allow_split, bool dl, bool wide, bool ksw) {
+                        bool allow_split, bool dl, bool wide, bool ksw, bool imw) {
     static const CostModel cm;
-    const CfgCost* cfgs = dl ? kDlCost : kRsCost;
+    const CfgCost* cfgs = dl ? (imw ? kDlCostImw : kDlCost) : kRsCost;
     const int ncfg = dl ? kNumDlCfg : kNumCfg;
     Plan best;
     best.dl = dl;
@@ -258,11 +276,11 @@ Plan make_plan_uncached(int64_t M, int64_t N, int64_t K, int64_t batch, int cus,
 // for the same few shapes again and again (workspace query, then launch), so
 // each thread keeps its last few plans.
 Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool allow_split,
-               bool dl, bool wide, bool ksw) {
+               bool dl, bool wide, bool ksw, bool imw = false) {
     struct Entry {
         int64_t M = -1, N = -1, K = -1, batch = -1;
         int cus = 0;
-        bool allow_split = false, dl = false, wide = false, ksw = false;
+        bool allow_split = false, dl = false, wide = false, ksw = false, imw = false;
         Plan plan;
     };
     constexpr int kEntries = 8;
@@ -270,12 +288,13 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool all
     thread_local int next = 0;
     for (const Entry& e : cache)
         if (e.M == M && e.N == N && e.K == K && e.batch == batch && e.cus == cus &&
-            e.allow_split == allow_split && e.dl == dl && e.wide == wide && e.ksw == ksw)
+            e.allow_split == allow_split && e.dl == dl && e.wide == wide && e.ksw == ksw &&
+            e.imw == imw)
             return e.plan;
     Entry& e = cache[next];
     next = (next + 1) % kEntries;
-    e = Entry{M, N, K, batch, cus, allow_split, dl, wide, ksw,
-              make_plan_uncached(M, N, K, batch, cus, allow_split, dl, wide, ksw)};
+    e = Entry{M, N, K, batch, cus, allow_split, dl, wide, ksw, imw,
+              make_plan_uncached(M, N, K, batch, cus, allow_split, dl, wide, ksw, imw)};
     return e.plan;
 }
 
@@ -347,12 +366,15 @@ GemmLaunchFn conv_launcher(int cfg, bool nchw) {
 
 // Workspace that covers the plan of either kernel family (for sizes queried
 // before the operand pointers, and hence the layouts, are known).
-size_t plan_ws(int64_t M, int64_t N, int64_t K, int64_t batch, int cus) {
+size_t plan_ws(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool imw = false) {
     size_t ws = 0;
     for (bool dl : {false, true})
         for (bool wide : {false, true})
             for (bool ksw : {false, true})
                 ws = std::max(ws, make_plan(M, N, K, batch, cus, true, dl, wide, ksw).ws_bytes);
+    if (imw)   // the weight-gradient operand's own table
+        for (bool wide : {false, true})
+            ws = std::max(ws, make_plan(M, N, K, batch, cus, true, true, wide, false, true).ws_bytes);
     Plan forced;
     if (forced_plan(M, N, K, batch, true, true, true, &forced)) ws = std::max(ws, forced.ws_bytes);
     return ws;
@@ -499,9 +521,11 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
         // the wave-split kernel takes every operand form but the implicit
         // convolution operands and the fused row sums
         const bool ksw_ok = !implicit && p.rowsum == nullptr;
-        plan = make_plan(M, N, K, batch, device_cu_count(), true, dl, wide_ok, ksw_ok);
+        plan = make_plan(M, N, K, batch, device_cu_count(), true, dl, wide_ok, ksw_ok,
+                         lb == L_IMW);
         if (plan.splits > 1 && (workspace == nullptr || ws_bytes < plan.ws_bytes))
-            plan = make_plan(M, N, K, batch, device_cu_count(), false, dl, wide_ok, ksw_ok);
+            plan = make_plan(M, N, K, batch, device_cu_count(), false, dl, wide_ok, ksw_ok,
+                             lb == L_IMW);
     }
     // Row sums of A are fused only into a direct-to-LDS launch of two
     // mn-contiguous operands without split-K (the caller sees p.rowsum cleared
@@ -1328,7 +1352,7 @@ size_t mt_conv2d_bwd_workspace_f32(const mt_conv2d_desc* d) {
     if (implicit_dw(d, np))
         need = std::max(need, align_up((size_t)d->n * d->c_in * d->h * d->w * sizeof(float), 256) +
                                   align_up((size_t)d->c_out * np * sizeof(float), 256) +
-                                  plan_ws(d->c_out, kg, np, 1, cus));
+                                  plan_ws(d->c_out, kg, np, 1, cus, true));
     mt_conv2d_desc t;
     if (dx_as_forward(d, Ho, Wo, &t)) {   // implicit dX (usually smaller than the above)
         const size_t g = plan_ws(d->c_in, d->n * d->h * d->w, d->c_out * d->kh * d->kw, 1, cus);
