@@ -869,18 +869,42 @@ conv_bias_grad_f32(const float* dy, float* db, int N, int C, int64_t HW, float b
     const int64_t per_img = vec ? HW / 4 : HW;       // items per image
     const int64_t total = (int64_t)N * per_img;
     float s[4] = {0.f, 0.f, 0.f, 0.f};               // 4 independent loads in flight
-    for (int64_t i0 = t; i0 < total; i0 += 4 * 256) {
+    if (total < ((int64_t)1 << 31)) {
+        // 32-bit index arithmetic; the four loads are issued before any is used
+        const int per = (int)per_img, tot = (int)total;
+        for (int i0 = t; i0 < tot; i0 += 4 * 256) {
+            float v[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int64_t i = i0 + u * 256;
-            if (i >= total) break;
-            const int64_t img = i / per_img, j = i - img * per_img;
-            const float* p = dy + ((int64_t)img * C + c) * HW;
-            if (vec) {
-                const f32x4 v = *reinterpret_cast<const f32x4*>(p + 4 * j);
-                s[u] += (v[0] + v[1]) + (v[2] + v[3]);
-            } else {
-                s[u] += p[j];
+            for (int u = 0; u < 4; ++u) {
+                const int i = i0 + u * 256;
+                const int ii = i < tot ? i : 0;
+                const int img = ii / per, j = ii - img * per;
+                const float* p = dy + ((int64_t)img * C + c) * HW;
+                if (vec) {
+                    const f32x4 x = *reinterpret_cast<const f32x4*>(p + 4 * j);
+                    v[u] = (x[0] + x[1]) + (x[2] + x[3]);
+                } else {
+                    v[u] = p[j];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (i0 + u * 256 < tot) s[u] += v[u];
+        }
+    } else {
+        for (int64_t i0 = t; i0 < total; i0 += 4 * 256) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int64_t i = i0 + u * 256;
+                if (i >= total) break;
+                const int64_t img = i / per_img, j = i - img * per_img;
+                const float* p = dy + ((int64_t)img * C + c) * HW;
+                if (vec) {
+                    const f32x4 v = *reinterpret_cast<const f32x4*>(p + 4 * j);
+                    s[u] += (v[0] + v[1]) + (v[2] + v[3]);
+                } else {
+                    s[u] += p[j];
+                }
             }
         }
     }
