@@ -245,6 +245,38 @@ def test_conv_implicit_shapes(dev, n, c, h, wd, co, kh, kw, stride, pad):
     assert_close(out, want, c * kh * kw, amax(x), amax(w), "implicit conv", extra=1e-5)
 
 
+# The layout launches ahead of the channels-last kernels move 2048-element
+# tiles shaped to the job (32x64, 64x32 when the inner extent is <= 32, 128x16
+# when <= 16), reading along the inner dimension or, for the dY copy of the
+# weight gradient, along the outer one; each geometry below puts one of the
+# jobs on a tile shape the benchmark layer does not use, with partial tiles:
+# 4x4 and 5x5 images (pixel extent 16 / 25), 40 images (dY copy extent 40),
+# 3x3 and 1x1 filters (tap extent 9 / 1), 48 channels (ragged channel tiles).
+@pytest.mark.parametrize("n,c,h,wd,co,kh,kw,pad", [
+    (2, 16, 4, 4, 16, 3, 3, 1),
+    (3, 32, 5, 5, 16, 3, 3, 1),
+    (40, 16, 5, 5, 48, 3, 3, 1),
+    (5, 48, 6, 7, 32, 1, 1, 0),
+    (2, 48, 9, 9, 80, 3, 3, 1),
+])
+def test_conv_layout_tile_shapes(dev, n, c, h, wd, co, kh, kw, pad):
+    x = oracle.normal((n, c, h, wd), 500 + n)
+    w = oracle.normal((co, c, kh, kw), 501 + co)
+    b = oracle.normal((co,), 502)
+    X, W = g(x, dev), g(w, dev)
+    out = sync_np(mt.conv2d(X, W, g(b, dev), 1, pad))
+    assert "b=im2col " in mt.last_config() + " ", mt.last_config()
+    assert_close(out, oracle.conv2d(x, w, b, 1, pad), c * kh * kw, amax(x), amax(w),
+                 "forward", extra=1e-5)
+    ho, wo = oracle.conv_out(h, pad, kh, 1), oracle.conv_out(wd, pad, kw, 1)
+    dy = oracle.normal((n, co, ho, wo), 503)
+    dx, dw, db = mt.conv2d_backward(X, W, g(dy, dev), 1, pad)
+    wdx, wdw, wdb = oracle.conv2d_backward(x, w, dy, 1, pad)
+    assert_close(sync_np(dx), wdx, co * kh * kw, amax(dy), amax(w), "dX")
+    assert_close(sync_np(dw), wdw, n * ho * wo, amax(dy), amax(x), "dW")
+    assert_close(sync_np(db), wdb, n * ho * wo, amax(dy), 1.0, "db")
+
+
 # The implicit GEMM over an NCHW view (K order (ci, r, s), the OIHW weights
 # read in place): any c_in with c_in*kh*kw % 4 == 0, including K ranges that
 # end in a partial chunk, fewer K than one chunk, rectangular kernels, strides
