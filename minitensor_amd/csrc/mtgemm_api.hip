@@ -1120,9 +1120,14 @@ int run_conv_implicit(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, const flo
 // The implicit-GEMM convolution over an NCHW view (L_IMR) reads the OIHW
 // weights as its A operand in 16-byte rows: kg % 4 == 0 (weights that are not
 // 16-byte aligned are first copied to the workspace, nchw_weight_ws bytes).
+// Its window test adds a tap to the window origin in 32-bit arithmetic, so
+// the padded extents stay below 2^30 (a tap never exceeds them when an
+// output exists).
 bool nchw_implicit(const mt_conv2d_desc* d) {
     const int64_t kg = d->c_in * d->kh * d->kw;
-    return kg > 0 && (kg & 3) == 0 && d->h * d->w < kMaxDim;
+    constexpr int64_t kWin = (int64_t)1 << 30;
+    return kg > 0 && (kg & 3) == 0 && d->h * d->w < kMaxDim && d->h + 2 * d->pad < kWin &&
+           d->w + 2 * d->pad < kWin;
 }
 size_t nchw_weight_ws(const mt_conv2d_desc* d) {
     return align_up((size_t)d->c_out * d->c_in * d->kh * d->kw * sizeof(float), 256);
@@ -1486,7 +1491,7 @@ int mt_conv2d_bwd_input_f32(const mt_conv2d_desc* d, const float* grad_out, cons
         return run_conv_implicit(&t, d->h, d->w, grad_out, st, nullptr, grad_input, wsp, ws_bytes,
                                  wjob, s);
     }
-    if (dx_as_forward(d, Ho, Wo, &t)) {
+    if (dx_as_forward(d, Ho, Wo, &t) && nchw_implicit(&t)) {
         // Other c_out: the implicit GEMM of dY (NCHW, read in place) with the
         // flipped, transposed weights in OIHW order: no dcol buffer, no copy of dY.
         int64_t th, tw;
