@@ -193,6 +193,18 @@ int mt_conv2d_bwd_input_f32(const mt_conv2d_desc* d, const float* grad_out, cons
                             float* grad_input, void* workspace, size_t ws_bytes, void* stream);
 int mt_conv2d_bwd_bias_f32(const mt_conv2d_desc* d, const float* grad_out, float* grad_bias,
                            float beta, void* stream);
+/* dW (+ beta_w·dW) and db (+ beta_b·db) in one call; grad_bias may be NULL
+ * (then as mt_conv2d_bwd_weight_f32).  When the implicit weight path runs
+ * with split-K, the reduction launch of its GEMM also sums db (one workgroup
+ * per output channel, fixed order), so db needs no launch of its own;
+ * otherwise the two run as above.  Same workspace as the weight gradient.
+ * Replaces conv2d_backward_weight_gpu followed by conv2d_backward_bias_gpu
+ * (reference src/gpu_ops.cpp:2623-2713 and 2483-2497; called in turn by
+ * Conv2DBackward, include/Autograd.hpp:471-505). */
+int mt_conv2d_bwd_weight_bias_f32(const mt_conv2d_desc* d, const float* input,
+                                  const float* grad_out, float* grad_weight, float beta_w,
+                                  float* grad_bias, float beta_b, void* workspace,
+                                  size_t ws_bytes, void* stream);
 size_t mt_conv2d_bwd_workspace_f32(const mt_conv2d_desc* d);
 
 /* ---- support kernels the Tensor layer needs around the GEMMs --------------- */

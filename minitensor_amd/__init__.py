@@ -100,6 +100,11 @@ _SIGS = {
                                                ctypes.c_void_p]),
     "mt_conv2d_bwd_bias_f32": (ctypes.c_int, [_P(Conv2dDesc), ctypes.c_void_p, ctypes.c_void_p,
                                               ctypes.c_float, ctypes.c_void_p]),
+    "mt_conv2d_bwd_weight_bias_f32": (ctypes.c_int, [_P(Conv2dDesc), ctypes.c_void_p,
+                                                     ctypes.c_void_p, ctypes.c_void_p,
+                                                     ctypes.c_float, ctypes.c_void_p,
+                                                     ctypes.c_float, ctypes.c_void_p,
+                                                     ctypes.c_size_t, ctypes.c_void_p]),
     "mt_conv2d_bwd_workspace_f32": (ctypes.c_size_t, [_P(Conv2dDesc)]),
     "mt_fill_f32": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64, ctypes.c_float,
                                    ctypes.c_void_p]),
@@ -383,16 +388,19 @@ def conv2d_backward(x: torch.Tensor, w: torch.Tensor, dy: torch.Tensor, stride: 
         dx = torch.empty_like(x)
         _check(lib().mt_conv2d_bwd_input_f32(ctypes.byref(d), dy.data_ptr(), w.data_ptr(),
                                              dx.data_ptr(), wp, wn, s), "mt_conv2d_bwd_input_f32")
+    if need_db:
+        db = torch.empty((co,), dtype=torch.float32, device=x.device)
     if need_dw:
         if dw is None:
             dw = torch.empty_like(w)
         elif tuple(dw.shape) != tuple(w.shape) or not dw.is_contiguous():
             raise ValueError("conv2d_backward: dw must be a dense tensor shaped like w")
-        _check(lib().mt_conv2d_bwd_weight_f32(ctypes.byref(d), x.data_ptr(), dy.data_ptr(),
-                                              dw.data_ptr(), float(beta_w), wp, wn, s),
-               "mt_conv2d_bwd_weight_f32")
-    if need_db:
-        db = torch.empty((co,), dtype=torch.float32, device=x.device)
+        # dW and db in one call (db can ride on the dW GEMM's reduction launch)
+        _check(lib().mt_conv2d_bwd_weight_bias_f32(ctypes.byref(d), x.data_ptr(), dy.data_ptr(),
+                                                   dw.data_ptr(), float(beta_w), _ptr(db), 0.0,
+                                                   wp, wn, s),
+               "mt_conv2d_bwd_weight_bias_f32")
+    elif need_db:
         _check(lib().mt_conv2d_bwd_bias_f32(ctypes.byref(d), dy.data_ptr(), db.data_ptr(), 0.0, s),
                "mt_conv2d_bwd_bias_f32")
     return dx, dw, db

@@ -82,6 +82,10 @@ void conv2d_backward_weight(const Tensor<T>& grad_output, const Tensor<T>& input
                             Tensor<T>& grad_weight, size_t stride, size_t padding);
 template <typename T>
 void conv2d_backward_bias(const Tensor<T>& grad_output, Tensor<T>& grad_bias);
+template <typename T>
+void conv2d_backward_weight_bias(const Tensor<T>& grad_output, const Tensor<T>& input,
+                                 Tensor<T>& grad_weight, Tensor<T>& grad_bias, size_t stride,
+                                 size_t padding);
 
 template <typename T>
 struct AddBackward : AutogradNode<T> {
@@ -155,12 +159,17 @@ struct Conv2DBackward : AutogradNode<T> {
             conv2d_backward_input(go, weight.contiguous(), gi, stride, padding);
             input.accumulate_grad(gi);
         }
-        if (weight.requires_grad()) {
+        const bool want_b = bias.defined() && !bias.empty() && bias.requires_grad();
+        if (weight.requires_grad() && want_b) {   // one library call for both
+            Tensor<T> gw(weight.shape(), weight.device()), gb(bias.shape(), bias.device());
+            conv2d_backward_weight_bias(go, input.contiguous(), gw, gb, stride, padding);
+            weight.accumulate_grad(gw);
+            bias.accumulate_grad(gb);
+        } else if (weight.requires_grad()) {
             Tensor<T> gw(weight.shape(), weight.device());
             conv2d_backward_weight(go, input.contiguous(), gw, stride, padding);
             weight.accumulate_grad(gw);
-        }
-        if (bias.defined() && !bias.empty() && bias.requires_grad()) {
+        } else if (want_b) {
             Tensor<T> gb(bias.shape(), bias.device());
             conv2d_backward_bias(go, gb);
             bias.accumulate_grad(gb);

@@ -420,6 +420,25 @@ void conv2d_backward_weight_gpu(const Tensor<T>& go, const Tensor<T>& in, Tensor
     if (!gw.is_contiguous()) copy_gpu_strided(o, gw);
 }
 
+// dW and db in one library call (mt_conv2d_bwd_weight_bias_f32): db can ride
+// on the reduction launch of the dW GEMM.
+template <typename T>
+void conv2d_backward_weight_bias_gpu(const Tensor<T>& go, const Tensor<T>& in, Tensor<T>& gw,
+                                     Tensor<T>& gb, size_t stride, size_t padding) {
+    mt_detail::require_float_gpu<T>();
+    const Tensor<T> g = go.contiguous(), x = in.contiguous();
+    Tensor<T> ow = mt_detail::dense_out(gw, 0.f), ob = mt_detail::dense_out(gb, 0.f);
+    const mt_conv2d_desc d = mt_detail::conv_desc(x.shape(), gw.shape(), stride, padding);
+    mt_detail::Workspace ws(mt_conv2d_bwd_workspace_f32(&d), gw.device());
+    mt_check_status(mt_conv2d_bwd_weight_bias_f32(&d, x.data() + x.offset(), g.data() + g.offset(),
+                                                  ow.data() + ow.offset(), 0.f,
+                                                  ob.data() + ob.offset(), 0.f, ws.get(),
+                                                  ws.size(), active_stream()),
+                    "conv2d backward weight and bias");
+    if (!gw.is_contiguous()) copy_gpu_strided(ow, gw);
+    if (!gb.is_contiguous()) copy_gpu_strided(ob, gb);
+}
+
 template <typename T>
 void conv2d_backward_bias_gpu(const Tensor<T>& go, Tensor<T>& gb, float beta = 0.f) {
     mt_detail::require_float_gpu<T>();
@@ -687,6 +706,19 @@ template <typename T>
 void conv2d_backward_bias(const Tensor<T>& go, Tensor<T>& gb) {
     if (gb.device().is_gpu()) conv2d_backward_bias_gpu(go, gb);
     else conv2d_backward_bias_cpu(go, gb);
+}
+
+// Both parameter gradients: one library call on the GPU, the two CPU paths
+// otherwise.
+template <typename T>
+void conv2d_backward_weight_bias(const Tensor<T>& go, const Tensor<T>& in, Tensor<T>& gw,
+                                 Tensor<T>& gb, size_t stride, size_t padding) {
+    if (gw.device().is_gpu() && gb.device().is_gpu()) {
+        conv2d_backward_weight_bias_gpu(go, in, gw, gb, stride, padding);
+    } else {
+        conv2d_backward_weight(go, in, gw, stride, padding);
+        conv2d_backward_bias(go, gb);
+    }
 }
 
 // ---- Linear ---------------------------------------------------------------

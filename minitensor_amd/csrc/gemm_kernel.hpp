@@ -99,6 +99,12 @@ struct GemmParams {
     // rowsum[m*rowsum_stride] = rowsum_beta*rowsum[...] + sum_k A(m, k).  In
     // dW = dYᵀ·X this is the bias gradient db = sum over the batch of dY.
     float* rowsum; int64_t rowsum_stride; float rowsum_beta;
+    // Optional channel sums (the convolution bias gradient db from dY [n][M][hw]),
+    // computed by the vector split-K reduction, one workgroup per row m:
+    // csum[m] = csum_beta*csum[m] + sum over img < csum_n, q < csum_hw of
+    // csum_src[(img*M + m)*csum_hw + q].  The launcher clears csum when the
+    // plan has no such reduction (the caller then sums separately).
+    const float* csum_src; float* csum; int csum_n; int64_t csum_hw; float csum_beta;
     int tiles_m, tiles_n, group_m;
 };
 

@@ -460,17 +460,62 @@ __global__ void __launch_bounds__(256) splitk_reduce_f32(GemmParams p) {
     }
 }
 
+// csum[m] of GemmParams (the convolution bias gradient), by one workgroup:
+// each thread sums a fixed set of positions with four independent
+// accumulators (16-byte loads when csum_hw % 4 == 0 and the source is
+// aligned), then a fixed-order tree: deterministic.
+__device__ __forceinline__ void channel_sum(const GemmParams& p, int m, float* red) {
+    const int t = threadIdx.x;
+    const bool vec = (p.csum_hw & 3) == 0 && ((uintptr_t)p.csum_src & 15u) == 0;
+    // csum_n * csum_hw is a GEMM extent (< 2^31): 32-bit index arithmetic
+    const int per_img = (int)(vec ? p.csum_hw / 4 : p.csum_hw);
+    const int total = p.csum_n * per_img;
+    float s[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int i0 = t; i0 < total; i0 += 4 * 256) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = i0 + u * 256 < total ? i0 + u * 256 : 0;
+            const int img = i / per_img, j = i - img * per_img;
+            const float* q = p.csum_src + ((int64_t)img * p.M + m) * p.csum_hw;
+            if (vec) {
+                const f32x4 x = *reinterpret_cast<const f32x4*>(q + 4 * j);
+                v[u] = (x[0] + x[1]) + (x[2] + x[3]);
+            } else {
+                v[u] = q[j];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (i0 + u * 256 < total) s[u] += v[u];
+    }
+    red[t] = (s[0] + s[1]) + (s[2] + s[3]);
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (t < w) red[t] += red[t + w];
+        __syncthreads();
+    }
+    if (t == 0) p.csum[m] = (p.csum_beta != 0.f ? p.csum_beta * p.csum[m] : 0.f) + red[0];
+    __syncthreads();
+}
+
 // Vector form (ws_vec: N % 4 == 0, 16-byte partials): blockIdx.y walks output
 // rows (batch-major), threads walk 4-column groups; the group is stored as one
 // 16-byte vector when C allows (c_vec), else element by element through
 // col(n).  Same per-element summation order as the scalar form.
+// CSUM: also the channel sums of GemmParams::csum (a separate instantiation,
+// so that the plain reduction carries neither its code nor its LDS).
+template <bool CSUM>
 __global__ void __launch_bounds__(256) splitk_reduce_vec_f32(GemmParams p) {
+    __shared__ float red[CSUM ? 256 : 1];
     const int64_t MN = (int64_t)p.M * p.N;
     const int64_t rows = (int64_t)p.M * p.batch;
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
     for (int64_t row = blockIdx.y; row < rows; row += gridDim.y) {
         const int bz = (int)(row / p.M);
         const int m = (int)(row - (int64_t)bz * p.M);
+        if constexpr (CSUM)
+            if (blockIdx.x == 0) channel_sum(p, m, red);
         const float brow = p.bias_axis == 1 ? p.bias[(int64_t)m * p.bias_stride] : 0.f;
         const float* src = p.ws + (int64_t)bz * MN + (int64_t)m * p.N;
         float* crow = p.C + (int64_t)bz * p.c_b + (int64_t)m * p.c_m;
@@ -539,6 +584,8 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
     p.group_m = 4;
     p.ws = plan.splits > 1 ? static_cast<float*>(workspace) : nullptr;
     p.ws_vec = p.ws != nullptr && ((uintptr_t)p.ws & 15u) == 0 && (N & 3) == 0;
+    // Channel sums ride on the vector reduction only (one row per workgroup row)
+    if (!p.ws_vec || batch != 1) p.csum = nullptr;
 
     const int64_t nblocks = (int64_t)plan.tiles_m * plan.tiles_n * plan.splits * batch;
     if (nblocks >= ((int64_t)1 << 31)) return MT_ERR_UNSUPPORTED;
@@ -560,7 +607,10 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
         if (p.ws_vec) {
             const dim3 grid((unsigned)std::min<int64_t>((N / 4 + 255) / 256, 64),
                             (unsigned)std::min<int64_t>(M * batch, 65535));
-            hipLaunchKernelGGL(splitk_reduce_vec_f32, grid, dim3(256), 0, stream, p);
+            if (p.csum)
+                hipLaunchKernelGGL(splitk_reduce_vec_f32<true>, grid, dim3(256), 0, stream, p);
+            else
+                hipLaunchKernelGGL(splitk_reduce_vec_f32<false>, grid, dim3(256), 0, stream, p);
         } else {
             const int64_t total = M * N * batch;
             const int64_t blocks = std::min<int64_t>((total + 255) / 256, 65536);
@@ -1395,15 +1445,22 @@ size_t mt_conv2d_bwd_workspace_f32(const mt_conv2d_desc* d) {
     return need;
 }
 
-int mt_conv2d_bwd_weight_f32(const mt_conv2d_desc* d, const float* input, const float* grad_out,
-                             float* grad_weight, float beta, void* workspace, size_t ws_bytes,
-                             void* stream) {
+}  // extern "C"
+
+namespace {
+
+// dW (+ beta·dW).  With grad_bias, the implicit path also hands db
+// (+ beta_b·db) to the split-K reduction of its GEMM when the plan has one
+// (GemmParams::csum); *db_done reports whether it did.
+int conv_bwd_weight(const mt_conv2d_desc* d, const float* input, const float* grad_out,
+                    float* grad_weight, float beta, float* grad_bias, float beta_b,
+                    void* workspace, size_t ws_bytes, hipStream_t s, bool* db_done) {
+    *db_done = false;
     int64_t Ho, Wo;
     if (!conv_dims(d, &Ho, &Wo)) return MT_ERR_INVALID;
     const int64_t kg = d->c_in * d->kh * d->kw, np = d->n * Ho * Wo, hw = Ho * Wo;
     if (kg == 0 || d->c_out == 0) return MT_OK;
     if (!grad_weight) return MT_ERR_INVALID;
-    hipStream_t s = static_cast<hipStream_t>(stream);
     const size_t col_b = align_up((size_t)kg * np * sizeof(float), 256);
     const size_t dyt_b = align_up((size_t)d->c_out * np * sizeof(float), 256);
     if (np > 0 && (!input || !grad_out)) return MT_ERR_INVALID;
@@ -1438,7 +1495,14 @@ int mt_conv2d_bwd_weight_f32(const mt_conv2d_desc* d, const float* input, const 
         g.c = (int)d->c_in; g.h = (int)d->h; g.w = (int)d->w;
         g.kh = (int)d->kh; g.kw = (int)d->kw; g.stride = (int)d->stride; g.pad = (int)d->pad;
         g.ho = (int)Ho; g.wo = (int)Wo;
-        return launch_gemm(p, true, L_KV, L_IMW, wsp + xt_b + dyt_b, ws_bytes - xt_b - dyt_b, s);
+        if (grad_bias) {
+            p.csum_src = grad_out; p.csum = grad_bias; p.csum_n = (int)d->n;
+            p.csum_hw = hw; p.csum_beta = beta_b;
+        }
+        const int rc =
+            launch_gemm(p, true, L_KV, L_IMW, wsp + xt_b + dyt_b, ws_bytes - xt_b - dyt_b, s);
+        *db_done = rc == MT_OK && p.csum != nullptr;
+        return rc;
     }
     if (np > 0 && (!workspace || ws_bytes < col_b + dyt_b)) return MT_ERR_WORKSPACE;
     float* col = static_cast<float*>(workspace);
@@ -1457,6 +1521,33 @@ int mt_conv2d_bwd_weight_f32(const mt_conv2d_desc* d, const float* input, const 
     char* gws = static_cast<char*>(workspace) + col_b + dyt_b;
     const size_t gws_b = ws_bytes > col_b + dyt_b ? ws_bytes - col_b - dyt_b : 0;
     return run_gemm(&A, &B, &C, 0, 0, &ep, np > 0 ? gws : nullptr, np > 0 ? gws_b : 0, s);
+}
+
+}  // namespace
+
+extern "C" {
+
+int mt_conv2d_bwd_weight_f32(const mt_conv2d_desc* d, const float* input, const float* grad_out,
+                             float* grad_weight, float beta, void* workspace, size_t ws_bytes,
+                             void* stream) {
+    bool db_done;
+    return conv_bwd_weight(d, input, grad_out, grad_weight, beta, nullptr, 0.f, workspace,
+                           ws_bytes, static_cast<hipStream_t>(stream), &db_done);
+}
+
+int mt_conv2d_bwd_weight_bias_f32(const mt_conv2d_desc* d, const float* input,
+                                  const float* grad_out, float* grad_weight, float beta_w,
+                                  float* grad_bias, float beta_b, void* workspace,
+                                  size_t ws_bytes, void* stream) {
+    int64_t Ho, Wo;
+    if (!conv_dims(d, &Ho, &Wo)) return MT_ERR_INVALID;
+    if (grad_bias && d->n * Ho * Wo > 0 && !grad_out) return MT_ERR_INVALID;
+    bool db_done = false;
+    const int rc = conv_bwd_weight(d, input, grad_out, grad_weight, beta_w, grad_bias, beta_b,
+                                   workspace, ws_bytes, static_cast<hipStream_t>(stream),
+                                   &db_done);
+    if (rc != MT_OK || !grad_bias || db_done) return rc;
+    return mt_conv2d_bwd_bias_f32(d, grad_out, grad_bias, beta_b, stream);
 }
 
 int mt_conv2d_bwd_input_f32(const mt_conv2d_desc* d, const float* grad_out, const float* weight,

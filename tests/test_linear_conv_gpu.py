@@ -1,5 +1,6 @@
 """GPU parity of the Linear GEMMs (fused bias, backward, bias gradient) and of
 the conv-as-GEMM path against the CPU oracle and the reference's own vectors."""
+import ctypes
 from pathlib import Path
 
 import numpy as np
@@ -183,6 +184,58 @@ def test_conv_backward_shapes(dev, n, c, h, wd, co, kh, kw, stride, pad):
     assert_close(dx, wdx, co * kh * kw, amax(dy), amax(w), "conv dX")
     assert_close(dw, wdw, n * ho * wo, amax(dy), amax(x), "conv dW")
     assert_close(db, wdb, n * ho * wo, amax(dy), 1.0, "conv db")
+
+
+@pytest.mark.parametrize("n,c,h,wd,co,stride,pad", [
+    (4, 16, 10, 10, 24, 1, 1),    # implicit weight path (split-K: db in its reduction)
+    (3, 8, 9, 11, 40, 2, 1),      # implicit, stride 2
+    (2, 3, 7, 7, 5, 1, 1),        # c_in % 4 != 0: column-buffer path, db on its own
+    (8, 64, 14, 14, 64, 1, 1),    # implicit with a larger K range
+])
+def test_conv_weight_bias_one_call(dev, n, c, h, wd, co, stride, pad):
+    """mt_conv2d_bwd_weight_bias_f32 against the oracle with accumulation into
+    existing gradients (beta_w = 0.5, beta_b = 2), bit-identical on a repeat,
+    and db equal to the stand-alone bias entry within the bound."""
+    x = oracle.normal((n, c, h, wd), 11)
+    w = oracle.normal((co, c, 3, 3), 12)
+    ho, wo = oracle.conv_out(h, pad, 3, stride), oracle.conv_out(wd, pad, 3, stride)
+    dy = oracle.normal((n, co, ho, wo), 13)
+    dw0 = oracle.normal((co, c, 3, 3), 14)
+    db0 = oracle.normal((co,), 15)
+    X, dY = g(x, dev), g(dy, dev)
+    d = mt.Conv2dDesc(n, c, h, wd, co, 3, 3, stride, pad)
+    ws = mt.workspace(mt.lib().mt_conv2d_bwd_workspace_f32(ctypes.byref(d)), dev)
+    outs = []
+    for _ in range(2):
+        dW, dB = g(dw0, dev), g(db0, dev)
+        rc = mt.lib().mt_conv2d_bwd_weight_bias_f32(ctypes.byref(d), X.data_ptr(), dY.data_ptr(),
+                                                    dW.data_ptr(), 0.5, dB.data_ptr(), 2.0,
+                                                    ws.data_ptr(), ws.numel(), None)
+        assert rc == 0, mt.lib().mt_strerror(rc).decode()
+        print(f"[config] {mt.last_config()}")
+        outs.append((sync_np(dW), sync_np(dB)))
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+    _, wdw, wdb = oracle.conv2d_backward(x, w, dy, stride, pad)
+    dw, db = outs[0]
+    assert_close(dw, 0.5 * dw0.astype(np.float64) + wdw, n * ho * wo, amax(dy), amax(x),
+                 "dW + 0.5 dW0", extra=1e-5)
+    assert_close(db, 2.0 * db0.astype(np.float64) + wdb, n * ho * wo, amax(dy), 1.0,
+                 "db + 2 db0", extra=1e-5)
+    alone = g(db0, dev)
+    assert mt.lib().mt_conv2d_bwd_bias_f32(ctypes.byref(d), dY.data_ptr(), alone.data_ptr(),
+                                           2.0, None) == 0
+    assert_close(db, sync_np(alone).astype(np.float64), n * ho * wo, amax(dy), 1.0,
+                 "db against the bias entry", extra=1e-5)
+    # grad_bias = NULL: the weight gradient alone, bit-identical to its own entry
+    dWa, dWb = g(dw0, dev), g(dw0, dev)
+    assert mt.lib().mt_conv2d_bwd_weight_bias_f32(ctypes.byref(d), X.data_ptr(), dY.data_ptr(),
+                                                  dWa.data_ptr(), 0.5, None, 0.0, ws.data_ptr(),
+                                                  ws.numel(), None) == 0
+    assert mt.lib().mt_conv2d_bwd_weight_f32(ctypes.byref(d), X.data_ptr(), dY.data_ptr(),
+                                             dWb.data_ptr(), 0.5, ws.data_ptr(), ws.numel(),
+                                             None) == 0
+    assert np.array_equal(sync_np(dWa), sync_np(dWb))
+    assert np.array_equal(sync_np(dWa), dw)
 
 
 def test_config5a_conv_backward_adjoint(dev):
