@@ -142,8 +142,8 @@ int mt_linear_backward_f32(const mt_mat_f32* dY, const mt_mat_f32* X, const mt_m
  *     OIHW weights, which it reads in place (a weight pointer that is not
  *     16-byte aligned is first copied to the workspace).
  * (Implicit GEMM; the workspace holds the copies and any split-K partials.)
- * Otherwise an im2col pass fills a column buffer in the workspace first.
- * mt_conv2d_workspace_f32
+ * Otherwise (or when h or w plus twice the padding reaches 2^30) an im2col
+ * pass fills a column buffer in the workspace first.  mt_conv2d_workspace_f32
  * reports the size of whichever path the geometry takes; a workspace that is
  * missing or too small returns MT_ERR_WORKSPACE.  Replaces conv2d_gpu +
  * im2col_kernel + batched_sgemm_kernel_v2 (reference src/gpu_ops.cpp:2237-2325,
