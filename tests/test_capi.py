@@ -116,6 +116,25 @@ def test_conv_rejects_invalid_descriptors():
                                  None) == mt.MT_ERR_WORKSPACE
 
 
+def test_conv_nchw_path_workspace_and_weight_bias_arguments():
+    lib = mt.lib()
+    # c_in*kh*kw % 4 == 0 with c_in % 16 != 0: the NCHW-view path needs room for
+    # an aligned weight copy and is refused without a workspace (before any launch)
+    d = mt.Conv2dDesc(2, 4, 8, 8, 6, 3, 3, 1, 1)
+    assert lib.mt_conv2d_workspace_f32(ctypes.byref(d)) >= 6 * 36 * 4
+    assert lib.mt_conv2d_fwd_f32(ctypes.byref(d), 0x1000, 0x1000, None, 0x1000, None, 0,
+                                 None) == mt.MT_ERR_WORKSPACE
+    # the combined weight + bias gradient validates like the two entries it replaces
+    bad = mt.Conv2dDesc(1, 3, 8, 8, 4, 0, 3, 1, 0)
+    assert lib.mt_conv2d_bwd_weight_bias_f32(ctypes.byref(bad), 0x1000, 0x1000, 0x1000, 0.0,
+                                             0x1000, 0.0, None, 0, None) == mt.MT_ERR_INVALID
+    assert lib.mt_conv2d_bwd_weight_bias_f32(None, 0x1000, 0x1000, 0x1000, 0.0, 0x1000, 0.0,
+                                             None, 0, None) == mt.MT_ERR_INVALID
+    d = mt.Conv2dDesc(2, 16, 8, 8, 6, 3, 3, 1, 1)
+    assert lib.mt_conv2d_bwd_weight_bias_f32(ctypes.byref(d), 0x1000, None, 0x1000, 0.0,
+                                             0x1000, 0.0, None, 0, None) == mt.MT_ERR_INVALID
+
+
 def test_linear_rejects_mismatched_shapes():
     lib = mt.lib()
     rc = lib.mt_linear_backward_f32(M(8, 10), M(8, 6), M(11, 6), None, None, 0.0, None, 0, 0.0,
