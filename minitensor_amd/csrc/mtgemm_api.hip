@@ -979,7 +979,8 @@ hipError_t transpose_dy(const mt_conv2d_desc* d, int64_t hw, const float* dy, fl
 // out dense [B][J][I], moved in TI x TJ tiles (2048 elements, 8 per thread)
 // through LDS.  Reads run along j (coalesced when sj0 == 1), or along i when
 // ri is set (si == 1: a batched copy that only reorders the outer
-// dimensions); writes run along i.  With b = image, i = channel, j = pixel it
+// dimensions); writes run along i.  Where rows are dense and 16-byte aligned
+// (vec) the accesses are 16 bytes wide, and a batched copy skips LDS.  With b = image, i = channel, j = pixel it
 // turns an NCHW view into channels-last; with b = c_out, i = c_in, j = filter
 // tap it turns OIHW weights into OHWI.  Tiles are TI x TJ = 32 x 64, or
 // 64 x 32 when J <= 32, or 128 x 16 when J <= 16 (filter taps), so that few
@@ -992,7 +993,8 @@ struct TJob {
     int lti, ltj;      // log2 of the tile's extent along i and j
     int ti, tj;        // tiles along i and j
     int ri;            // read along i
-    int64_t blocks;    // ti * tj * B
+    int vec;           // 16-byte accesses: 1 tiled transpose, 2 flat row copy (ri, jw == 1)
+    int64_t blocks;    // ti * tj * B, or 512-vector blocks of the flat copy
 };
 
 TJob tjob(const float* in, int64_t sb, int64_t si, int64_t sj1, int64_t sj0, int64_t jw,
@@ -1006,7 +1008,25 @@ TJob tjob(const float* in, int64_t sb, int64_t si, int64_t sj1, int64_t sj0, int
     t.ti = (int)((I + (1 << t.lti) - 1) >> t.lti);
     t.tj = (int)((J + (1 << t.ltj) - 1) >> t.ltj);
     t.ri = si == 1 && sj0 != 1;
-    t.blocks = (I == 0 || J == 0) ? 0 : (int64_t)t.ti * t.tj * B;
+    // 16-byte loads and stores: every row start of the input and the output
+    // 16-byte aligned and the rows whole multiples of 4 floats
+    const bool aligned = ((uintptr_t)in & 15u) == 0 && ((uintptr_t)out & 15u) == 0 &&
+                         (I & 3) == 0 && (sb & 3) == 0;
+    if (aligned && !t.ri && J > 32 && sj0 == 1 && sj1 == jw && (J & 3) == 0 && (si & 3) == 0) {
+        // j is linear and contiguous in the input: 64 x 32 or 32 x 64 tiles,
+        // whichever covers I x J with fewer
+        t.vec = 1;
+        const int64_t n32 = ((I + 63) >> 6) * ((J + 31) >> 5), n64 = ((I + 31) >> 5) * ((J + 63) >> 6);
+        t.ltj = n32 < n64 ? 5 : 6;
+        t.lti = 11 - t.ltj;
+        t.ti = (int)((I + (1 << t.lti) - 1) >> t.lti);
+        t.tj = (int)((J + (1 << t.ltj) - 1) >> t.ltj);
+    } else if (aligned && t.ri && jw == 1 && (sj1 & 3) == 0) {
+        t.vec = 2;   // a copy of i-contiguous rows
+    }
+    t.blocks = (I == 0 || J == 0) ? 0
+               : t.vec == 2      ? ((I >> 2) * J * B + 511) >> 9
+                                 : (int64_t)t.ti * t.tj * B;
     return t;
 }
 
@@ -1034,12 +1054,61 @@ __global__ void __launch_bounds__(256) transpose_f32(TJob j0, TJob j1, int xcd) 
         const bool second = blk >= j0.blocks;
         const TJob jb = second ? j1 : j0;
         int64_t r = second ? blk - j0.blocks : blk;
+        if (jb.vec == 2) {
+            // flat copy of I-float rows, row = b * J + j: 512 16-byte groups
+            // per block, two per thread
+            const int64_t q4 = jb.I >> 2, n4 = q4 * jb.J * jb.B;
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int64_t g = r * 512 + k * 256 + t;
+                if (g >= n4) break;
+                int64_t row, iq, b, j;
+                if (n4 <= INT32_MAX) {
+                    const uint32_t rw = (uint32_t)g / (uint32_t)q4;
+                    const uint32_t bb = rw / (uint32_t)jb.J;
+                    row = rw; iq = (uint32_t)g - rw * (uint32_t)q4;
+                    b = bb; j = rw - bb * (uint32_t)jb.J;
+                } else {
+                    row = g / q4; iq = g - row * q4; b = row / jb.J; j = row - b * jb.J;
+                }
+                *reinterpret_cast<f32x4*>(jb.out + row * jb.I + 4 * iq) =
+                    *reinterpret_cast<const f32x4*>(jb.in + b * jb.sb + j * jb.sj1 + 4 * iq);
+            }
+            continue;
+        }
         const int per_b = jb.ti * jb.tj;
         const int b = (int)(r / per_b);
         r -= (int64_t)b * per_b;
         const int TI = 1 << jb.lti, TJ = 1 << jb.ltj, pitch = TJ + 1;
         const int i0 = (int)(r / jb.tj) << jb.lti, jt0 = (int)(r % jb.tj) << jb.ltj;
         const float* src = jb.in + (int64_t)b * jb.sb;
+        if (jb.vec == 1) {
+            // two 16-byte loads along j and two 16-byte stores along i per
+            // thread (TI x TJ = 64 x 32 or 32 x 64)
+            const int jq = t & ((TJ >> 2) - 1), ir = t >> (jb.ltj - 2), rstep = 256 >> (jb.ltj - 2);
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int il = ir + k * rstep, i = i0 + il, j = jt0 + 4 * jq;
+                f32x4 x = {0.f, 0.f, 0.f, 0.f};
+                if (i < jb.I && j < jb.J)
+                    x = *reinterpret_cast<const f32x4*>(src + (int64_t)i * jb.si + j);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) tile[il * pitch + 4 * jq + e] = x[e];
+            }
+            __syncthreads();
+            const int iq = t & ((TI >> 2) - 1), jr = t >> (jb.lti - 2), jstep = 256 >> (jb.lti - 2);
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int jl = jr + k * jstep, j = jt0 + jl, i = i0 + 4 * iq;
+                if (i < jb.I && j < jb.J) {
+                    const float* c = tile + (4 * iq) * pitch + jl;
+                    const f32x4 x = {c[0], c[pitch], c[2 * pitch], c[3 * pitch]};
+                    *reinterpret_cast<f32x4*>(jb.out + ((int64_t)b * jb.J + j) * jb.I + i) = x;
+                }
+            }
+            __syncthreads();
+            continue;
+        }
         // i-major lanes (consecutive i) for ri reads and for the writes;
         // j-major lanes (consecutive j) for the other reads
         const int im_i = t & (TI - 1), im_j = t >> jb.lti, im_step = 256 >> jb.lti;
