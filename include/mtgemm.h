@@ -137,10 +137,11 @@ int mt_linear_backward_f32(const mt_mat_f32* dY, const mt_mat_f32* X, const mt_m
  *   c_in % 16 == 0: the input is copied to channels-last in the workspace
  *     (unless it already is channels-last), the weights to OHWI, and the GEMM
  *     kernel gathers the im2col operand from that copy with 16-byte loads;
- *   else c_in*kh*kw % 4 == 0: the GEMM kernel gathers the im2col operand
- *     from the NCHW input itself, 4 bytes per load, with the K order of the
- *     OIHW weights, which it reads in place (a weight pointer that is not
- *     16-byte aligned is first copied to the workspace).
+ *   else c_in*kh*kw % 4 == 0: the GEMM kernel builds the im2col operand
+ *     from the NCHW input itself, with the K order of the OIHW weights,
+ *     which it reads in place (a weight pointer that is not 16-byte aligned
+ *     is first copied to the workspace): from halo patches of the input in
+ *     LDS where they pay, else gathered per K-chunk, 4 bytes per load.
  * (Implicit GEMM; the workspace holds the copies and any split-K partials.)
  * Otherwise (or when h or w plus twice the padding reaches 2^30) an im2col
  * pass fills a column buffer in the workspace first.  mt_conv2d_workspace_f32
@@ -247,6 +248,10 @@ int mt_gemm_config_count(int family);
  * 256x256, 64x64 and 128x128 tiles, take the convolution weight gradient's
  * implicit operand but not the forward convolution's implicit im2col
  * operand or fused row sums.)
+ * A forced direct-to-LDS configuration also builds the im2col operand of a
+ * convolution over an NCHW view from halo patches in LDS whenever the patches
+ * fit, without the rule that otherwise keeps the per-chunk gather where the
+ * patches would not pay.
  * MT_FAMILY_AUTO clears it.  While it is set, workspace queries include its
  * split-K partials and a launch given less returns MT_ERR_WORKSPACE.
  * Returns MT_ERR_INVALID for an unknown family, configuration or split count. */

@@ -85,6 +85,13 @@ GemmLaunchFn dl_convr_launcher_cfg0();
 GemmLaunchFn dl_convr_launcher_cfg1();
 GemmLaunchFn dl_convr_launcher_cfg2();
 GemmLaunchFn dl_convr_launcher_cfg3();
+// The same convolution with B built in LDS from a halo patch (L_IMH,
+// gemm_dlh_kernel.hpp): ConvGeom::hp and pw set, LDS per workgroup
+// dlh_lds_floats of the configuration's tile.
+GemmLaunchFn dl_convh_launcher_cfg0();
+GemmLaunchFn dl_convh_launcher_cfg1();
+GemmLaunchFn dl_convh_launcher_cfg2();
+GemmLaunchFn dl_convh_launcher_cfg3();
 // Convolution weight gradient: A = dY [c_out][n*h_out*w_out] (L_KV), B = L_IMW.
 GemmLaunchFn dl_convw_launcher_cfg0();
 GemmLaunchFn dl_convw_launcher_cfg1();

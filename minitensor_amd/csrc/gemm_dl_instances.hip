@@ -4,9 +4,11 @@
 // convolution (A k-contiguous weights, B = L_IM from a channels-last input or
 // L_IMR from an NCHW view) and its weight gradient
 // (A = dY as [c_out][n*h_out*w_out], B = L_IMW), and the mn-contiguous pair
-// with fused row sums of A (the Linear dW GEMM with its bias gradient).
+// with fused row sums of A (the Linear dW GEMM with its bias gradient); and
+// the halo-patch convolution kernel gemm_f32_dlh of the same tile.
 #include "gemm_configs.hpp"
 #include "gemm_dl_kernel.hpp"
+#include "gemm_dlh_kernel.hpp"
 
 #ifndef MT_CFG
 #error "build with -DMT_CFG=<tile configuration index>"
@@ -23,6 +25,18 @@ hipError_t launch_dl(const GemmParams& p, unsigned nblocks, hipStream_t s) {
     return hipGetLastError();
 }
 
+// The halo-patch kernel's LDS depends on the convolution's geometry.
+template <int CFG>
+hipError_t launch_dlh(const GemmParams& p, unsigned nblocks, hipStream_t s) {
+    using C = DlCfg<CFG>;
+    const size_t bytes = sizeof(float) * dlh_lds_floats<C::BM, C::BN, C::WM, C::WN>(p.cv);
+    HaloTable t;
+    halo_table(p.cv, C::BN, &t);
+    hipLaunchKernelGGL((gemm_f32_dlh<C::BM, C::BN, C::WM, C::WN>), dim3(nblocks),
+                       dim3(dl_threads<CFG>()), bytes, s, p, t);
+    return hipGetLastError();
+}
+
 #define MT_DL_TABLE(CFG) \
     { { launch_dl<CFG, L_KV, L_KV>, launch_dl<CFG, L_KV, L_MV> }, \
       { launch_dl<CFG, L_MV, L_KV>, launch_dl<CFG, L_MV, L_MV> } }
@@ -36,6 +50,7 @@ GemmLaunchFn dl_launcher_cfg0(int la, int lb) {
 }
 GemmLaunchFn dl_conv_launcher_cfg0() { return launch_dl<0, L_KV, L_IM>; }
 GemmLaunchFn dl_convr_launcher_cfg0() { return launch_dl<0, L_KV, L_IMR>; }
+GemmLaunchFn dl_convh_launcher_cfg0() { return launch_dlh<0>; }
 GemmLaunchFn dl_convw_launcher_cfg0() { return launch_dl<0, L_KV, L_IMW>; }
 GemmLaunchFn dl_rowsum_launcher_cfg0() { return launch_dl<0, L_MV, L_MV, true>; }
 #elif MT_CFG == 1
@@ -45,6 +60,7 @@ GemmLaunchFn dl_launcher_cfg1(int la, int lb) {
 }
 GemmLaunchFn dl_conv_launcher_cfg1() { return launch_dl<1, L_KV, L_IM>; }
 GemmLaunchFn dl_convr_launcher_cfg1() { return launch_dl<1, L_KV, L_IMR>; }
+GemmLaunchFn dl_convh_launcher_cfg1() { return launch_dlh<1>; }
 GemmLaunchFn dl_convw_launcher_cfg1() { return launch_dl<1, L_KV, L_IMW>; }
 GemmLaunchFn dl_rowsum_launcher_cfg1() { return launch_dl<1, L_MV, L_MV, true>; }
 #elif MT_CFG == 2
@@ -54,6 +70,7 @@ GemmLaunchFn dl_launcher_cfg2(int la, int lb) {
 }
 GemmLaunchFn dl_conv_launcher_cfg2() { return launch_dl<2, L_KV, L_IM>; }
 GemmLaunchFn dl_convr_launcher_cfg2() { return launch_dl<2, L_KV, L_IMR>; }
+GemmLaunchFn dl_convh_launcher_cfg2() { return launch_dlh<2>; }
 GemmLaunchFn dl_convw_launcher_cfg2() { return launch_dl<2, L_KV, L_IMW>; }
 GemmLaunchFn dl_rowsum_launcher_cfg2() { return launch_dl<2, L_MV, L_MV, true>; }
 #elif MT_CFG == 3
@@ -63,6 +80,7 @@ GemmLaunchFn dl_launcher_cfg3(int la, int lb) {
 }
 GemmLaunchFn dl_conv_launcher_cfg3() { return launch_dl<3, L_KV, L_IM>; }
 GemmLaunchFn dl_convr_launcher_cfg3() { return launch_dl<3, L_KV, L_IMR>; }
+GemmLaunchFn dl_convh_launcher_cfg3() { return launch_dlh<3>; }
 GemmLaunchFn dl_convw_launcher_cfg3() { return launch_dl<3, L_KV, L_IMW>; }
 GemmLaunchFn dl_rowsum_launcher_cfg3() { return launch_dl<3, L_MV, L_MV, true>; }
 #else

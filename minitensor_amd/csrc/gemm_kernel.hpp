@@ -57,8 +57,10 @@ enum : int {
     L_MS = 3,  // mn-contiguous LDS tile, scalar gathers (any strides)
     L_IM = 4,  // B only, direct-to-LDS kernel: implicit im2col of a channels-last input
     L_IMW = 5, // B only, direct-to-LDS kernel: implicit im2colᵀ (conv weight gradient)
-    L_IMR = 6  // B only, direct-to-LDS kernel: implicit im2col of an NCHW view, K order
+    L_IMR = 6, // B only, direct-to-LDS kernel: implicit im2col of an NCHW view, K order
                // (ci, r, s), gathered by 4-byte DMA
+    L_IMH = 7  // B only (gemm_f32_dlh): L_IMR's operand built in LDS from a halo
+               // patch of the input
 };
 
 // Geometry of an implicit-im2col B operand over a channels-last input
@@ -78,7 +80,52 @@ struct ConvGeom {
     int64_t img_stride;
     int c, h, w, kh, kw, stride, pad, ho, wo;
     int64_t sc, sh, sw;   // L_IMR: element strides of a channel, a row, a column
+    int hp, pw;           // L_IMH: padded rows per image, (ho-1)*stride + kh, and
+                          // padded columns, (wo-1)*stride + kw
 };
+
+// Padded input rows a tile of bn consecutive output pixels can touch: at
+// most ceil((bn-1)/wo) row steps, each +stride within an image and +kh across
+// an image boundary (at most ceil(steps/ho) of those), plus the kh rows of the
+// last window.
+__host__ __device__ inline int halo_rows(const ConvGeom& g, int bn) {
+    const int steps = (bn - 1 + g.wo - 1) / g.wo;
+    const int cross = (steps + g.ho - 1) / g.ho;
+    return steps * g.stride + (g.kh > g.stride ? cross * (g.kh - g.stride) : 0) + g.kh;
+}
+
+// Floats between consecutive channels of a patch: one channel's band
+// (halo_rows x pw) rounded up to whole 64-element DMA instructions, at most
+// kHaloIpcMax of them.
+constexpr int kHaloIpcMax = 12;
+__host__ __device__ inline int halo_chan_stride(const ConvGeom& g, int bn) {
+    return (halo_rows(g, bn) * g.pw + 63) & ~63;
+}
+
+// Patch offsets of the 16*kh*kw k of a patch (k = ch*kh*kw + r*kw + s ->
+// ch*halo_chan_stride + r*pw + s), passed to gemm_f32_dlh as a kernel
+// argument so that a chunk's offsets are wave-uniform scalar loads.
+constexpr int kHaloMaxTaps = 25;
+struct HaloTable {
+    int off[16 * kHaloMaxTaps];
+};
+inline void halo_table(const ConvGeom& g, int bn, HaloTable* t) {
+    const int khw = g.kh * g.kw, cst = halo_chan_stride(g, bn);
+    for (int e = 0; e < 16 * khw; ++e) {
+        const int ch = e / khw, tap = e - ch * khw, r = tap / g.kw;
+        t->off[e] = ch * cst + r * g.pw + (tap - r * g.kw);
+    }
+}
+
+// LDS of one gemm_f32_dlh workgroup, in floats: the A ring and two patches
+// of 16 channels, or the epilogue's staging if that is larger.
+template <int BM, int BN, int WM, int WN>
+__host__ __device__ inline int dlh_lds_floats(const ConvGeom& g) {
+    constexpr int NW = (BM / WM) * (BN / WN);
+    const int need = 2 * BM * 16 + 2 * 16 * halo_chan_stride(g, BN);
+    return need > 1024 * NW ? need : 1024 * NW;
+}
+
 
 struct GemmParams {
     const float* A; int64_t a_mn, a_k, a_b;   // A(m,k) = A[m*a_mn + k*a_k + b*a_b]

@@ -61,6 +61,21 @@ int device_cu_count() {
     return cus;
 }
 
+// LDS a workgroup may take on the current device (bytes).
+int device_lds_limit() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 65536;
+    int v = cache[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+    int b = 0;
+    if (hipDeviceGetAttribute(&b, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
+        b <= 0)
+        b = 65536;
+    cache[dev].store(b, std::memory_order_relaxed);
+    return b;
+}
+
 bool valid_mat(const mt_mat_f32* X) {
     if (!X) return false;
     if (X->rows < 0 || X->cols < 0 || X->batch < 0) return false;
@@ -89,6 +104,7 @@ const char* layout_name(int l) {
         case L_IM: return "im2col";
         case L_IMW: return "im2colT";
         case L_IMR: return "im2col_nchw";
+        case L_IMH: return "im2col_halo";
         case L_KS: return "ks";
         default: return "ms";
     }
@@ -354,6 +370,66 @@ GemmLaunchFn convw_launcher(int cfg, bool ktail) {
     }
 }
 
+// LDS floats of the halo-patch kernel of dl configuration cfg (0-3).
+int halo_lds_floats(int cfg, const ConvGeom& g) {
+    switch (cfg) {
+        case 0: return dlh_lds_floats<DlCfg<0>::BM, DlCfg<0>::BN, DlCfg<0>::WM, DlCfg<0>::WN>(g);
+        case 1: return dlh_lds_floats<DlCfg<1>::BM, DlCfg<1>::BN, DlCfg<1>::WM, DlCfg<1>::WN>(g);
+        case 2: return dlh_lds_floats<DlCfg<2>::BM, DlCfg<2>::BN, DlCfg<2>::WM, DlCfg<2>::WN>(g);
+        case 3: return dlh_lds_floats<DlCfg<3>::BM, DlCfg<3>::BN, DlCfg<3>::WM, DlCfg<3>::WN>(g);
+        default: return -1;
+    }
+}
+
+// Whether the halo-patch kernel of configuration cfg takes the L_IMR
+// geometry g (hp and pw set) with K ranges of kps: at least two taps (a patch
+// then serves two or more chunks, which the kernel's B prefetch relies on),
+// taps, stride and padded extents small enough for its 32-bit patch
+// arithmetic, a channel's band at most kHaloIpcMax DMA instructions, the
+// images one band spans addressable with 32-bit offsets, and the workgroup's
+// LDS within the device's limit.  It pays only when a patch is small next to
+// the per-chunk B tiles it replaces and a workgroup multiplies at least one
+// whole patch: patch (16 bands) at most 0.3 of kh*kw tiles of BN x 16, and
+// kps >= 16*kh*kw (smaller ratios or K ranges measured slower than the
+// per-chunk gather, e.g. 45 against 30 us for c_in 8 at 56x56); cost = false
+// skips that rule (a forced configuration: the test hook of the kernel).
+bool halo_fits(const ConvGeom& g, int n_img, int cfg, int kps, bool cost) {
+    static constexpr int kBn[4] = {DlCfg<0>::BN, DlCfg<1>::BN, DlCfg<2>::BN, DlCfg<3>::BN};
+    if (cfg < 0 || cfg > 3) return false;
+    if (g.kh < 1 || g.kw < 1 || g.kh * g.kw < 2 || g.kh * g.kw > kHaloMaxTaps || g.stride < 1 ||
+        g.stride > 16)
+        return false;
+    if (g.ho < 1 || g.wo < 1 || g.pw < 1 || g.pw > 4096 || g.hp < 1) return false;
+    if ((int64_t)n_img * g.hp + 512 * (int64_t)g.stride >= ((int64_t)1 << 31)) return false;
+    const int rows = halo_rows(g, kBn[cfg]);
+    const int cst = halo_chan_stride(g, kBn[cfg]);
+    if (cst > 64 * kHaloIpcMax) return false;
+    const int khw = g.kh * g.kw;
+    if (cost && (kps < 16 * khw || 10 * cst > 3 * khw * kBn[cfg])) return false;
+    const int64_t span = (rows + g.hp - 1) / g.hp + 1;   // images one band can touch
+    if (span * g.img_stride + (int64_t)(g.h - 1) * g.sh + (int64_t)(g.w - 1) * g.sw >=
+        ((int64_t)1 << 31))
+        return false;
+    const int f = halo_lds_floats(cfg, g);
+    return f > 0 && (int64_t)f * 4 <= device_lds_limit();
+}
+
+// The ConvGeom patch extents of an L_IMR convolution.
+void set_halo_geometry(ConvGeom& g) {
+    g.hp = (g.ho - 1) * g.stride + g.kh;
+    g.pw = (g.wo - 1) * g.stride + g.kw;
+}
+
+GemmLaunchFn convh_launcher(int cfg) {
+    switch (cfg) {
+        case 0: return dl_convh_launcher_cfg0();
+        case 1: return dl_convh_launcher_cfg1();
+        case 2: return dl_convh_launcher_cfg2();
+        case 3: return dl_convh_launcher_cfg3();
+        default: return nullptr;
+    }
+}
+
 GemmLaunchFn conv_launcher(int cfg, bool nchw) {
     switch (cfg) {
         case 0: return nchw ? dl_convr_launcher_cfg0() : dl_conv_launcher_cfg0();
@@ -559,7 +635,8 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
     // sums, a non-empty K range.
     const bool wide_ok = dl && lb != L_IM && lb != L_IMR && p.rowsum == nullptr && K > 0;
     Plan plan;
-    if (forced_plan(M, N, K, batch, dl, !implicit, wide_ok, &plan)) {
+    const bool forced = forced_plan(M, N, K, batch, dl, !implicit, wide_ok, &plan);
+    if (forced) {
         if (plan.splits > 1 && (workspace == nullptr || ws_bytes < plan.ws_bytes))
             return MT_ERR_WORKSPACE;
     } else {
@@ -589,13 +666,19 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
 
     const int64_t nblocks = (int64_t)plan.tiles_m * plan.tiles_n * plan.splits * batch;
     if (nblocks >= ((int64_t)1 << 31)) return MT_ERR_UNSUPPORTED;
+    // The NCHW-view operand is built from halo patches in LDS when the
+    // configuration's patches fit (same K order, operands and output).
+    const bool halo = lb == L_IMR && p.cv.hp > 0 &&
+                      halo_fits(p.cv, (int)(N / ((int64_t)p.cv.ho * p.cv.wo)), plan.cfg,
+                                p.k_per_split, !forced);
     std::snprintf(g_last_config, sizeof g_last_config,
                   "%s %dx%d a=%s b=%s split=%d wgs=%lld cfg=%d",
                   plan.ksw ? "ksw" : plan.dl ? "dl" : "rs", plan.bm,
-                  plan.bn, layout_name(la), layout_name(lb), plan.splits, (long long)nblocks,
-                  plan.cfg);
+                  plan.bn, layout_name(la), layout_name(halo ? L_IMH : lb), plan.splits,
+                  (long long)nblocks, plan.cfg);
 
-    GemmLaunchFn fn = lb == L_IM || lb == L_IMR ? conv_launcher(plan.cfg, lb == L_IMR)
+    GemmLaunchFn fn = halo ? convh_launcher(plan.cfg)
+                      : lb == L_IM || lb == L_IMR ? conv_launcher(plan.cfg, lb == L_IMR)
                       : lb == L_IMW         ? convw_launcher(plan.cfg, (K & 15) != 0)
                       : p.rowsum != nullptr ? rowsum_launcher(plan.cfg)
                                             : pick_launcher(plan, la, lb, (K & 15) != 0);
@@ -1275,6 +1358,7 @@ int run_conv_nchw(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, const float* 
     g.c = (int)d->c_in; g.h = (int)d->h; g.w = (int)d->w;
     g.kh = (int)d->kh; g.kw = (int)d->kw; g.stride = (int)d->stride; g.pad = (int)d->pad;
     g.ho = (int)Ho; g.wo = (int)Wo;
+    set_halo_geometry(g);
     return launch_gemm(p, true, L_KV, L_IMR, workspace, ws_bytes, s);
 }
 
@@ -1432,8 +1516,9 @@ int mt_conv2d_fwd_strided_f32(const mt_conv2d_desc* d, const float* input,
 
     // c_in % 16 == 0: the channels-last kernel (16-byte DMA gathers) on a
     // channels-last copy of the input (the input itself when it is one) and
-    // OHWI weights.  Its gathers beat the NCHW-view kernel's 4-byte ones by
-    // more than the two copies cost (benchmark layer: 84 vs 95 us).
+    // OHWI weights.  Its 16-byte gathers beat the NCHW-view kernels (4-byte
+    // gathers or halo patches) by more than the layout launch costs
+    // (benchmark layer, forward: 79.5 us against 84.5 with halo patches).
     if (implicit_geometry(d) && d->h * d->w < kMaxDim) {
         const ImplicitWs iw = implicit_ws(d);
         if (!workspace || ws_bytes < iw.xt + iw.wt || ((uintptr_t)workspace & 15u) != 0)

@@ -334,7 +334,10 @@ def test_conv_layout_tile_shapes(dev, n, c, h, wd, co, kh, kw, pad):
 # read in place): any c_in with c_in*kh*kw % 4 == 0, including K ranges that
 # end in a partial chunk, fewer K than one chunk, rectangular kernels, strides
 # 2 and 3, padding 0 and 2, and output-channel tails; forward and (stride 1,
-# square kernels) the input gradient.
+# square kernels) the input gradient.  Its B operand is built from halo
+# patches in LDS where they fit (b=im2col_halo), else gathered per chunk
+# (b=im2col_nchw).
+NCHW_PATHS = ("b=im2col_nchw", "b=im2col_halo")
 @pytest.mark.parametrize("n,c,h,wd,co,kh,kw,stride,pad", [
     (2, 4, 9, 9, 8, 3, 3, 1, 1),       # kg = 36: a partial last chunk
     (1, 12, 7, 7, 10, 5, 5, 2, 2),     # kg = 300, stride 2
@@ -349,7 +352,7 @@ def test_conv_nchw_implicit_geometries(dev, n, c, h, wd, co, kh, kw, stride, pad
     out = sync_np(mt.conv2d(g(x, dev), g(w, dev), g(b, dev), stride, pad))
     cfg = mt.last_config()
     print(f"[config] {cfg}")
-    assert "b=im2col_nchw" in cfg, cfg
+    assert any(k in cfg for k in NCHW_PATHS), cfg
     assert_close(out, oracle.conv2d(x, w, b, stride, pad), c * kh * kw, amax(x), amax(w),
                  "NCHW implicit conv", extra=1e-5)
     if stride == 1 and kh == kw and pad <= kh - 1 and (co * kh * kw) % 4 == 0:
@@ -359,7 +362,7 @@ def test_conv_nchw_implicit_geometries(dev, n, c, h, wd, co, kh, kw, stride, pad
                                       need_db=False)
         cfg = mt.last_config()
         print(f"[config] dX {cfg}")
-        assert "b=im2col_nchw" in cfg, cfg
+        assert any(k in cfg for k in NCHW_PATHS), cfg
         wdx, _, _ = oracle.conv2d_backward(x, w, dy, 1, pad)
         assert_close(sync_np(dx), wdx, co * kh * kw, amax(dy), amax(w), "NCHW implicit dX")
 
@@ -377,9 +380,94 @@ def test_conv_nchw_unaligned_weight(dev):
     out = sync_np(mt.conv2d(g(x, dev), W, None, 1, 1))
     cfg = mt.last_config()
     print(f"[config] {cfg}")
-    assert "b=im2col_nchw" in cfg, cfg
+    assert any(k in cfg for k in NCHW_PATHS), cfg
     assert_close(out, oracle.conv2d(x, w, None, 1, 1), c * 9, amax(x), amax(w),
                  "unaligned weight")
+
+
+# The halo-patch kernel (gemm_f32_dlh): bands that span image boundaries
+# (images smaller than one tile, a 3-row image), strides 1-3, kernels 2x2 to
+# 5x5 and 3x2 / 1x3, padding 0-2, K ranges ending in a partial chunk
+# (c*kh*kw % 16 != 0) and patches of one partial channel group, every dl tile
+# configuration (those whose bands fit; the others gather per chunk), and
+# split factors whose K ranges start inside a patch.  A forced configuration
+# takes the halo kernel wherever its patches fit (the automatic choice also
+# weighs whether they pay), so the forced runs cover it.
+@pytest.mark.parametrize("n,c,h,wd,co,kh,kw,stride,pad", [
+    (2, 20, 14, 14, 24, 3, 3, 1, 1),    # two patches, the second partial
+    (5, 4, 3, 5, 7, 3, 3, 1, 1),        # 3x5 images: a band spans many images
+    (3, 12, 9, 11, 16, 3, 3, 2, 1),     # stride 2
+    (2, 8, 13, 10, 9, 5, 5, 1, 2),      # 5x5, pad 2
+    (2, 8, 20, 30, 9, 3, 3, 3, 1),      # stride 3
+    (2, 4, 10, 9, 8, 2, 2, 1, 0),       # 2x2 (kg 16)
+    (1, 36, 7, 8, 20, 3, 2, 1, 1),      # 3x2, three patches
+    (2, 28, 6, 17, 12, 1, 3, 1, 1),     # 1x3
+])
+def test_conv_halo_geometries(dev, n, c, h, wd, co, kh, kw, stride, pad):
+    x = oracle.normal((n, c, h, wd), 410 + c)
+    w = oracle.normal((co, c, kh, kw), 411 + co)
+    b = oracle.normal((co,), 412)
+    want = oracle.conv2d(x, w, b, stride, pad)
+    X, W, B = g(x, dev), g(w, dev), g(b, dev)
+    out = sync_np(mt.conv2d(X, W, B, stride, pad))
+    cfg = mt.last_config()
+    print(f"[config] {cfg}")
+    seen = [cfg]
+    K = c * kh * kw
+    assert_close(out, want, K, amax(x), amax(w), "halo conv", extra=1e-5)
+    for tc in range(4):
+        for sp in (1, 2, 3, 5):
+            with mt.forced_config(mt.FAMILY_DL, tc, sp):
+                out = sync_np(mt.conv2d(X, W, B, stride, pad))
+                cfg = mt.last_config()
+            print(f"[config] cfg {tc} split {sp}: {cfg}")
+            # (a tile's band may exceed the patch limit at the larger tiles)
+            assert any(k in cfg for k in NCHW_PATHS), cfg
+            seen.append(cfg)
+            assert_close(out, want, K, amax(x), amax(w), f"halo conv cfg {tc} split {sp}",
+                         extra=1e-5)
+    assert sum("b=im2col_halo" in c for c in seen) >= 4, seen
+    if stride == 1 and kh == kw and pad <= kh - 1 and (co * kh * kw) % 4 == 0 and co % 16:
+        ho, wo = oracle.conv_out(h, pad, kh, 1), oracle.conv_out(wd, pad, kw, 1)
+        dy = oracle.normal((n, co, ho, wo), 413)
+        with mt.forced_config(mt.FAMILY_DL, 2, 2):
+            dx, _, _ = mt.conv2d_backward(X, W, g(dy, dev), 1, pad, need_dw=False,
+                                          need_db=False)
+            cfg = mt.last_config()
+        print(f"[config] dX {cfg}")
+        assert "b=im2col_halo" in cfg, cfg
+        wdx, _, _ = oracle.conv2d_backward(x, w, dy, 1, pad)
+        assert_close(sync_np(dx), wdx, co * kh * kw, amax(dy), amax(w), "halo dX")
+
+
+def test_conv_halo_repeat_bitwise(dev):
+    """The halo kernel sums in a fixed order: repeated calls give the same bits."""
+    n, c, h, wd, co = 3, 20, 11, 13, 40
+    X = g(oracle.normal((n, c, h, wd), 420), dev)
+    W = g(oracle.normal((co, c, 3, 3), 421), dev)
+    with mt.forced_config(mt.FAMILY_DL, 1, 2):
+        a = sync_np(mt.conv2d(X, W, None, 1, 1))
+        assert "b=im2col_halo" in mt.last_config(), mt.last_config()
+        for _ in range(3):
+            assert np.array_equal(sync_np(mt.conv2d(X, W, None, 1, 1)), a)
+
+
+@pytest.mark.parametrize("n,c,h,wd,co,kh,kw,stride,pad", [
+    (2, 8, 6, 6, 5, 1, 1, 1, 0),        # one tap: no patch reuse
+    (1, 4, 5, 200, 6, 3, 3, 1, 1),      # 202 padded columns: the band is too wide
+    (2, 8, 20, 20, 16, 3, 3, 1, 1),     # K 72: less than one patch, not worth it
+])
+def test_conv_nchw_gather_fallback(dev, n, c, h, wd, co, kh, kw, stride, pad):
+    """Geometries the halo kernel does not take, or where its patches would not
+    pay, run the per-chunk NCHW gather."""
+    x = oracle.normal((n, c, h, wd), 430 + wd)
+    w = oracle.normal((co, c, kh, kw), 431)
+    out = sync_np(mt.conv2d(g(x, dev), g(w, dev), None, stride, pad))
+    cfg = mt.last_config()
+    print(f"[config] {cfg}")
+    assert "b=im2col_nchw" in cfg, cfg
+    assert_close(out, oracle.conv2d(x, w, None, stride, pad), c * kh * kw, amax(x), amax(w),
+                 "NCHW gather conv")
 
 
 @pytest.mark.parametrize("view", ["channel_slice", "spatial_crop", "nhwc", "batch_step"])
