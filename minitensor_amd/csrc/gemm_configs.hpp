@@ -75,6 +75,8 @@ GemmLaunchFn dl_launcher_cfg3(int la, int lb);
 GemmLaunchFn dlp_launcher(int cfg, bool tail, int la, int lb);
 // Configurations 4-6 for the convolution weight gradient (A L_KV, B L_IMW).
 GemmLaunchFn dlp_convw_launcher(int cfg, bool tail);
+// Configurations 4-6 for the weight gradient with A = dY in NCHW (L_KVI).
+GemmLaunchFn dlp_convwi_launcher(int cfg);
 // Implicit-im2col convolution: A = weights (L_KV), B = L_IM (GemmParams::cv).
 GemmLaunchFn dl_conv_launcher_cfg0();
 GemmLaunchFn dl_conv_launcher_cfg1();
@@ -97,6 +99,11 @@ GemmLaunchFn dl_convw_launcher_cfg0();
 GemmLaunchFn dl_convw_launcher_cfg1();
 GemmLaunchFn dl_convw_launcher_cfg2();
 GemmLaunchFn dl_convw_launcher_cfg3();
+// The same with A = dY in NCHW (L_KVI; K a multiple of 16).
+GemmLaunchFn dl_convwi_launcher_cfg0();
+GemmLaunchFn dl_convwi_launcher_cfg1();
+GemmLaunchFn dl_convwi_launcher_cfg2();
+GemmLaunchFn dl_convwi_launcher_cfg3();
 // A and B mn-contiguous, with the row sums of A (GemmParams::rowsum).
 GemmLaunchFn dl_rowsum_launcher_cfg0();
 GemmLaunchFn dl_rowsum_launcher_cfg1();

@@ -4,7 +4,8 @@
 // convolution (A k-contiguous weights, B = L_IM from a channels-last input or
 // L_IMR from an NCHW view) and its weight gradient
 // (A = dY as [c_out][n*h_out*w_out], B = L_IMW), and the mn-contiguous pair
-// with fused row sums of A (the Linear dW GEMM with its bias gradient); and
+// with fused row sums of A (the Linear dW GEMM with its bias gradient), the
+// weight gradient with dY read in NCHW (A = L_KVI); and
 // the halo-patch convolution kernel gemm_f32_dlh of the same tile.
 #include "gemm_configs.hpp"
 #include "gemm_dl_kernel.hpp"
@@ -52,6 +53,7 @@ GemmLaunchFn dl_conv_launcher_cfg0() { return launch_dl<0, L_KV, L_IM>; }
 GemmLaunchFn dl_convr_launcher_cfg0() { return launch_dl<0, L_KV, L_IMR>; }
 GemmLaunchFn dl_convh_launcher_cfg0() { return launch_dlh<0>; }
 GemmLaunchFn dl_convw_launcher_cfg0() { return launch_dl<0, L_KV, L_IMW>; }
+GemmLaunchFn dl_convwi_launcher_cfg0() { return launch_dl<0, L_KVI, L_IMW>; }
 GemmLaunchFn dl_rowsum_launcher_cfg0() { return launch_dl<0, L_MV, L_MV, true>; }
 #elif MT_CFG == 1
 GemmLaunchFn dl_launcher_cfg1(int la, int lb) {
@@ -62,6 +64,7 @@ GemmLaunchFn dl_conv_launcher_cfg1() { return launch_dl<1, L_KV, L_IM>; }
 GemmLaunchFn dl_convr_launcher_cfg1() { return launch_dl<1, L_KV, L_IMR>; }
 GemmLaunchFn dl_convh_launcher_cfg1() { return launch_dlh<1>; }
 GemmLaunchFn dl_convw_launcher_cfg1() { return launch_dl<1, L_KV, L_IMW>; }
+GemmLaunchFn dl_convwi_launcher_cfg1() { return launch_dl<1, L_KVI, L_IMW>; }
 GemmLaunchFn dl_rowsum_launcher_cfg1() { return launch_dl<1, L_MV, L_MV, true>; }
 #elif MT_CFG == 2
 GemmLaunchFn dl_launcher_cfg2(int la, int lb) {
@@ -72,6 +75,7 @@ GemmLaunchFn dl_conv_launcher_cfg2() { return launch_dl<2, L_KV, L_IM>; }
 GemmLaunchFn dl_convr_launcher_cfg2() { return launch_dl<2, L_KV, L_IMR>; }
 GemmLaunchFn dl_convh_launcher_cfg2() { return launch_dlh<2>; }
 GemmLaunchFn dl_convw_launcher_cfg2() { return launch_dl<2, L_KV, L_IMW>; }
+GemmLaunchFn dl_convwi_launcher_cfg2() { return launch_dl<2, L_KVI, L_IMW>; }
 GemmLaunchFn dl_rowsum_launcher_cfg2() { return launch_dl<2, L_MV, L_MV, true>; }
 #elif MT_CFG == 3
 GemmLaunchFn dl_launcher_cfg3(int la, int lb) {
@@ -82,6 +86,7 @@ GemmLaunchFn dl_conv_launcher_cfg3() { return launch_dl<3, L_KV, L_IM>; }
 GemmLaunchFn dl_convr_launcher_cfg3() { return launch_dl<3, L_KV, L_IMR>; }
 GemmLaunchFn dl_convh_launcher_cfg3() { return launch_dlh<3>; }
 GemmLaunchFn dl_convw_launcher_cfg3() { return launch_dl<3, L_KV, L_IMW>; }
+GemmLaunchFn dl_convwi_launcher_cfg3() { return launch_dl<3, L_KVI, L_IMW>; }
 GemmLaunchFn dl_rowsum_launcher_cfg3() { return launch_dl<3, L_MV, L_MV, true>; }
 #else
 #error "unknown MT_CFG"

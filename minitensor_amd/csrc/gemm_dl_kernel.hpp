@@ -61,6 +61,16 @@ __device__ __forceinline__ int kswz(int r) { return (r >> 2) & 3; }
 static __device__ const float __attribute__((aligned(16))) dl_zero_page[4] = {0.f, 0.f, 0.f,
                                                                               0.f};
 
+// n / d for 0 <= n < 2^31 and d >= 1 with a double reciprocal rd = 1/d and
+// one upward correction (the product is within 2^-52 relative of n/d, so its
+// truncation is the quotient or one less, never more): a few vector
+// instructions where the integer division costs about thirty.
+__device__ __forceinline__ int div_by(int n, int d, double rd) {
+    int q = (int)((double)n * rd);
+    q += n - q * d >= d;
+    return q;
+}
+
 template <int L, int BMN, int NW>
 struct DlLoader {
     using T = DlTile<L, BMN, NW>;
@@ -117,6 +127,53 @@ struct DlLoader {
             const float* s = kofs[j] < klen - chunk * 16 ? src[j] + chunk * kstep : dl_zero_page;
             __builtin_amdgcn_global_load_lds(
                 (const void __attribute__((address_space(1)))*)s,
+                (void __attribute__((address_space(3)))*)(tile + q * 256), 16, 0, 0);
+        }
+    }
+};
+
+// A operand of layout L_KVI (the convolution weight gradient's dY, read in
+// NCHW): k-contiguous rows that restart every a_hw k at the next image, in
+// the L_KV tile layout.  A lane's 16 bytes are four consecutive k of one
+// image (the host guarantees a_hw % 4 == 0, K % 16 == 0 and 16-byte aligned
+// rows and images), so its source is the image (div_by) plus the row plus
+// k % a_hw, recomputed from the chunk index on every issue (a re-fetched
+// chunk reads the same bytes).
+template <int BMN, int NW>
+struct DlKviLoader {
+    using T = DlTile<L_KV, BMN, NW>;
+    const float* row[T::per_wave];   // X + row*a_mn of each instruction's row
+    int kofs[T::per_wave];           // k of this lane's 16 bytes within a chunk
+    int k0, hw;
+    double rhw;
+    int64_t img;
+
+    __device__ __forceinline__ void init(const GemmParams& p, const float* X, int MN, int mn0,
+                                         int kb, int wave, int lane) {
+        k0 = kb;
+        hw = p.a_hw;
+        rhw = 1.0 / (double)p.a_hw;
+        img = p.a_img;
+#pragma unroll
+        for (int j = 0; j < T::per_wave; ++j) {
+            const int q = j * NW + wave;
+            const int r = q * 16 + (lane >> 2);
+            const int g = (lane & 3) ^ kswz(r);
+            const int64_t rr = min((int64_t)mn0 + r, (int64_t)MN - 1);
+            row[j] = X + rr * p.a_mn;
+            kofs[j] = g * 4;
+        }
+    }
+
+    __device__ __forceinline__ void issue(float* tile, int chunk, int wave) const {
+#pragma unroll
+        for (int j = 0; j < T::per_wave; ++j) {
+            const int q = j * NW + wave;
+            const int k = k0 + chunk * 16 + kofs[j];
+            const int im = div_by(k, hw, rhw);
+            const float* src = row[j] + (int64_t)im * img + (k - im * hw);
+            __builtin_amdgcn_global_load_lds(
+                (const void __attribute__((address_space(1)))*)src,
                 (void __attribute__((address_space(3)))*)(tile + q * 256), 16, 0, 0);
         }
     }
@@ -345,6 +402,7 @@ struct DlImwLoader {
     int dr[T::per_wave], ds[T::per_wave], ci[T::per_wave];   // tap - pad, channel
     bool nok[T::per_wave];        // column inside N
     int k0, k_end;
+    double rhw, rwo;              // 1 / (ho*wo), 1 / wo
     ConvGeom g;
 
     __device__ __forceinline__ void init(const GemmParams& p, const float* Xt, int n0, int kb,
@@ -353,6 +411,8 @@ struct DlImwLoader {
         X = Xt;
         k0 = kb;
         k_end = kend;
+        rhw = 1.0 / (double)(g.ho * g.wo);
+        rwo = 1.0 / (double)g.wo;
 #pragma unroll
         for (int j = 0; j < T::per_wave; ++j) {
             const int e = (j * NW + wave) * 256 + lane * 4;
@@ -373,8 +433,8 @@ struct DlImwLoader {
         for (int j = 0; j < T::per_wave; ++j) {
             const int q = j * NW + wave;
             const int k = k0 + chunk * 16 + kr[j];
-            const int img = k / hw, rem = k - img * hw;
-            const int oh = rem / g.wo, ow = rem - oh * g.wo;
+            const int img = div_by(k, hw, rhw), rem = k - img * hw;
+            const int oh = div_by(rem, g.wo, rwo), ow = rem - oh * g.wo;
             const int ih = oh * g.stride + dr[j], iw = ow * g.stride + ds[j];
             const bool ok = nok[j] && k < k_end && (unsigned)ih < (unsigned)g.h &&
                             (unsigned)iw < (unsigned)g.w;
@@ -471,7 +531,9 @@ gemm_f32_dl(GemmParams p) {
     constexpr int MB = WM / 32, NB = WN / 32;
     static_assert(STAGES >= 2, "the ring needs at least two slots");
     static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be 32-aligned");
-    using TA = DlTile<LA, BM, NW>;
+    constexpr bool kvi = (LA == L_KVI);   // A split into images (no partial chunks)
+    constexpr int LAF = kvi ? L_KV : LA;  // LDS layout of A's tile
+    using TA = DlTile<LAF, BM, NW>;
     using TB = DlTile<LB, BN, NW>;
     constexpr bool imr = (LB == L_IMR);   // B moved by 4-byte DMA
     constexpr int STAGE = TA::floats + TB::floats;
@@ -525,15 +587,16 @@ gemm_f32_dl(GemmParams p) {
                 for (int s = 0; s < 8; ++s) rsum[i] += fa[i][s];
     };
 
-    DlTail<LA, BM, NT> ta;
+    DlTail<LAF, BM, NT> ta;
     std::conditional_t<imw, DlImwTail<BN, NT>, DlTail<LBF, BN, NT>> tb;
-    DlLoader<LA, BM, NW> la;
+    std::conditional_t<kvi, DlKviLoader<BM, NW>, DlLoader<LA, BM, NW>> la;
     std::conditional_t<
         im, DlImLoader<BN, NW>,
         std::conditional_t<imw, DlImwLoader<BN, NW>,
                            std::conditional_t<imr, DlImrLoader<BN, NW>, DlLoader<LBF, BN, NW>>>>
         lb;
-    la.init(Ab, p.a_mn, p.a_k, p.M, m0, k_begin, wave, lane);
+    if constexpr (kvi) la.init(p, Ab, p.M, m0, k_begin, wave, lane);
+    else la.init(Ab, p.a_mn, p.a_k, p.M, m0, k_begin, wave, lane);
     if constexpr (im || imw || imr) lb.init(p, Bb, n0, k_begin, k_end, wave, lane);
     else lb.init(Bb, p.b_mn, p.b_k, p.N, n0, k_begin, wave, lane);
     if (tail) {
@@ -567,7 +630,7 @@ gemm_f32_dl(GemmParams p) {
         }
         __builtin_amdgcn_s_barrier();
         float fa[MB][8], fb[NB][8];
-        dl_frags<LA, BM, MB>(st, ra, lane, fa);
+        dl_frags<LAF, BM, MB>(st, ra, lane, fa);
         dl_frags<LBF, BN, NB>(st + TA::floats, rb, lane, fb);
         mfma_chunk<MB, NB>(acc, fa, fb);
         add_rows(fa);
@@ -587,7 +650,7 @@ gemm_f32_dl(GemmParams p) {
         }
         const float* At = smem + (kt % STAGES) * STAGE;
         float fa[MB][8], fb[NB][8];
-        dl_frags<LA, BM, MB>(At, ra, lane, fa);
+        dl_frags<LAF, BM, MB>(At, ra, lane, fa);
         dl_frags<LBF, BN, NB>(At + TA::floats, rb, lane, fb);
         mfma_chunk<MB, NB>(acc, fa, fb);
         add_rows(fa);

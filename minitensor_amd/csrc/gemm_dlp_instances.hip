@@ -1,7 +1,7 @@
 // gemm_dlp_instances.hip -- instantiates gemm_f32_dlp (direct-to-LDS with
 // fragment prefetch) for direct-to-LDS configurations 4-6, with and
 // without a partial last K-chunk, for the 2x2 vector operand layouts and the
-// convolution weight gradient (A = dY k-contiguous, B = L_IMW).
+// convolution weight gradient (A = dY k-contiguous or read in NCHW, B = L_IMW).
 #include "gemm_configs.hpp"
 #include "gemm_dlp_kernel.hpp"
 
@@ -28,6 +28,13 @@ GemmLaunchFn dlp_convw_launcher(int cfg, bool tail) {
         {launch_dlp<5, false, L_KV, L_IMW>, launch_dlp<5, true, L_KV, L_IMW>},
         {launch_dlp<6, false, L_KV, L_IMW>, launch_dlp<6, true, L_KV, L_IMW>}};
     return table[cfg - 4][tail];
+}
+
+GemmLaunchFn dlp_convwi_launcher(int cfg) {
+    static const GemmLaunchFn table[3] = {launch_dlp<4, false, L_KVI, L_IMW>,
+                                          launch_dlp<5, false, L_KVI, L_IMW>,
+                                          launch_dlp<6, false, L_KVI, L_IMW>};
+    return table[cfg - 4];
 }
 
 GemmLaunchFn dlp_launcher(int cfg, bool tail, int la, int lb) {

@@ -101,11 +101,15 @@ gemm_f32_dlp(GemmParams p) {
     constexpr int NW = (BM / WM) * WAVES_N;
     constexpr int MB = WM / 32, NB = WN / 32;
     static_assert(STAGES >= 2, "the ring needs at least two slots");
-    static_assert((LA == L_KV || LA == L_MV) && (LB == L_KV || LB == L_MV || LB == L_IMW),
+    static_assert((LA == L_KV || LA == L_MV || LA == L_KVI) &&
+                      (LB == L_KV || LB == L_MV || LB == L_IMW),
                   "vector operand layouts or the implicit im2col-transpose operand");
     constexpr bool imw = (LB == L_IMW);
     constexpr int LBF = imw ? L_MV : LB;     // LDS layout of B's tile
-    using TA = DlTile<LA, BM, NW>;
+    constexpr bool kvi = (LA == L_KVI);      // A split into images (no partial chunks)
+    static_assert(!(kvi && TAIL), "the image-split A operand's K ranges hold whole chunks");
+    constexpr int LAF = kvi ? L_KV : LA;     // LDS layout of A's tile
+    using TA = DlTile<LAF, BM, NW>;
     using TB = DlTile<LB, BN, NW>;
     constexpr int STAGE = TA::floats + TB::floats;
     constexpr int LOADS = TA::per_wave + TB::per_wave;   // wave instructions per chunk
@@ -134,14 +138,15 @@ gemm_f32_dlp(GemmParams p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    DlLoader<LA, BM, NW> la;
+    std::conditional_t<kvi, DlKviLoader<BM, NW>, DlLoader<LA, BM, NW>> la;
     std::conditional_t<imw, DlImwLoader<BN, NW>, DlLoader<LB, BN, NW>> lb;
-    la.init(Ab, p.a_mn, p.a_k, p.M, m0, k_begin, wave, lane);
+    if constexpr (kvi) la.init(p, Ab, p.M, m0, k_begin, wave, lane);
+    else la.init(Ab, p.a_mn, p.a_k, p.M, m0, k_begin, wave, lane);
     if constexpr (imw) lb.init(p, Bb, n0, k_begin, k_end, wave, lane);
     else lb.init(Bb, p.b_mn, p.b_k, p.N, n0, k_begin, wave, lane);
     // (The implicit operand's loader tests k < k_end itself, on every chunk.)
     auto issue = [&](float* slot, int chunk) {
-        if constexpr (TAIL) la.issue_bounded(slot, chunk, wave, klen);
+        if constexpr (TAIL && !kvi) la.issue_bounded(slot, chunk, wave, klen);
         else la.issue(slot, chunk, wave);
         if constexpr (TAIL && !imw) lb.issue_bounded(slot + TA::floats, chunk, wave, klen);
         else lb.issue(slot + TA::floats, chunk, wave);
@@ -155,7 +160,7 @@ gemm_f32_dlp(GemmParams p) {
     __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(LOADS * (STAGES - 1)));
     __builtin_amdgcn_s_barrier();
     float fa0[MB][8], fb0[NB][8], fa1[MB][8], fb1[NB][8];
-    dl_frags<LA, BM, MB>(smem, ra, lane, fa0);
+    dl_frags<LAF, BM, MB>(smem, ra, lane, fa0);
     dl_frags<LBF, BN, NB>(smem + TA::floats, rb, lane, fb0);
 
     // Step kt: multiply chunk kt (registers ca/cb) while reading chunk kt+1
@@ -179,7 +184,7 @@ gemm_f32_dlp(GemmParams p) {
         const int cn = min(kt + STAGES, nk - 1);
         issue(refill, cn);
         const float* const next = smem + ((kt + 1) % STAGES) * STAGE;
-        dl_frags<LA, BM, MB>(next, ra, lane, na);
+        dl_frags<LAF, BM, MB>(next, ra, lane, na);
         dl_frags<LBF, BN, NB>(next + TA::floats, rb, lane, nb);
         mfma_steps<MB, NB, PRE, 8>(acc, ca, cb);
         if constexpr (MB * NB * 8 >= 128) dlp_interleave<(8 - PRE) * MB * NB>();

@@ -59,8 +59,11 @@ enum : int {
     L_IMW = 5, // B only, direct-to-LDS kernel: implicit im2colᵀ (conv weight gradient)
     L_IMR = 6, // B only, direct-to-LDS kernel: implicit im2col of an NCHW view, K order
                // (ci, r, s), gathered by 4-byte DMA
-    L_IMH = 7  // B only (gemm_f32_dlh): L_IMR's operand built in LDS from a halo
+    L_IMH = 7, // B only (gemm_f32_dlh): L_IMR's operand built in LDS from a halo
                // patch of the input
+    L_KVI = 8  // A only, direct-to-LDS kernels: k-contiguous rows split into images,
+               // A(m, k) = A[(k / a_hw)*a_img + m*a_mn + k % a_hw] (dY of a
+               // convolution read in NCHW as [c_out][n*h_out*w_out])
 };
 
 // Geometry of an implicit-im2col B operand over a channels-last input
@@ -129,6 +132,7 @@ __host__ __device__ inline int dlh_lds_floats(const ConvGeom& g) {
 
 struct GemmParams {
     const float* A; int64_t a_mn, a_k, a_b;   // A(m,k) = A[m*a_mn + k*a_k + b*a_b]
+    int64_t a_img; int a_hw;                  // L_KVI: image stride, k per image
     const float* B; int64_t b_mn, b_k, b_b;   // B(k,n) = B[n*b_mn + k*b_k + b*b_b]
     float* C; int64_t c_m, c_n, c_b;          // C(m,n) = C[m*c_m + col(n) + b*c_b]
     // col(n) = n*c_n when c_n_inner >= N, otherwise

@@ -360,7 +360,18 @@ GemmLaunchFn rowsum_launcher(int cfg) {
     }
 }
 
-GemmLaunchFn convw_launcher(int cfg, bool ktail) {
+// kvi: A is dY read in NCHW (L_KVI, whole chunks only).
+GemmLaunchFn convw_launcher(int cfg, bool ktail, bool kvi) {
+    if (kvi) {
+        if (ktail) return nullptr;
+        switch (cfg) {
+            case 0: return dl_convwi_launcher_cfg0();
+            case 1: return dl_convwi_launcher_cfg1();
+            case 2: return dl_convwi_launcher_cfg2();
+            case 3: return dl_convwi_launcher_cfg3();
+            default: return dlp_convwi_launcher(cfg);
+        }
+    }
     switch (cfg) {
         case 0: return dl_convw_launcher_cfg0();
         case 1: return dl_convw_launcher_cfg1();
@@ -679,7 +690,7 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
 
     GemmLaunchFn fn = halo ? convh_launcher(plan.cfg)
                       : lb == L_IM || lb == L_IMR ? conv_launcher(plan.cfg, lb == L_IMR)
-                      : lb == L_IMW         ? convw_launcher(plan.cfg, (K & 15) != 0)
+                      : lb == L_IMW ? convw_launcher(plan.cfg, (K & 15) != 0, la == L_KVI)
                       : p.rowsum != nullptr ? rowsum_launcher(plan.cfg)
                                             : pick_launcher(plan, la, lb, (K & 15) != 0);
     if (fn == nullptr) return MT_ERR_UNSUPPORTED;
@@ -1630,14 +1641,25 @@ int conv_bwd_weight(const mt_conv2d_desc* d, const float* input, const float* gr
         float* dyt = reinterpret_cast<float*>(wsp + xt_b);
         int64_t st[4];
         dense_strides(d, st);
-        // x -> channels-last and dY [n][c_out][hw] -> dYt [c_out][n][hw], one launch
+        // dY is read in NCHW by the GEMM (L_KVI) when every 16-byte group of a
+        // row is four pixels of one image and K holds whole chunks; else it is
+        // copied to dYt [c_out][n][hw].  x -> channels-last in the same launch.
+        const bool kvi = (np & 15) == 0 && (hw & 3) == 0 && np < ((int64_t)1 << 24) &&
+                         ((uintptr_t)grad_out & 15u) == 0;
         if (launch_transposes(tjob(input, st[0], st[1], st[2], st[3], d->w, d->c_in, d->h * d->w,
                                    d->n, xt),
-                              tjob(grad_out, hw, 1, d->c_out * hw, 0, 1, hw, d->n, d->c_out, dyt),
+                              kvi ? TJob{}
+                                  : tjob(grad_out, hw, 1, d->c_out * hw, 0, 1, hw, d->n, d->c_out,
+                                         dyt),
                               s) != hipSuccess)
             return MT_ERR_HIP;
         GemmParams p{};
-        p.A = dyt; p.a_mn = np; p.a_k = 1; p.a_b = 0;
+        if (kvi) {
+            p.A = grad_out; p.a_mn = hw; p.a_k = 1; p.a_b = 0;
+            p.a_img = d->c_out * hw; p.a_hw = (int)hw;
+        } else {
+            p.A = dyt; p.a_mn = np; p.a_k = 1; p.a_b = 0;
+        }
         p.B = xt;
         p.C = grad_weight; p.c_m = kg; p.c_n = d->kh * d->kw; p.c_b = 0;
         p.c_n_inner = d->c_in; p.c_n_outer = 1;
@@ -1653,8 +1675,8 @@ int conv_bwd_weight(const mt_conv2d_desc* d, const float* input, const float* gr
             p.csum_src = grad_out; p.csum = grad_bias; p.csum_n = (int)d->n;
             p.csum_hw = hw; p.csum_beta = beta_b;
         }
-        const int rc =
-            launch_gemm(p, true, L_KV, L_IMW, wsp + xt_b + dyt_b, ws_bytes - xt_b - dyt_b, s);
+        const int rc = launch_gemm(p, true, kvi ? L_KVI : L_KV, L_IMW, wsp + xt_b + dyt_b,
+                                   ws_bytes - xt_b - dyt_b, s);
         *db_done = rc == MT_OK && p.csum != nullptr;
         return rc;
     }
