@@ -307,10 +307,12 @@ __device__ __forceinline__ f32x16 mfma_32x32x2(float a, float b, const f32x16& c
 }
 
 // Column offset col(n) of the output (see GemmParams).
+// (c_n_inner < N < 2^31 when the scatter applies: a 32-bit division.)
 __device__ __forceinline__ int64_t col_offset(const GemmParams& p, int n) {
     if (p.c_n_inner >= p.N) return (int64_t)n * p.c_n;
-    const int64_t no = n / p.c_n_inner, ni = n - no * p.c_n_inner;
-    return no * p.c_n_outer + ni * p.c_n;
+    const unsigned inner = (unsigned)p.c_n_inner;
+    const unsigned no = (unsigned)n / inner, ni = (unsigned)n - no * inner;
+    return (int64_t)no * p.c_n_outer + (int64_t)ni * p.c_n;
 }
 
 // s_waitcnt immediate (gfx9 encoding): vmcnt(n), lgkmcnt(0), expcnt unconstrained.
