@@ -105,6 +105,7 @@ const char* layout_name(int l) {
         case L_IMW: return "im2colT";
         case L_IMR: return "im2col_nchw";
         case L_IMH: return "im2col_halo";
+        case L_KVI: return "kv_nchw";
         case L_KS: return "ks";
         default: return "ms";
     }
