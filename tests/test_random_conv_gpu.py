@@ -115,3 +115,73 @@ def test_random_conv_auto_plan(dev, case):
     assert_close(dW, wdw, n * ho * wo, amax(dy), amax(x), f"random conv dW {case}",
                  extra=2e-6 * (1.0 + beta_w) if beta_w != 0.0 else 0.0)
     assert_close(db, wdb, n * ho * wo, amax(dy), 1.0, f"random conv db {case}")
+
+
+# The halo-patch kernel under forced tile configurations and split factors
+# (a forced configuration takes it wherever its patches fit): NCHW-view
+# geometries with c_in not a multiple of 16 (the channels-last kernel takes
+# those) and c_in*kh*kw % 4 == 0, at least two taps, strides 1-3, padding
+# 0-2, dense or channel-slice inputs, and the dX of the stride-1 square
+# cases through the same kernel.
+def _halo_case(rng, i: int) -> dict:
+    while True:
+        kh = int(rng.integers(1, 6))
+        kw = kh if rng.random() < 0.5 else int(rng.integers(1, 6))
+        c = int(rng.integers(1, 41))
+        if c % 16 == 0 or (c * kh * kw) % 4 or kh * kw < 2:
+            continue
+        d = dict(n=int(rng.integers(1, 5)), c=c, co=int(rng.integers(1, 49)),
+                 h=int(rng.integers(2, 20)), w=int(rng.integers(2, 30)), kh=kh, kw=kw,
+                 stride=int(rng.integers(1, 4)), pad=int(rng.integers(0, 3)),
+                 cfg=int(rng.integers(0, 4)), split=int(rng.choice([1, 2, 3, 5])),
+                 view=str(rng.choice(["dense", "channel_slice"])), seed=7000 + 10 * i)
+        if (oracle.conv_out(d["h"], d["pad"], kh, d["stride"]) > 0
+                and oracle.conv_out(d["w"], d["pad"], kw, d["stride"]) > 0):
+            return d
+
+
+N_HALO = 30
+_hrng = np.random.default_rng(20261203)
+HALO_CASES = [_halo_case(_hrng, i) for i in range(N_HALO)]
+_halo_seen = []
+
+
+@pytest.mark.parametrize("case", HALO_CASES, ids=[f"h{i}" for i in range(N_HALO)])
+def test_random_conv_halo_forced(dev, case):
+    n, c, h, wd, co = case["n"], case["c"], case["h"], case["w"], case["co"]
+    kh, kw, stride, pad, seed = case["kh"], case["kw"], case["stride"], case["pad"], case["seed"]
+    x = oracle.normal((n, c, h, wd), seed)
+    w = oracle.normal((co, c, kh, kw), seed + 1)
+    b = oracle.normal((co,), seed + 2)
+    X = _input_view(x, case["view"], seed, dev)
+    W, Bt = torch.from_numpy(w).to(dev), torch.from_numpy(b).to(dev)
+    with mt.forced_config(mt.FAMILY_DL, case["cfg"], case["split"]):
+        y = mt.conv2d(X, W, Bt, stride, pad)
+        cfg = mt.last_config()
+        y2 = mt.conv2d(X, W, Bt, stride, pad)
+    torch.cuda.synchronize()
+    print(f"[case] {case} -> forward {cfg}", flush=True)
+    _halo_seen.append("b=im2col_halo" in cfg)
+    y, y2 = y.cpu().numpy(), y2.cpu().numpy()
+    assert np.array_equal(y.view(np.uint32), y2.view(np.uint32)), "forward not deterministic"
+    assert_close(y, oracle.conv2d(x, w, b, stride, pad), c * kh * kw, amax(x), amax(w),
+                 f"forced halo conv {case}", extra=2e-6 * (1.0 + amax(b)))
+    if stride == 1 and kh == kw and pad <= kh - 1 and (co * kh * kw) % 4 == 0 and co % 16:
+        ho, wo = oracle.conv_out(h, pad, kh, 1), oracle.conv_out(wd, pad, kw, 1)
+        dy = oracle.normal((n, co, ho, wo), seed + 3)
+        with mt.forced_config(mt.FAMILY_DL, case["cfg"], case["split"]):
+            dX, _, _ = mt.conv2d_backward(torch.from_numpy(x).to(dev), W,
+                                          torch.from_numpy(dy).to(dev), 1, pad,
+                                          need_dw=False, need_db=False)
+            print(f"[case] dX {mt.last_config()}", flush=True)
+        wdx, _, _ = oracle.conv2d_backward(x, w, dy, 1, pad)
+        assert_close(dX.cpu().numpy(), wdx, co * kh * kw, amax(dy), amax(w),
+                     f"forced halo dX {case}")
+
+
+def test_random_conv_halo_forced_coverage():
+    """Most of the forced draws above ran the halo kernel (the rest had bands
+    too large for their tile)."""
+    if len(_halo_seen) < N_HALO:
+        pytest.skip("the forced halo draws did not all run in this session")
+    assert sum(_halo_seen) >= N_HALO // 2, _halo_seen
