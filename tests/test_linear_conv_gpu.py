@@ -594,3 +594,54 @@ def test_conv_backward_weight_implicit(dev, n, c, h, wd, co, kh, kw, stride, pad
     mt.conv2d_backward(X, W, dY, stride, pad, need_dx=False, need_db=False, dw=dw, beta_w=1.0)
     assert_close(sync_np(dw), 2 * wdw, n * ho * wo, amax(dy), amax(x), "implicit conv dW += ",
                  extra=1e-6)
+
+
+# The weight gradient reads dY in NCHW as its A operand (a=kv_nchw) when a
+# 16-byte group of a row is four pixels of one image (h_out*w_out % 4 == 0),
+# K = n*h_out*w_out holds whole chunks (% 16 == 0) and dY is 16-byte aligned;
+# otherwise dY is first copied to [c_out][n*h_out*w_out] (a=kv).  Both,
+# including K ranges that start inside an image and split factors that cut
+# images, against the oracle, and db summed alongside.
+@pytest.mark.parametrize("n,c,h,wd,co,split,expect", [
+    (4, 8, 6, 6, 24, 1, "a=kv_nchw"),    # hw 36, K 144
+    (8, 12, 5, 8, 40, 3, "a=kv_nchw"),   # hw 40, K 320: splits cut images
+    (3, 8, 6, 6, 24, 1, "a=kv "),        # K 108: not whole chunks
+    (4, 8, 5, 5, 24, 1, "a=kv "),        # hw 25: groups straddle images
+])
+def test_conv_dw_dy_layout(dev, n, c, h, wd, co, split, expect):
+    x = oracle.normal((n, c, h, wd), 440 + n)
+    w = oracle.normal((co, c, 3, 3), 441)
+    dy = oracle.normal((n, co, h, wd), 442)
+    X, W, dY = g(x, dev), g(w, dev), g(dy, dev)
+    _, wdw, wdb = oracle.conv2d_backward(x, w, dy, 1, 1)
+    with mt.forced_config(mt.FAMILY_DL, 3, split):
+        _, dw, db = mt.conv2d_backward(X, W, dY, 1, 1, need_dx=False)
+        cfg = mt.last_config()
+    print(f"[config] dW {cfg}")
+    assert expect in cfg + " ", cfg
+    assert_close(sync_np(dw), wdw, n * h * wd, amax(dy), amax(x), "dW with dY layout")
+    assert_close(sync_np(db), wdb, n * h * wd, amax(dy), 1.0, "db with dY layout")
+
+
+def test_conv_dw_dy_unaligned(dev):
+    """A dY view that is not 16-byte aligned is copied, not read in place."""
+    n, c, h, wd, co = 4, 8, 6, 6, 24
+    x = oracle.normal((n, c, h, wd), 450)
+    w = oracle.normal((co, c, 3, 3), 451)
+    dy = oracle.normal((n, co, h, wd), 452)
+    buf = torch.zeros(dy.size + 1, dtype=torch.float32, device=dev)
+    buf[1:] = g(dy.reshape(-1), dev)
+    dY = buf[1:].view(n, co, h, wd)
+    assert dY.data_ptr() % 16 != 0
+    d = mt.Conv2dDesc(n, c, h, wd, co, 3, 3, 1, 1)
+    ws = mt.workspace(mt.lib().mt_conv2d_bwd_workspace_f32(ctypes.byref(d)), dev)
+    dW = torch.empty(co, c, 3, 3, device=dev)
+    X = g(x, dev)
+    assert mt.lib().mt_conv2d_bwd_weight_f32(ctypes.byref(d), X.data_ptr(),
+                                             dY.data_ptr(), dW.data_ptr(), 0.0, ws.data_ptr(),
+                                             ws.numel(), None) == 0
+    cfg = mt.last_config()
+    print(f"[config] dW {cfg}")
+    assert "a=kv " in cfg + " ", cfg
+    _, wdw, _ = oracle.conv2d_backward(x, w, dy, 1, 1)
+    assert_close(sync_np(dW), wdw, n * h * wd, amax(dy), amax(x), "dW, unaligned dY")
