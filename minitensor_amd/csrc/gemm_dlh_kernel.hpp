@@ -175,10 +175,18 @@ gemm_f32_dlh(GemmParams p, HaloTable ht) {
     const int J0 = k_begin >> 4;              // global index of the first chunk
     const int Gf = J0 / khw;                  // its patch
     const int Gl = nk > 0 ? (J0 + nk - 1) / khw : Gf;
+    // APF: the A fragments are also read a chunk ahead (A's DMA then runs two
+    // chunks ahead, in the slot whose fragments are already in registers).
+    // It pays for wave tiles of at most two 32x32 blocks, whose few MFMAs per
+    // chunk cannot cover the A reads after the barrier (128x128 tiles: 53.1
+    // against 55.3 us for a c_in 120 3x3 layer); for four blocks it was
+    // slower (256x128: 84.9 against 84.2 us, c_in 252).
+    constexpr bool APF = MB * NB <= 2;
     if (nk > 0) {
         issue_patch(Gf, patch);
         if (Gl > Gf) issue_patch(Gf + 1, patch + pst);
         issue_a(0);
+        if (APF && nk > 1) issue_a(1);
     }
 
     // The B fragments of chunk kt+1 are read while chunk kt is multiplied:
@@ -190,39 +198,63 @@ gemm_f32_dlh(GemmParams p, HaloTable ht) {
     // no use but stays inside the buffers.  Two fragment sets alternate.
     int q_in = J0 - Gf * khw;                 // chunk index within its patch
     int G = Gf;
-    auto step = [&](int kt, float (&cur)[NB][8], float (&nxt)[NB][8]) {
-        // Everything issued so far has landed (two slots: nothing newer is in
-        // flight), then everyone's; the barrier also retires every wave's
-        // reads of the A slot and of the patch buffer refilled below.
+    constexpr int NMF = 8 * MB * NB, NRA = 2 * MB, NRB = 8 * NB;
+    float fa0[MB][8], fa1[MB][8], fb0[NB][8], fb1[NB][8];
+    if constexpr (APF) {
+        // chunk 0's fragments; A(1) has landed too, for the first step
         __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
         __builtin_amdgcn_s_barrier();
-        if (kt + 1 < nk) issue_a(kt + 1);
+        dl_frags<L_KV, BM, MB>(smem, ra, lane, fa0);
+        frag_b(q_in, patch, fb0);
+    }
+    auto step = [&](int kt, float (&fac)[MB][8], float (&fbc)[NB][8], float (&fan)[MB][8],
+                    float (&fbn)[NB][8]) {
+        // Everything issued so far has landed (nothing newer is in flight),
+        // then everyone's; the barrier also retires every wave's reads of the
+        // A slot and of the patch buffer refilled below.
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+        __builtin_amdgcn_s_barrier();
+        if constexpr (APF) {
+            if (kt + 2 < nk) issue_a(kt + 2);
+        } else {
+            if (kt + 1 < nk) issue_a(kt + 1);
+        }
         if (kt > 0 && q_in == 0 && G < Gl) issue_patch(G + 1, patch + ((G + 1 - Gf) & 1) * pst);
-        if (kt == 0) frag_b(q_in, patch, cur);
-        float fa[MB][8];
-        dl_frags<L_KV, BM, MB>(smem + (kt & 1) * TA::floats, ra, lane, fa);
+        if constexpr (!APF) {
+            if (kt == 0) frag_b(q_in, patch, fbc);
+            dl_frags<L_KV, BM, MB>(smem + (kt & 1) * TA::floats, ra, lane, fac);
+        }
         if (++q_in == khw) {
             q_in = 0;
             ++G;
         }
-        frag_b(q_in, patch + ((G - Gf) & 1) * pst, nxt);
-        mfma_chunk<MB, NB>(acc, fa, cur);
+        if constexpr (APF) dl_frags<L_KV, BM, MB>(smem + ((kt + 1) & 1) * TA::floats, ra, lane, fan);
+        frag_b(q_in, patch + ((G - Gf) & 1) * pst, fbn);
+        mfma_chunk<MB, NB>(acc, fac, fbc);
         // Interleave the next chunk's fragment reads (and their address
-        // arithmetic) with this chunk's MFMAs, after this chunk's A reads,
-        // so that they run in the MFMAs' shadow.
-        __builtin_amdgcn_sched_group_barrier(0x100, 2 * MB, 0);
+        // arithmetic) with this chunk's MFMAs, after this chunk's own A reads
+        // (without APF), so that they run in the MFMAs' shadow.
+        if constexpr (APF && NMF >= NRA + NRB) {
 #pragma unroll
-        for (int i = 0; i < 8 * NB; ++i) {
+            for (int i = 0; i < NRA; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+        } else {
+            __builtin_amdgcn_sched_group_barrier(0x100, NRA, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < NRB; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, 8 * MB * NB - 8 * NB, 0);
+        constexpr int rest = NMF - NRB - (APF && NMF >= NRA + NRB ? NRA : 0);
+        if constexpr (rest > 0) __builtin_amdgcn_sched_group_barrier(0x008, rest, 0);
     };
-    float fb0[NB][8], fb1[NB][8];
     for (int kt = 0; kt < nk; kt += 2) {
-        step(kt, fb0, fb1);
-        if (kt + 1 < nk) step(kt + 1, fb1, fb0);
+        step(kt, fa0, fb0, fa1, fb1);
+        if (kt + 1 < nk) step(kt + 1, fa1, fb1, fa0, fb0);
     }
 
     store_tile_lds<MB, NB, NW, WAVES_N, WM, WN, STAGING>(p, acc, smem, m0, n0, wave, lane,
