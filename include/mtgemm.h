@@ -246,8 +246,8 @@ int mt_gemm_config_count(int family);
  * thread whose operands that family takes; the others keep the cost model.
  * (Direct-to-LDS configurations 4-6, the fragment-prefetching kernel with
  * 256x256, 64x64 and 128x128 tiles, take the convolution weight gradient's
- * implicit operand but not the forward convolution's implicit im2col
- * operand or fused row sums.)
+ * implicit operand and the fused row sums but not the forward convolution's
+ * implicit im2col operand.)
  * A forced direct-to-LDS configuration also builds the im2col operand of a
  * convolution over an NCHW view from halo patches in LDS whenever the patches
  * fit, without the rule that otherwise keeps the per-chunk gather where the

@@ -73,6 +73,8 @@ GemmLaunchFn dl_launcher_cfg3(int la, int lb);
 // Configurations 4-6 (gemm_f32_dlp); la, lb in {L_KV, L_MV}; tail: K is
 // not a multiple of 16.
 GemmLaunchFn dlp_launcher(int cfg, bool tail, int la, int lb);
+// Configurations 4-6 with the row sums of A (GemmParams::rowsum); A and B L_MV.
+GemmLaunchFn dlp_rowsum_launcher(int cfg, bool tail);
 // Configurations 4-6 for the convolution weight gradient (A L_KV, B L_IMW).
 GemmLaunchFn dlp_convw_launcher(int cfg, bool tail);
 // Configurations 4-6 for the weight gradient with A = dY in NCHW (L_KVI).

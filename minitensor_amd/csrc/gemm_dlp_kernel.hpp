@@ -93,7 +93,10 @@ __device__ __forceinline__ void mfma_steps(f32x16 (&acc)[MB][NB], const float (&
 
 // WPE: waves per SIMD the register allocation targets (1 lets the 128x128
 // wave tile keep its 256 accumulators in AGPRs beside 256 VGPRs).
-template <int BM, int BN, int WM, int WN, int LA, int LB, int STAGES, int WPE, bool TAIL>
+// RS: also produce the row sums of A (GemmParams::rowsum), as gemm_f32_dl's
+// row-sum form does: same waves, same order of additions.
+template <int BM, int BN, int WM, int WN, int LA, int LB, int STAGES, int WPE, bool TAIL,
+          bool RS = false>
 __global__ void __launch_bounds__((BM / WM) * (BN / WN) * 64)
 __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 gemm_f32_dlp(GemmParams p) {
@@ -137,6 +140,22 @@ gemm_f32_dlp(GemmParams p) {
         for (int j = 0; j < NB; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    // Fused row sums of A: the waves of the first wave column of the first
+    // tile column see every A fragment of their rows exactly once (a partial
+    // last chunk holds zeros past K; re-fetched chunks are not multiplied).
+    static_assert(!RS || (LA == L_MV && LB == L_MV), "row sums: two mn-contiguous operands");
+    const bool do_rs = RS && id.tn == 0 && (wave % WAVES_N) == 0;
+    float rsum[MB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) rsum[i] = 0.f;
+    auto add_rows = [&](const float (&fa)[MB][8]) {
+        if (RS && do_rs)
+#pragma unroll
+            for (int i = 0; i < MB; ++i)
+#pragma unroll
+                for (int s = 0; s < 8; ++s) rsum[i] += fa[i][s];
+    };
 
     std::conditional_t<kvi, DlKviLoader<BM, NW>, DlLoader<LA, BM, NW>> la;
     std::conditional_t<imw, DlImwLoader<BN, NW>, DlLoader<LB, BN, NW>> lb;
@@ -189,6 +208,7 @@ gemm_f32_dlp(GemmParams p) {
         mfma_steps<MB, NB, PRE, 8>(acc, ca, cb);
         if constexpr (MB * NB * 8 >= 128) dlp_interleave<(8 - PRE) * MB * NB>();
         else if constexpr (MB == 2 && NB == 1) dlp_interleave_reads<LOADS>();
+        add_rows(ca);
     };
 
     int kt = 0;
@@ -211,6 +231,20 @@ gemm_f32_dlp(GemmParams p) {
             for (int s = 0; s < 8; ++s) fb0[j][s] = fb1[j][s];
     }
     mfma_chunk<MB, NB>(acc, fa0, fb0);
+    add_rows(fa0);
+    if (RS && do_rs) {
+        // lanes c and c+32 hold the two k-halves of row c: combine, then
+        // the lower lane writes (same order for every row: deterministic)
+#pragma unroll
+        for (int i = 0; i < MB; ++i) {
+            const float tot = rsum[i] + __shfl_xor(rsum[i], 32);
+            const int m = m0 + ra + i * 32 + (lane & 31);
+            if (lane < 32 && m < p.M) {
+                float* d = p.rowsum + (int64_t)m * p.rowsum_stride;
+                *d = (p.rowsum_beta != 0.f ? p.rowsum_beta * *d : 0.f) + tot;
+            }
+        }
+    }
     // (store_tile_lds first waits for the re-fetches past the last chunk.)
     store_tile_lds<MB, NB, NW, WAVES_N, WM, WN, STAGES * STAGE>(p, acc, smem, m0, n0, wave, lane,
                                                                 id.split, id.bz);

@@ -348,16 +348,17 @@ bool forced_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dl_ok, boo
     return false;
 }
 
-// The implicit-im2col (L_IM) and row-sum forms exist for DlCfg 0..3 only; the
-// planner never picks the prefetching configurations for them (nullptr is a
-// safety net).  The weight-gradient operand (L_IMW) exists for all.
-GemmLaunchFn rowsum_launcher(int cfg) {
+// The implicit-im2col form (L_IM) exists for DlCfg 0..3 only; the planner
+// never picks the prefetching configurations for it (nullptr is a safety
+// net).  The row-sum form and the weight-gradient operand (L_IMW) exist for
+// all.
+GemmLaunchFn rowsum_launcher(int cfg, bool tail) {
     switch (cfg) {
         case 0: return dl_rowsum_launcher_cfg0();
         case 1: return dl_rowsum_launcher_cfg1();
         case 2: return dl_rowsum_launcher_cfg2();
         case 3: return dl_rowsum_launcher_cfg3();
-        default: return nullptr;
+        default: return dlp_rowsum_launcher(cfg, tail);
     }
 }
 
@@ -642,10 +643,14 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
     p.c_vec = p.c_n == 1 && (N & 3) == 0 && ((uintptr_t)p.C & 15u) == 0 && (p.c_m & 3) == 0 &&
               (batch == 1 || (p.c_b & 3) == 0) &&
               (p.c_n_inner >= N || ((p.c_n_inner & 3) == 0 && (p.c_n_outer & 3) == 0));
+    // Row sums of A are fused only into a direct-to-LDS launch of two
+    // mn-contiguous operands without split-K (the caller sees p.rowsum cleared
+    // and computes them separately).
+    if (batch != 1 || la != L_MV || lb != L_MV) p.rowsum = nullptr;
     // The prefetching configurations' contract: vector layouts or the
-    // weight-gradient operand (not the implicit-im2col one), no fused row
-    // sums, a non-empty K range.
-    const bool wide_ok = dl && lb != L_IM && lb != L_IMR && p.rowsum == nullptr && K > 0;
+    // weight-gradient operand (not the implicit-im2col one), a non-empty K
+    // range.
+    const bool wide_ok = dl && lb != L_IM && lb != L_IMR && K > 0;
     Plan plan;
     const bool forced = forced_plan(M, N, K, batch, dl, !implicit, wide_ok, &plan);
     if (forced) {
@@ -661,11 +666,7 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
             plan = make_plan(M, N, K, batch, device_cu_count(), false, dl, wide_ok, ksw_ok,
                              lb == L_IMW);
     }
-    // Row sums of A are fused only into a direct-to-LDS launch of two
-    // mn-contiguous operands without split-K (the caller sees p.rowsum cleared
-    // and computes them separately).
-    if (!plan.dl || plan.splits > 1 || batch != 1 || la != L_MV || lb != L_MV)
-        p.rowsum = nullptr;
+    if (!plan.dl || plan.splits > 1) p.rowsum = nullptr;
     p.splits = plan.splits;
     p.k_per_split = plan.splits > 1 ? plan.kps : (int)std::max<int64_t>(K, 1);
     p.tiles_m = plan.tiles_m;
@@ -692,7 +693,7 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
     GemmLaunchFn fn = halo ? convh_launcher(plan.cfg)
                       : lb == L_IM || lb == L_IMR ? conv_launcher(plan.cfg, lb == L_IMR)
                       : lb == L_IMW ? convw_launcher(plan.cfg, (K & 15) != 0, la == L_KVI)
-                      : p.rowsum != nullptr ? rowsum_launcher(plan.cfg)
+                      : p.rowsum != nullptr ? rowsum_launcher(plan.cfg, (K & 15) != 0)
                                             : pick_launcher(plan, la, lb, (K & 15) != 0);
     if (fn == nullptr) return MT_ERR_UNSUPPORTED;
     hipError_t e = fn(p, (unsigned)nblocks, stream);

@@ -130,21 +130,31 @@ def test_forced_rs_k0_writes_bias(dev, family):
     np.testing.assert_array_equal(sync_np(C), np.broadcast_to(bias, (33, 40)))
 
 
-@pytest.mark.parametrize("cfg", DL_CONFIGS)
-def test_forced_dl_linear_dw_fused_row_sums(dev, cfg):
+@pytest.mark.parametrize("cfg", DL_CONFIGS + DLPS)
+@pytest.mark.parametrize("rows", [301, 256])
+def test_forced_dl_linear_dw_fused_row_sums(dev, cfg, rows):
     # dW = dYᵀ·X with db = Σ_rows dY fused into the same launch (both operands
-    # mn-contiguous, no split): every direct-to-LDS tile, with a K tail.
-    x = oracle.normal((301, 96), 910 + cfg)
+    # mn-contiguous, no split): every direct-to-LDS tile, with and without a
+    # K tail (K = rows), then accumulated with beta = 1.
+    x = oracle.normal((rows, 96), 910 + cfg)
     w = oracle.normal((72, 96), 920 + cfg, std=0.1)
-    dy = oracle.normal((301, 72), 930 + cfg, std=0.1)
+    dy = oracle.normal((rows, 72), 930 + cfg, std=0.1)
     dw = torch.empty(72, 96, device=dev)
     db = torch.empty(72, device=dev)
     with mt.forced_config(mt.FAMILY_DL, cfg, 1):
         mt.linear_backward(g(dy, dev), g(x, dev), g(w, dev), need_dx=False, dw=dw, db=db)
         check_config(mt.FAMILY_DL, cfg, 1)
     _, wdw, wdb = oracle.linear_backward(dy, x, w)
-    assert_close(sync_np(dw), wdw, 301, amax(dy), amax(x), f"forced dl{cfg} dW")
-    assert_close(sync_np(db), wdb, 301, amax(dy), 1.0, f"forced dl{cfg} fused db")
+    assert_close(sync_np(dw), wdw, rows, amax(dy), amax(x), f"forced dl{cfg} dW")
+    assert_close(sync_np(db), wdb, rows, amax(dy), 1.0, f"forced dl{cfg} fused db")
+    with mt.forced_config(mt.FAMILY_DL, cfg, 1):
+        mt.linear_backward(g(dy, dev), g(x, dev), g(w, dev), need_dx=False, dw=dw, db=db,
+                           beta_w=1.0, beta_b=1.0)
+    # two sums of `rows` products each: twice the bound (4·rows under the root)
+    assert_close(sync_np(db), 2 * wdb, 4 * rows, amax(dy), 1.0,
+                 f"forced dl{cfg} fused db, beta 1")
+    assert_close(sync_np(dw), 2 * wdw, 4 * rows, amax(dy), amax(x),
+                 f"forced dl{cfg} dW, beta 1")
 
 
 @pytest.mark.parametrize("cfg", DL_CONFIGS)
@@ -324,20 +334,7 @@ def _not_dlp(name: str) -> None:
 def test_forced_dlp_outside_its_contract_uses_the_cost_model(dev, DLP):
     # A forced prefetching configuration where its contract does not hold: the
     # launch takes the cost model's plan instead, and the result is still
-    # exact.  The Linear weight gradient with its fused row sums keeps a
-    # row-sum kernel:
-    x = oracle.normal((301, 96), 2000)
-    w = oracle.normal((72, 96), 2001, std=0.1)
-    dy = oracle.normal((301, 72), 2002, std=0.1)
-    dw = torch.empty(72, 96, device=dev)
-    db = torch.empty(72, device=dev)
-    with mt.forced_config(mt.FAMILY_DL, DLP, 1):
-        mt.linear_backward(g(dy, dev), g(x, dev), g(w, dev), need_dx=False, dw=dw, db=db)
-        _not_dlp(mt.last_config())
-    _, wdw, wdb = oracle.linear_backward(dy, x, w)
-    assert_close(sync_np(dw), wdw, 301, amax(dy), amax(x), "dlp fallback dW")
-    assert_close(sync_np(db), wdb, 301, amax(dy), 1.0, "dlp fallback db")
-    # ... and the implicit-im2col convolution forward keeps gemm_f32_dl
+    # exact.  The implicit-im2col convolution forward keeps gemm_f32_dl:
     n, c, h, wd, co, k = 2, 32, 9, 10, 40, 3
     xc = oracle.normal((n, c, h, wd), 2003)
     wc = oracle.normal((co, c, k, k), 2004)
