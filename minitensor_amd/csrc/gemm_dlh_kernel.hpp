@@ -140,12 +140,11 @@ gemm_f32_dlh(GemmParams p, HaloTable ht) {
     };
 
     // B fragments of the chunk at position q of patch buffer pb: the 8 k of
-    // this lane are 16*q + h8 + s in the patch, at the offsets of the
-    // argument table (scalar loads; each half of the wave selects its
+    // this lane are 16*q + 8*(lane/32) + s in the patch, at the offsets of
+    // the argument table (scalar loads; each half of the wave selects its
     // eight).  No k needs masking: a split's K range ends on a chunk
     // boundary except at K itself, and the k of the last chunk past K are
     // channels past c, which the patch holds as zeros (A is zero there too).
-    const int h8 = 8 * (lane >> 5);
     const bool hi = lane >= 32;
     auto frag_b = [&](int q, const float* pb, float (&fb)[NB][8]) {
         const int* tq = ht.off + 16 * q;
