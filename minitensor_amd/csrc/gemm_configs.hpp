@@ -48,9 +48,10 @@ template <> struct DlCfg<2> { static constexpr int BM = 64, BN = 64, WM = 32, WN
 // (e.g. convolutions with 256 output channels: 49 tiles x split 5 = 245).
 template <> struct DlCfg<3> { static constexpr int BM = 256, BN = 128, WM = 64, WN = 64, STAGES = 2; };
 // Configurations 4-6 are the fragment-prefetching kernel gemm_f32_dlp
-// (gemm_dlp_kernel.hpp): vector layouts and the weight-gradient operand
-// L_IMW; no implicit-im2col (L_IM) or row-sum form.  4: 4 waves of 128x128 (one per SIMD); 5: 4 waves of 32x32; 6: 8 waves
-// of 64x32 (two per SIMD), the 128x128 tile for K ranges of 512 and more.
+// (gemm_dlp_kernel.hpp): vector layouts, the weight-gradient operand L_IMW
+// and the row-sum form; no implicit-im2col (L_IM) form.  4: 4 waves of
+// 128x128 (one per SIMD); 5: 4 waves of 32x32; 6: 8 waves of 64x32 (two per
+// SIMD), the 128x128 tile for K ranges of 512 and more.
 // WPE: waves per SIMD its registers are sized for.
 template <> struct DlCfg<4> { static constexpr int BM = 256, BN = 256, WM = 128, WN = 128, STAGES = 2, WPE = 1; };
 template <> struct DlCfg<5> { static constexpr int BM = 64, BN = 64, WM = 32, WN = 32, STAGES = 2, WPE = 8; };

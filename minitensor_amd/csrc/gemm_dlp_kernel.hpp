@@ -34,8 +34,8 @@
 //   * The epilogue is store_tile_lds, as in gemm_f32_dl.
 // Host contract (checked in the dispatcher): operand layouts L_KV / L_MV (B
 // also the implicit im2col-transpose operand L_IMW of the convolution weight
-// gradient) and a non-empty K range.  Rows or columns beyond M or N read
-// clamped, valid rows, as in gemm_f32_dl.
+// gradient; A and B both L_MV for the row-sum form) and a non-empty K range.
+// Rows or columns beyond M or N read clamped, valid rows, as in gemm_f32_dl.
 #pragma once
 
 #include "gemm_dl_kernel.hpp"
