@@ -8,6 +8,7 @@
 #include <cstdint>
 #include <functional>
 #include <stdexcept>
+#include <string>
 #include <unordered_map>
 
 #include "TensorOps.hpp"
@@ -74,10 +75,15 @@ void matmul_into(const Tensor<T>& a, const Tensor<T>& b, Tensor<T>& out) {
 }
 
 // out = conv2d(input, weight) into out's shape.  The registry's binary
-// signature carries no stride or padding (include/Dispatch.hpp:21-22), so they
-// are inferred from the shapes: stride 1 with the padding that gives out's
-// size, else the "same" padding (kh-1)/2 of ResNet-style layers with the
-// smallest stride that gives it.  Any other shape throws std::invalid_argument.
+// signature carries no stride or padding (include/Dispatch.hpp:18-21), so they
+// are inferred from the shapes: every stride s >= 1 and padding
+// 0 <= p < max(kh, kw) whose output size is out's is a candidate; two
+// candidates compute the same thing when their paddings are equal and their
+// strides are too (or the output is 1x1, where the stride is never used).
+// Exactly one distinct candidate must remain: none, or several (a 9x9 input
+// with a 3x3 kernel gives 3x3 at stride 3 with padding 0 or 1, and at stride
+// 4 with padding 1), throws std::invalid_argument naming them; such callers
+// call conv2d(input, weight, bias, stride, pad) with the values they mean.
 template <typename T>
 void conv2d_into(const Tensor<T>& input, const Tensor<T>& weight, Tensor<T>& out) {
     if (input.shape().size() != 4 || weight.shape().size() != 4 || out.shape().size() != 4)
@@ -85,24 +91,30 @@ void conv2d_into(const Tensor<T>& input, const Tensor<T>& weight, Tensor<T>& out
     const size_t H = input.shape()[2], W = input.shape()[3];
     const size_t kh = weight.shape()[2], kw = weight.shape()[3];
     const size_t Ho = out.shape()[2], Wo = out.shape()[3];
-    auto fits = [&](size_t s, size_t p) {
-        return safe_out_size(H, p, kh, s) == Ho && safe_out_size(W, p, kw, s) == Wo;
-    };
-    size_t stride = 0, pad = 0;
-    const long twice = (long)Ho - (long)H + (long)kh - 1;
-    if (twice >= 0 && twice % 2 == 0 && fits(1, (size_t)twice / 2)) {
-        stride = 1;
-        pad = (size_t)twice / 2;
-    } else {
-        pad = (kh - 1) / 2;
-        for (size_t s = 2; s <= std::max(H, W) + 2 * pad; ++s)
-            if (fits(s, pad)) {
+    const bool one = Ho == 1 && Wo == 1;
+    size_t stride = 0, pad = 0, distinct = 0;
+    std::string found;
+    for (size_t p = 0; p < std::max<size_t>(std::max(kh, kw), 1); ++p) {
+        // beyond the padded extent every stride gives one output position
+        const size_t s_max = std::max(H, W) + 2 * p + 1;
+        for (size_t s = 1; s <= s_max; ++s) {
+            if (safe_out_size(H, p, kh, s) != Ho || safe_out_size(W, p, kw, s) != Wo) continue;
+            if (distinct < 4)
+                found += (distinct ? ", " : "") + std::string("stride ") + std::to_string(s) +
+                         " pad " + std::to_string(p);
+            if (distinct++ == 0) {
                 stride = s;
-                break;
+                pad = p;
             }
+            if (one) break;   // the other strides compute the same 1x1 output
+        }
     }
-    if (stride == 0)
+    if (distinct == 0)
         throw std::invalid_argument("conv2d: no stride and padding give the output shape");
+    if (distinct > 1)
+        throw std::invalid_argument("conv2d: the output shape fits " + std::to_string(distinct) +
+                                    " stride/padding pairs (" + found + (distinct > 4 ? ", ..." : "") +
+                                    "); call conv2d(input, weight, bias, stride, pad)");
     Tensor<T> r = conv2d(input, weight, Tensor<T>(), stride, pad);
     if (r.shape() != out.shape()) throw std::invalid_argument("conv2d: output shape mismatch");
     copy_strided(r, out);

@@ -346,11 +346,13 @@ TEST_CPU(cpu_dispatch_registry) {
     dispatch_binary_op(OpType::Matmul, mat23(), mat32(), out);
     CHECK_EQ_F(out.data()[0], 58); CHECK_EQ_F(out.data()[3], 154);
     CHECK(OpRegistry<float>::instance().lookup_binary(OpType::Conv2D) != nullptr);
-    Tensor<float> x({1, 1, 3, 3}), w({1, 1, 2, 2}), y({1, 1, 2, 2});
-    for (int i = 0; i < 9; ++i) x.data()[i] = (float)(i + 1);
+    // 5x5 input, 2x2 kernel of ones, 4x4 output: only stride 1 without
+    // padding gives it (padding 1 gives 6, 3 or 2 columns)
+    Tensor<float> x({1, 1, 5, 5}), w({1, 1, 2, 2}), y({1, 1, 4, 4});
+    for (int i = 0; i < 25; ++i) x.data()[i] = (float)(i + 1);
     w.fill(1);
     dispatch_binary_op(OpType::Conv2D, x, w, y);
-    CHECK_EQ_F(y.data()[0], 12); CHECK_EQ_F(y.data()[3], 28);
+    CHECK_EQ_F(y.data()[0], 16); CHECK_EQ_F(y.data()[15], 88);
 }
 
 
@@ -421,6 +423,43 @@ TEST_CPU(cpu_dispatch_conv2d_infers_stride) {
     }
     Tensor<float> bad({2, 4, 50, 50});
     CHECK_THROWS(dispatch_binary_op(OpType::Conv2D, x, w, bad), std::invalid_argument);
+    // a "full" convolution (stride 1, padding kh - 1) is the only fit of its shape
+    Tensor<float> full_want = conv2d(x, w, Tensor<float>(), 1, 2);
+    Tensor<float> full(full_want.shape());
+    dispatch_binary_op(OpType::Conv2D, x, w, full);
+    CHECK(max_err(full, full_want) == 0);
+}
+
+TEST_CPU(cpu_dispatch_conv2d_refuses_ambiguous_shapes) {
+    // 9x9 input, 3x3 kernel, 3x3 output: stride 3 with padding 0, and stride 3
+    // or 4 with padding 1, all give it; 4x4 -> 2x2: stride 1 unpadded or the
+    // stride-2 "same" downsample.  The registry cannot tell them apart: it
+    // throws, and the caller states stride and padding to conv2d.
+    Tensor<float> x = uniform({1, 2, 9, 9}, 81), w = uniform({3, 2, 3, 3}, 82);
+    Tensor<float> out({1, 3, 3, 3});
+    CHECK_THROWS(dispatch_binary_op(OpType::Conv2D, x, w, out), std::invalid_argument);
+    Tensor<float> x4 = uniform({1, 2, 4, 4}, 83), out4({1, 3, 2, 2});
+    CHECK_THROWS(dispatch_binary_op(OpType::Conv2D, x4, w, out4), std::invalid_argument);
+    // the explicit call computes the intended stride-3, unpadded layer: each
+    // output is one whole 3x3 window of the input
+    Tensor<float> y = conv2d(x, w, Tensor<float>(), 3, 0);
+    CHECK(y.shape() == out.shape());
+    for (size_t co = 0; co < 3; ++co)
+        for (size_t oh = 0; oh < 3; ++oh)
+            for (size_t ow = 0; ow < 3; ++ow) {
+                double acc = 0;
+                for (size_t ci = 0; ci < 2; ++ci)
+                    for (size_t r = 0; r < 3; ++r)
+                        for (size_t t = 0; t < 3; ++t)
+                            acc += (double)x.data()[(ci * 9 + oh * 3 + r) * 9 + ow * 3 + t] *
+                                   w.data()[((co * 2 + ci) * 3 + r) * 3 + t];
+                CHECK(std::abs(y.data()[(co * 3 + oh) * 3 + ow] - acc) < 1e-5);
+            }
+    // a 1x1 output is computed the same way at every stride, so it is one
+    // candidate per padding; a 3x3 input and kernel give 1x1 with padding 0
+    // (any stride), 1 (stride >= 3) and 2 (stride >= 5): three
+    Tensor<float> x3 = uniform({1, 2, 3, 3}, 84), out1({1, 3, 1, 1});
+    CHECK_THROWS(dispatch_binary_op(OpType::Conv2D, x3, w, out1), std::invalid_argument);
 }
 
 // =====================================================================
@@ -769,6 +808,13 @@ TEST_GPU(gpu_dispatch_conv2d) {
         dispatch_binary_op(OpType::Conv2D, x.to(GPU), w.to(GPU), out);
         check_close(out, want, 144, 1, 1);
     }
+    // shapes that several stride/padding pairs give are refused on the GPU too
+    Tensor<float> x9 = uniform({1, 16, 9, 9}, 85);
+    Tensor<float> out9({1, 8, 3, 3}, GPU);
+    CHECK_THROWS(dispatch_binary_op(OpType::Conv2D, x9.to(GPU), w.to(GPU), out9),
+                 std::invalid_argument);
+    Tensor<float> want9 = conv2d(x9, w, Tensor<float>(), 3, 0);
+    check_close(conv2d(x9.to(GPU), w.to(GPU), Tensor<float>(), 3, 0), want9, 144, 1, 1);
 }
 
 TEST_GPU(gpu_sum_and_copy_launchers_by_name) {
