@@ -64,7 +64,8 @@ def parse():
     p.add_argument("--copy-probe", action="store_true",
                    help="also run a 256 MiB device copy (rocprof counter calibration)")
     p.add_argument("--only", default="",
-                   help="comma list of secondary configs (c1,c3,c4,c5a,c5b): run just those "
+                   help="comma list of secondary configs (c1,c3,c4,c5a,c5b,skinny) and/or "
+                        "'sustained' (the headline GEMM back to back for 2.5 s): run just those "
                         "and print their JSON, without the headline and CPU legs "
                         "(per-workload profiles)")
     return p.parse_args()
@@ -180,7 +181,50 @@ def time_graph(fn, calls: int = 20, replays: int = 10, preroll_ms: float = PRERO
     return per
 
 
-SECONDARY = ("c1", "c3", "c4", "c5a", "c5b")
+SECONDARY = ("c1", "c3", "c4", "c5a", "c5b", "skinny")
+SUSTAINED_S = 2.5
+
+
+def sustained(step, flops: float, seconds: float = SUSTAINED_S) -> dict:
+    """The headline GEMM back to back for `seconds` of GPU time, an event
+    after every step (the queue is kept about 64 steps deep, so the GPU never
+    idles): min / median / mean of the per-step times over the whole window,
+    the mean over its last second, and the mean of its first 100 steps (the
+    regime of the short timed window)."""
+    import torch
+    stream = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    step()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    n = max(200, int(seconds * 1e3 / max(t0.elapsed_time(t1), 1e-3)))
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    evs[0].record(stream)
+    for i in range(n):
+        step()
+        evs[i + 1].record(stream)
+        if i >= 64:
+            evs[i - 63].synchronize()
+    torch.cuda.synchronize()
+    per = [evs[i].elapsed_time(evs[i + 1]) for i in range(n)]
+    span = evs[0].elapsed_time(evs[-1])
+    acc, last = 0.0, []
+    for p in reversed(per):
+        if acc >= 1000.0:
+            break
+        acc += p
+        last.append(p)
+    st = _stats(per)
+    first = sum(per[:100]) / 100
+    last_mean = sum(last) / len(last)
+    return {"steps": n, "seconds": round(span / 1e3, 3), "ms_min": st["min"],
+            "ms_median": st["median"], "ms_mean": st["mean"],
+            "ms_mean_first_100": round(first, 5), "ms_mean_last_second": round(last_mean, 5),
+            "tflops_mean": round(flops / st["mean"] / 1e9, 3),
+            "tflops_last_second": round(flops / last_mean / 1e9, 3)}
 
 
 def secondary(dev, only=SECONDARY) -> dict:
@@ -303,6 +347,19 @@ def secondary(dev, only=SECONDARY) -> dict:
         ms = both(lambda: mt.gemm(A, B, out=C, ws=ws), 200, 20)
         rec("c5b_bmm_64x512x512x64", ms, 2 * 64 * 512 * 512 * 64,
             4 * 64 * (512 * 64 + 64 * 512 + 512 * 512), mt.last_config())
+
+    if "skinny" in only:
+        # The reference's HBM-bound matmul rows (test/benchmark.cpp:732,737-738,
+        # bench_matmul(M, N, K)): vector x matrix, the outer product and 63
+        # rows, contiguous row-major, bytes = (MK + KN + MN)·4 as the
+        # reference counts them (test/benchmark.cpp:168).
+        for m, k, nn in ((1, 4096, 4096), (4096, 1, 4096), (63, 4096, 4096)):
+            A, B = u(m, k), u(k, nn)
+            C = torch.empty(m, nn, device=dev)
+            ws = ws_for(A, B, C)
+            ms = both(lambda: mt.gemm(A, B, out=C, ws=ws), 200, 20)
+            rec(f"skinny_{m}x{k}x{nn}", ms, 2 * m * nn * k, 4 * (m * k + k * nn + m * nn),
+                mt.last_config())
     return out
 
 
@@ -461,39 +518,48 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    M = N = K = 4096
+    flops = 2.0 * M * N * K
+
+    def headline_step():
+        g = torch.Generator(device=dev)
+        g.manual_seed(42)
+        A = torch.rand(M, K, device=dev, generator=g) * 2 - 1
+        B = torch.rand(K, N, device=dev, generator=g) * 2 - 1
+        C = torch.empty(M, N, device=dev)
+        ws = mt.workspace(mt.lib().mt_gemm_workspace_f32(mt.mat(A), mt.mat(B), mt.mat(C)), dev)
+        return lambda: mt.gemm(A, B, out=C, ws=ws)
+
     if args.only:
         names = tuple(x.strip() for x in args.only.split(",") if x.strip())
-        unknown = [x for x in names if x not in SECONDARY]
+        unknown = [x for x in names if x not in SECONDARY + ("sustained",)]
         if unknown:
-            print(f"bench.py: unknown --only entries {unknown}; choose from {SECONDARY}",
-                  file=sys.stderr)
+            print(f"bench.py: unknown --only entries {unknown}; choose from "
+                  f"{SECONDARY + ('sustained',)}", file=sys.stderr)
             sys.exit(2)
-        sec = secondary(dev, names)
+        res = {"secondary": secondary(dev, tuple(x for x in names if x != "sustained"))}
+        if "sustained" in names:
+            step = headline_step()
+            for _ in range(args.warmup):
+                step()
+            res["sustained"] = sustained(step, flops)
+            res["sustained"]["kernel"] = mt.last_config()
         if args.copy_probe:
             copy_probe(dev)
-        print(json.dumps({"secondary": sec}), flush=True)
+        print(json.dumps(res), flush=True)
         return
-    M = N = K = 4096
-    g = torch.Generator(device=dev)
-    g.manual_seed(42)
-    A = torch.rand(M, K, device=dev, generator=g) * 2 - 1
-    B = torch.rand(K, N, device=dev, generator=g) * 2 - 1
-    C = torch.empty(M, N, device=dev)
-    ws = mt.workspace(mt.lib().mt_gemm_workspace_f32(mt.mat(A), mt.mat(B), mt.mat(C)), dev)
-
-    def step():
-        mt.gemm(A, B, out=C, ws=ws)
+    step = headline_step()
 
     t0 = time.perf_counter()
     span_ms, per_ms, n_pre = time_steps(step, args.steps, args.warmup)
     wall = time.perf_counter() - t0
     ms = span_ms / args.steps
     kernel_cfg = mt.last_config()
-    flops = 2.0 * M * N * K
     tflops = flops / ms / 1e9
     st = _stats(per_ms)
     ref_win = reference_window(step)
     ref_win["tflops"] = round(flops / ref_win["ms_mean"] / 1e9, 3)
+    sus = sustained(step, flops)
 
     if args.copy_probe:
         copy_probe(dev)
@@ -527,6 +593,7 @@ def main():
                    "kernel": kernel_cfg, "preroll_steps": n_pre,
                    "wall_s_warmup_preroll_timed": round(wall, 4)},
         "reference_window": ref_win,
+        "sustained": sus,
         "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / PEAK_TFLOPS, 4),
                      "traffic": traffic},
