@@ -236,8 +236,14 @@ enum {
     MT_FAMILY_AUTO = 0,  /* the cost model chooses (default)                   */
     MT_FAMILY_RS = 1,    /* register-staged kernel: any operand layout          */
     MT_FAMILY_DL = 2,    /* direct-to-LDS kernel: k- or mn-contiguous operands  */
-    MT_FAMILY_KSW = 3    /* wave-split kernel: small tiles, K split across the
+    MT_FAMILY_KSW = 3,   /* wave-split kernel: small tiles, K split across the
                             waves of a workgroup; any operand layout            */
+    MT_FAMILY_SKINNY = 4 /* vector-ALU kernels of the HBM-bound shapes:
+                            configuration 0 GEMV (at most 8 rows of A against a
+                            k- or mn-contiguous B, or at most 8 columns of B
+                            against such an A; `splits` K splits), 1 rank-k
+                            (K <= 16, at least 256 columns); no implicit
+                            convolution operands, no fused row sums          */
 };
 /* Number of tile configurations of a family (0 for MT_FAMILY_AUTO). */
 int mt_gemm_config_count(int family);

@@ -421,11 +421,11 @@ def last_config() -> str:
     return lib().mt_last_config().decode()
 
 
-FAMILY_AUTO, FAMILY_RS, FAMILY_DL, FAMILY_KSW = 0, 1, 2, 3
+FAMILY_AUTO, FAMILY_RS, FAMILY_DL, FAMILY_KSW, FAMILY_SKINNY = 0, 1, 2, 3, 4
 
 
 def config_count(family: int) -> int:
-    """Tile configurations of a kernel family (FAMILY_RS or FAMILY_DL)."""
+    """Tile configurations of a kernel family (FAMILY_RS, _DL, _KSW or _SKINNY)."""
     return lib().mt_gemm_config_count(int(family))
 
 

@@ -128,4 +128,19 @@ constexpr int kNumKswCfg = 4;
 GemmLaunchFn ksw_launcher(int cfg, bool va, bool vb);
 void ksw_tile(int cfg, int* bm, int* bn);
 
+// Vector-ALU kernels of the HBM-bound shapes (gemm_skinny_kernel.hpp):
+// GEMV for M <= rows <= 8 (B k-contiguous when kv, else mn-contiguous;
+// nullptr for more rows), rank-k for 1 <= K <= 16, and the reduction of the
+// GEMV kernels' split-K partials (16-byte workspace, grid over groups of
+// 16 column quads x M*batch rows).
+constexpr int kGemvMaxRows = 8;    // rows of A the GEMV kernels take
+constexpr int kRankKMax = 16;      // K the rank-k kernel takes
+constexpr int kGemvMvCols = 256;   // columns per GEMV workgroup, B mn-contiguous
+constexpr int kGemvKvCols = 16;    // columns per GEMV workgroup, B k-contiguous
+constexpr int kRankKCols = 1024;   // columns per rank-k workgroup
+constexpr int kRankKRows = 16;     // rows per rank-k workgroup
+GemmLaunchFn gemv_launcher(bool kv, int rows);
+GemmLaunchFn rankk_launcher(int K);
+hipError_t launch_skinny_reduce(const GemmParams& p, hipStream_t s);
+
 }  // namespace mtk

@@ -453,6 +453,106 @@ GemmLaunchFn conv_launcher(int cfg, bool nchw) {
     }
 }
 
+// ---- HBM-bound shapes on the vector ALUs (gemm_skinny_kernel.hpp) ----------
+// GEMV: at most kGemvMaxRows rows of A against a B that is k- or
+// mn-contiguous (or, transposed, at most that many columns of B against such
+// an A), K >= kGemvMinK; rank-k: 1 <= K <= kRankKMax with at least
+// kRankKMinN columns.  No implicit convolution operand and no fused row or
+// channel sums: those shapes keep the MFMA kernels.
+enum { SK_NONE = 0, SK_GEMV = 1, SK_RANKK = 2 };
+constexpr int kGemvMinK = 16;
+constexpr int kRankKMinN = 256;
+constexpr int kGemvMaxSplits = 64;
+constexpr int kGemvWgsPerCu = 4;
+
+struct SkinnyPlan {
+    int kind = SK_NONE;
+    bool transpose = false;  // computes Cᵀ = Bᵀ·Aᵀ (the few columns of B become rows)
+    bool kv = false;         // GEMV: the large operand is k-contiguous
+    int rows = 0;            // GEMV: rows of the kernel's instantiation (1, 2, 4, 8)
+    int splits = 1, kps = 0;
+    int tiles_m = 1, tiles_n = 1;
+    size_t ws_bytes = 0;
+    unsigned blocks = 0;
+};
+
+// GEMV of m <= kGemvMaxRows rows against an n-column operand, K = k.  The
+// split count aims at kGemvWgsPerCu workgroups per CU (every workgroup
+// resident at once: the kernels are bound by the loads in flight), with at
+// least 64 k per split (mn-contiguous B) or four 64-deep steps per lane
+// (k-contiguous B), at most kGemvMaxSplits; forced_splits > 0 asks for that
+// many.
+SkinnyPlan gemv_plan(int64_t m, int64_t n, int64_t k, int64_t batch, bool kv, int cus,
+                     int forced_splits) {
+    SkinnyPlan s;
+    s.kind = SK_GEMV;
+    s.kv = kv;
+    s.rows = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
+    const int64_t cols = kv ? kGemvKvCols : kGemvMvCols;
+    s.tiles_n = (int)((n + cols - 1) / cols);
+    const int64_t gran = kv ? 64 : 4, min_kps = kv ? 256 : 64;
+    int64_t want = forced_splits;
+    if (want <= 0) {
+        const int64_t base = (int64_t)s.tiles_n * batch;
+        want = std::max<int64_t>(1, (kGemvWgsPerCu * (int64_t)cus + base - 1) / base);
+        want = std::min<int64_t>({want, std::max<int64_t>(1, k / min_kps), kGemvMaxSplits});
+    }
+    int64_t kps = (k + want - 1) / want;
+    kps = (kps + gran - 1) / gran * gran;
+    s.kps = (int)kps;
+    s.splits = (int)((k + kps - 1) / kps);
+    s.ws_bytes = s.splits > 1 ? (size_t)s.splits * batch * m * n * sizeof(float) : 0;
+    s.blocks = (unsigned)((int64_t)s.tiles_n * s.splits * batch);
+    return s;
+}
+
+SkinnyPlan rankk_plan(int64_t m, int64_t n, int64_t k, int64_t batch) {
+    SkinnyPlan s;
+    s.kind = SK_RANKK;
+    s.kps = (int)k;
+    s.tiles_n = (int)((n + kRankKCols - 1) / kRankKCols);
+    s.tiles_m = (int)((m + kRankKRows - 1) / kRankKRows);
+    s.blocks = (unsigned)((int64_t)s.tiles_n * s.tiles_m * batch);
+    return s;
+}
+
+// Which vector-ALU kernel, if any, takes this GEMM (`scatter`: C's columns are
+// scattered, which the transposed form cannot take).  A forced configuration
+// of another family keeps the shape on that family; a forced MT_FAMILY_SKINNY
+// configuration applies where its kernel takes the operands.
+SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int la, int lb,
+                       bool scatter, int cus) {
+    const ForcedConfig f = g_forced;
+    SkinnyPlan none;
+    if (K <= 0 || (f.family != MT_FAMILY_AUTO && f.family != MT_FAMILY_SKINNY)) return none;
+    const bool forced = f.family == MT_FAMILY_SKINNY;
+    const int splits = forced ? f.splits : 0;
+    const bool vec_b = lb == L_MV || lb == L_KV, vec_a = la == L_MV || la == L_KV;
+    if ((!forced || f.cfg == 1) && K <= kRankKMax && N >= kRankKMinN) return rankk_plan(M, N, K, batch);
+    if (forced && f.cfg != 0) return none;
+    if (K < kGemvMinK) return none;
+    if (M <= kGemvMaxRows && vec_b) return gemv_plan(M, N, K, batch, lb == L_KV, cus, splits);
+    if (N <= kGemvMaxRows && vec_a && !scatter) {
+        SkinnyPlan s = gemv_plan(N, M, K, batch, la == L_KV, cus, splits);
+        s.transpose = true;
+        return s;
+    }
+    return none;
+}
+
+// Workspace the GEMV plans of this shape may need (layouts unknown).
+size_t skinny_ws(int64_t M, int64_t N, int64_t K, int64_t batch, int cus) {
+    if (K < kGemvMinK) return 0;
+    const ForcedConfig f = g_forced;
+    const int splits = f.family == MT_FAMILY_SKINNY ? f.splits : 0;
+    size_t ws = 0;
+    for (bool kv : {false, true}) {
+        if (M <= kGemvMaxRows) ws = std::max(ws, gemv_plan(M, N, K, batch, kv, cus, splits).ws_bytes);
+        if (N <= kGemvMaxRows) ws = std::max(ws, gemv_plan(N, M, K, batch, kv, cus, splits).ws_bytes);
+    }
+    return ws;
+}
+
 // Workspace that covers the plan of either kernel family (for sizes queried
 // before the operand pointers, and hence the layouts, are known).
 size_t plan_ws(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool imw = false) {
@@ -466,7 +566,7 @@ size_t plan_ws(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool imw
             ws = std::max(ws, make_plan(M, N, K, batch, cus, true, true, wide, false, true).ws_bytes);
     Plan forced;
     if (forced_plan(M, N, K, batch, true, true, true, &forced)) ws = std::max(ws, forced.ws_bytes);
-    return ws;
+    return std::max(ws, skinny_ws(M, N, K, batch, cus));
 }
 
 GemmLaunchFn pick_launcher(const Plan& plan, int la, int lb, bool ktail) {
@@ -631,6 +731,70 @@ __global__ void __launch_bounds__(256) splitk_reduce_vec_f32(GemmParams p) {
     }
 }
 
+// The transposed problem Cᵀ = Bᵀ·Aᵀ: the operands swap roles, C's row and
+// column strides swap, a per-row bias becomes a per-column one.  Only for
+// unscattered outputs.
+GemmParams transposed_params(const GemmParams& p) {
+    GemmParams q = p;
+    q.A = p.B; q.a_mn = p.b_mn; q.a_k = p.b_k; q.a_b = p.b_b;
+    q.B = p.A; q.b_mn = p.a_mn; q.b_k = p.a_k; q.b_b = p.a_b;
+    q.c_m = p.c_n; q.c_n = p.c_m;
+    q.M = p.N; q.N = p.M;
+    q.c_n_inner = q.N;
+    q.c_n_outer = 0;
+    q.bias_axis = p.bias_axis == MT_BIAS_ROW   ? MT_BIAS_COL
+                  : p.bias_axis == MT_BIAS_COL ? MT_BIAS_ROW
+                                               : p.bias_axis;
+    q.c_vec = q.c_n == 1 && (q.N & 3) == 0 && ((uintptr_t)q.C & 15u) == 0 && (q.c_m & 3) == 0 &&
+              (q.batch == 1 || (q.c_b & 3) == 0);
+    return q;
+}
+
+// Launches a vector-ALU plan (and, for a split GEMV, the reduction of its
+// partials).  A GEMV plan whose partials the workspace cannot hold runs
+// unsplit, unless the configuration is forced (MT_ERR_WORKSPACE).
+int launch_skinny(const GemmParams& p0, SkinnyPlan sp, void* workspace, size_t ws_bytes,
+                  hipStream_t stream) {
+    if (sp.splits > 1 && (workspace == nullptr || ws_bytes < sp.ws_bytes)) {
+        if (g_forced.family == MT_FAMILY_SKINNY) return MT_ERR_WORKSPACE;
+        const bool t = sp.transpose;
+        sp = t ? gemv_plan(p0.N, p0.M, p0.K, p0.batch, sp.kv, device_cu_count(), 1)
+               : gemv_plan(p0.M, p0.N, p0.K, p0.batch, sp.kv, device_cu_count(), 1);
+        sp.transpose = t;
+    }
+    GemmParams p = sp.transpose ? transposed_params(p0) : p0;
+    p.splits = sp.splits;
+    p.k_per_split = sp.kps;
+    p.tiles_m = sp.tiles_m;
+    p.tiles_n = sp.tiles_n;
+    p.group_m = 1;
+    p.ws = sp.splits > 1 ? static_cast<float*>(workspace) : nullptr;
+    p.ws_vec = p.ws != nullptr && ((uintptr_t)p.ws & 15u) == 0 && (p.N & 3) == 0;
+    std::snprintf(g_last_config, sizeof g_last_config, "sk %s%s rows=%d split=%d wgs=%u cfg=%d",
+                  sp.kind == SK_RANKK ? "rankk" : sp.kv ? "gemv_kv" : "gemv_mv",
+                  sp.transpose ? "_t" : "", sp.kind == SK_GEMV ? sp.rows : 0, sp.splits,
+                  sp.blocks, sp.kind == SK_RANKK ? 1 : 0);
+    const GemmLaunchFn fn =
+        sp.kind == SK_RANKK ? rankk_launcher(p.K) : gemv_launcher(sp.kv, sp.rows);
+    if (fn == nullptr || sp.blocks == 0) return MT_ERR_UNSUPPORTED;
+    hipError_t e = fn(p, sp.blocks, stream);
+    if (e == hipErrorStreamCaptureUnsupported) e = hipSuccess;
+    if (e != hipSuccess) return MT_ERR_HIP;
+    if (sp.splits > 1) {
+        if (p.ws_vec && (int64_t)p.M * p.batch <= 65535) {
+            e = launch_skinny_reduce(p, stream);
+        } else {
+            const int64_t total = (int64_t)p.M * p.N * p.batch;
+            const int64_t blocks = std::min<int64_t>((total + 255) / 256, 65536);
+            hipLaunchKernelGGL(splitk_reduce_f32, dim3((unsigned)blocks), dim3(256), 0, stream, p);
+            e = hipGetLastError();
+        }
+        if (e == hipErrorStreamCaptureUnsupported) e = hipSuccess;
+        if (e != hipSuccess) return MT_ERR_HIP;
+    }
+    return MT_OK;
+}
+
 // Completes the plan-dependent fields of p (tile grid, split-K, vector
 // epilogue flags), then launches the GEMM kernel and, for split-K, the
 // deterministic reduction.  lb == L_IM selects the implicit-im2col kernel.
@@ -647,6 +811,12 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
     // mn-contiguous operands without split-K (the caller sees p.rowsum cleared
     // and computes them separately).
     if (batch != 1 || la != L_MV || lb != L_MV) p.rowsum = nullptr;
+    // The HBM-bound shapes (few rows or columns, or K <= 16) on the vector ALUs.
+    if (!implicit && la != L_KVI && p.rowsum == nullptr && p.csum == nullptr) {
+        const SkinnyPlan sp =
+            skinny_plan(M, N, K, batch, la, lb, p.c_n_inner < N, device_cu_count());
+        if (sp.kind != SK_NONE) return launch_skinny(p, sp, workspace, ws_bytes, stream);
+    }
     // The prefetching configurations' contract: vector layouts or the
     // weight-gradient operand (not the implicit-im2col one), a non-empty K
     // range.
@@ -1856,10 +2026,11 @@ int mt_version(void) { return MTGEMM_VERSION; }
 const char* mt_last_config(void) { return g_last_config; }
 
 int mt_gemm_config_count(int family) {
-    return family == MT_FAMILY_RS    ? kNumCfg
-           : family == MT_FAMILY_DL  ? kNumDlCfg
-           : family == MT_FAMILY_KSW ? kNumKswCfg
-                                     : 0;
+    return family == MT_FAMILY_RS       ? kNumCfg
+           : family == MT_FAMILY_DL     ? kNumDlCfg
+           : family == MT_FAMILY_KSW    ? kNumKswCfg
+           : family == MT_FAMILY_SKINNY ? 2
+                                        : 0;
 }
 
 int mt_gemm_force_config(int family, int cfg, int splits) {
@@ -1867,7 +2038,8 @@ int mt_gemm_force_config(int family, int cfg, int splits) {
         g_forced = ForcedConfig{};
         return MT_OK;
     }
-    if ((family != MT_FAMILY_RS && family != MT_FAMILY_DL && family != MT_FAMILY_KSW) || cfg < 0 ||
+    if ((family != MT_FAMILY_RS && family != MT_FAMILY_DL && family != MT_FAMILY_KSW &&
+         family != MT_FAMILY_SKINNY) || cfg < 0 ||
         cfg >= mt_gemm_config_count(family) || splits < 1 || splits > kMaxForcedSplits)
         return MT_ERR_INVALID;
     g_forced = ForcedConfig{family, cfg, splits};

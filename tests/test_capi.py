@@ -161,12 +161,14 @@ def test_config_counts():
     assert mt.config_count(mt.FAMILY_RS) == 3
     assert mt.config_count(mt.FAMILY_DL) == 7
     assert mt.config_count(mt.FAMILY_KSW) == 4
+    assert mt.config_count(mt.FAMILY_SKINNY) == 2
     assert mt.config_count(mt.FAMILY_AUTO) == 0
 
 
 @pytest.mark.parametrize("family,cfg,splits", [
-    (4, 0, 1), (-1, 0, 1), (mt.FAMILY_RS, 3, 1), (mt.FAMILY_DL, 7, 1), (mt.FAMILY_DL, -1, 1),
-    (mt.FAMILY_KSW, 4, 1), (mt.FAMILY_KSW, -1, 1),
+    (5, 0, 1), (-1, 0, 1), (mt.FAMILY_RS, 3, 1), (mt.FAMILY_DL, 7, 1), (mt.FAMILY_DL, -1, 1),
+    (mt.FAMILY_KSW, 4, 1), (mt.FAMILY_KSW, -1, 1), (mt.FAMILY_SKINNY, 2, 1),
+    (mt.FAMILY_SKINNY, 0, 65),
     (mt.FAMILY_DL, 0, 0), (mt.FAMILY_DL, 0, 65)])
 def test_force_config_rejects_unknown(family, cfg, splits):
     assert mt.lib().mt_gemm_force_config(family, cfg, splits) == mt.MT_ERR_INVALID
@@ -187,3 +189,17 @@ def test_forced_split_is_in_the_workspace_query():
     a, b = M(256, 40), M(40, 256)
     with mt.forced_config(mt.FAMILY_DL, 1, 16):
         assert lib.mt_gemm_workspace_f32(a, b, c) >= 3 * 256 * 256 * 4
+
+
+def test_gemv_split_partials_in_the_workspace_query():
+    """The workspace query covers the split-K partials of the vector-ALU GEMV
+    plan: 1x4096·4096x4096 splits K into 64 ranges on a 256-CU device (four
+    workgroups per CU over 16 column groups), 64 x 4096 floats; a forced
+    skinny configuration with 16 splits needs 16 x 4096."""
+    a, b, c = M(1, 4096), M(4096, 4096), M(1, 4096)
+    lib = mt.lib()
+    assert lib.mt_gemm_workspace_f32(a, b, c) == 64 * 4096 * 4
+    with mt.forced_config(mt.FAMILY_SKINNY, 0, 16):
+        assert lib.mt_gemm_workspace_f32(a, b, c) == 16 * 4096 * 4
+    # the outer product (rank-k) needs no workspace beyond the MFMA plans'
+    assert lib.mt_gemm_workspace_f32(M(4096, 1), M(1, 4096), M(4096, 4096)) == 0

@@ -246,10 +246,24 @@ def _views(a, b, ta, tb, dev):
 
 
 # Vector-layout operands go to the direct-to-LDS kernel or, for small output
-# tile counts, to the wave-split kernel; the cost model picks.  (Every
-# configuration of both is also forced on these layouts in
+# tile counts, to the wave-split kernel; the cost model picks.  Shapes with at
+# most 8 rows or columns, or K <= 16, go to the vector-ALU kernels ("sk",
+# tests/test_skinny_gpu.py); the direct-to-LDS kernel is then also forced on
+# them (configurations 2 and 5, the plain and the prefetching 64x64 tile),
+# so that its one-row / one-column tails stay covered.  (Every configuration
+# of both MFMA families is also forced on these layouts in
 # test_configs_gpu.py and test_ksw_gpu.py.)
-VECTOR_PATHS = ("dl ", "ksw ")
+VECTOR_PATHS = ("dl ", "ksw ", "sk ")
+
+
+def _also_forced_dl(A, B, want, K, am, bm, what):
+    if not mt.last_config().startswith("sk "):
+        return
+    for cfg in (2, 5):
+        with mt.forced_config(mt.FAMILY_DL, cfg, 1):
+            c = run(A, B)
+            assert mt.last_config().startswith("dl "), mt.last_config()
+        assert_close(c, want, K, am, bm, f"{what} forced dl cfg {cfg}")
 
 
 @pytest.mark.parametrize("ta,tb", [(False, False), (False, True), (True, False), (True, True)])
@@ -260,7 +274,10 @@ def test_dl_layouts_and_tails(dev, ta, tb, M, N, K):
     A, B = _views(a, b, ta, tb, dev)
     c = run(A, B)
     assert mt.last_config().startswith(VECTOR_PATHS), mt.last_config()
-    assert_close(c, oracle.matmul(a, b), K, amax(a), amax(b), f"dl {M}x{N}x{K} ta={ta} tb={tb}")
+    want = oracle.matmul(a, b)
+    what = f"dl {M}x{N}x{K} ta={ta} tb={tb}"
+    assert_close(c, want, K, amax(a), amax(b), what)
+    _also_forced_dl(A, B, want, K, amax(a), amax(b), what)
 
 
 @pytest.mark.parametrize("M,N,K", [(128, 128, 4100), (96, 64, 6004), (1, 256, 64), (256, 1, 64),
@@ -271,8 +288,10 @@ def test_dl_split_k_and_edges(dev, M, N, K):
     A, B = to_gpu(a, dev), to_gpu(b, dev)
     c = run(A, B)
     assert mt.last_config().startswith(VECTOR_PATHS), mt.last_config()
-    assert_close(c, oracle.matmul(a, b), K, amax(a), amax(b), f"dl {M}x{N}x{K}")
+    want = oracle.matmul(a, b)
+    assert_close(c, want, K, amax(a), amax(b), f"dl {M}x{N}x{K}")
     np.testing.assert_array_equal(c, run(A, B))   # deterministic, also under split-K
+    _also_forced_dl(A, B, want, K, amax(a), amax(b), f"dl {M}x{N}x{K}")
 
 
 def test_dl_batched_transposed(dev):
