@@ -28,8 +28,13 @@
 // them per lane cost more vector instructions than the multiply hides.
 //
 // Reads the same operands and writes the same output and split-K partials as
-// gemm_f32_dl with B = L_IMR; the products are summed in the same order
-// (16-deep chunks, the permuted K order of gemm_kernel.hpp).
+// gemm_f32_dl with B = L_IMR, in 16-deep chunks with the permuted K order of
+// gemm_kernel.hpp.  The order of the chunks differs when the K range ends in
+// a partial chunk (c*kh*kw % 16 != 0): gemm_f32_dl multiplies that chunk
+// first, this kernel last.  The two paths are therefore not bitwise equal in
+// general (each is deterministic, and both are within the parity bound); the
+// planner may switch between them (LDS limit, cost rule, forced
+// configurations), and nothing relies on their bits agreeing.
 #pragma once
 
 #include "gemm_dl_kernel.hpp"

@@ -291,7 +291,12 @@ Plan make_plan_uncached(int64_t M, int64_t N, int64_t K, int64_t batch, int cus,
 
 // The cost model is a pure function of its arguments; a training loop asks
 // for the same few shapes again and again (workspace query, then launch), so
-// each thread keeps its last few plans.
+// each thread keeps its last kEntries plans.  A workspace query of one GEMM
+// visits up to 10 keys (both families, with and without the prefetching
+// configurations and the wave-split kernel, the weight-gradient table), and
+// one convolution backward query four such shapes (about 34 keys): the cache
+// holds several layers' worth, so the launch that follows a query finds its
+// plan instead of rerunning the cost model.
 Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool allow_split,
                bool dl, bool wide, bool ksw, bool imw = false) {
     struct Entry {
@@ -300,7 +305,7 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool all
         bool allow_split = false, dl = false, wide = false, ksw = false, imw = false;
         Plan plan;
     };
-    constexpr int kEntries = 8;
+    constexpr int kEntries = 128;
     thread_local Entry cache[kEntries];
     thread_local int next = 0;
     for (const Entry& e : cache)

@@ -143,7 +143,6 @@ def _halo_case(rng, i: int) -> dict:
 N_HALO = 30
 _hrng = np.random.default_rng(20261203)
 HALO_CASES = [_halo_case(_hrng, i) for i in range(N_HALO)]
-_halo_seen = []
 
 
 @pytest.mark.parametrize("case", HALO_CASES, ids=[f"h{i}" for i in range(N_HALO)])
@@ -161,7 +160,6 @@ def test_random_conv_halo_forced(dev, case):
         y2 = mt.conv2d(X, W, Bt, stride, pad)
     torch.cuda.synchronize()
     print(f"[case] {case} -> forward {cfg}", flush=True)
-    _halo_seen.append("b=im2col_halo" in cfg)
     y, y2 = y.cpu().numpy(), y2.cpu().numpy()
     assert np.array_equal(y.view(np.uint32), y2.view(np.uint32)), "forward not deterministic"
     assert_close(y, oracle.conv2d(x, w, b, stride, pad), c * kh * kw, amax(x), amax(w),
@@ -179,9 +177,18 @@ def test_random_conv_halo_forced(dev, case):
                      f"forced halo dX {case}")
 
 
-def test_random_conv_halo_forced_coverage():
-    """Most of the forced draws above ran the halo kernel (the rest had bands
-    too large for their tile)."""
-    if len(_halo_seen) < N_HALO:
-        pytest.skip("the forced halo draws did not all run in this session")
-    assert sum(_halo_seen) >= N_HALO // 2, _halo_seen
+def test_random_conv_halo_forced_coverage(dev):
+    """Most of the forced draws above run the halo kernel (the rest have bands
+    too large for their tile): each case's forward is run here again, under
+    its forced configuration, so the check holds whatever subset of the
+    parametrized tests ran in this process."""
+    seen = []
+    for case in HALO_CASES:
+        x = oracle.normal((case["n"], case["c"], case["h"], case["w"]), case["seed"])
+        w = oracle.normal((case["co"], case["c"], case["kh"], case["kw"]), case["seed"] + 1)
+        X = _input_view(x, case["view"], case["seed"], dev)
+        with mt.forced_config(mt.FAMILY_DL, case["cfg"], case["split"]):
+            mt.conv2d(X, torch.from_numpy(w).to(dev), None, case["stride"], case["pad"])
+            seen.append("b=im2col_halo" in mt.last_config())
+    torch.cuda.synchronize()
+    assert sum(seen) >= N_HALO // 2, seen
