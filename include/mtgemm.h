@@ -180,13 +180,22 @@ int mt_conv2d_fwd_strided_f32(const mt_conv2d_desc* d, const float* input,
  *           implicit-GEMM forward convolution of dY with the weights
  *           transposed to [c_in][c_out] and flipped, padding kh-1-pad (no
  *           column buffer; channels-last when c_out % 16 == 0, else from
- *           the NCHW dY); otherwise dcol = Wᵀ · dY, then a deterministic
- *           col2im gather into dX
+ *           the NCHW dY); other strides up to 4 (and other stride-1 kernels):
+ *           one implicit GEMM per stride phase (ih % s, iw % s) of dX, a
+ *           stride-1 convolution of dY with that phase's flipped sub-kernel
+ *           scattered to every s-th pixel (channels-last dY when
+ *           c_out % 16 == 0, else dY read in place when every phase's
+ *           c_out*taps % 4 == 0); otherwise dcol = Wᵀ · dY, then a
+ *           deterministic col2im gather into dX
  *           replaces conv2d_backward_input_gpu + fused_backward_input_kernel
  *           (reference src/gpu_ops.cpp:2499-2550, 861-907)
  *   bias:   db[c] = Σ_{n,y,x} dY[n,c,y,x] (+ beta·db)
  *           replaces conv2d_backward_bias_gpu (reference src/gpu_ops.cpp:2483-2497)
- * One workspace query covers weight and input. */
+ * One workspace query covers weight and input: the larger of what the two
+ * paths the geometry takes use, for 16-byte-aligned tensors.  (A dY that is
+ * not 16-byte aligned cannot be read in place by the implicit weight
+ * gradient, which then copies it: c_out*n*h_out*w_out floats, rounded up to
+ * 256 bytes, more; with less the call returns MT_ERR_WORKSPACE.) */
 int mt_conv2d_bwd_weight_f32(const mt_conv2d_desc* d, const float* input, const float* grad_out,
                              float* grad_weight, float beta, void* workspace, size_t ws_bytes,
                              void* stream);

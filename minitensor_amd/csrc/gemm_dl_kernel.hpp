@@ -244,7 +244,7 @@ struct DlImLoader {
             const int img = n / hw, rem = n - img * hw;
             const int oh = rem / g.wo, ow = rem - oh * g.wo;
             ih0[j] = n < p.N ? oh * g.stride - g.pad : -(1 << 30);   // past N: zeros
-            iw0[j] = ow * g.stride - g.pad;
+            iw0[j] = ow * g.stride - g.pad_w;
             pix[j] = X + (int64_t)img * g.img_stride +
                      ((int64_t)ih0[j] * g.w + iw0[j]) * g.c + grp * 4;
         }
@@ -332,7 +332,7 @@ struct DlImrLoader {
         const int img = n / hw, rem = n - img * hw;
         const int oh = rem / g.wo, ow = rem - oh * g.wo;
         ih0 = nok ? oh * g.stride - g.pad : -(1 << 29);
-        iw0 = ow * g.stride - g.pad;
+        iw0 = ow * g.stride - g.pad_w;
         pix = X + (int64_t)img * g.img_stride + (int64_t)(oh * g.stride - g.pad) * sh +
               (int64_t)iw0 * sw;
 #pragma unroll
@@ -423,7 +423,7 @@ struct DlImwLoader {
             ci[j] = n - tap * g.c;
             const int r = tap / g.kw;
             dr[j] = r - g.pad;
-            ds[j] = (tap - r * g.kw) - g.pad;
+            ds[j] = (tap - r * g.kw) - g.pad_w;
         }
     }
 
@@ -470,7 +470,7 @@ struct DlImwTail {
                 const int oh = rem / g.wo, ow = rem - oh * g.wo;
                 const int tap = n / g.c, c = n - tap * g.c;
                 const int r = tap / g.kw, s = tap - r * g.kw;
-                const int ih = oh * g.stride - g.pad + r, iw = ow * g.stride - g.pad + s;
+                const int ih = oh * g.stride - g.pad + r, iw = ow * g.stride - g.pad_w + s;
                 if ((unsigned)ih < (unsigned)g.h && (unsigned)iw < (unsigned)g.w)
                     x = X[(int64_t)img * g.img_stride + ((int64_t)ih * g.w + iw) * g.c + c];
             }

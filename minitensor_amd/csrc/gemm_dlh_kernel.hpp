@@ -108,7 +108,7 @@ gemm_f32_dlh(GemmParams p, HaloTable ht) {
             const int prow = e / pw, pcol = e - prow * pw;
             const int R = R0 + prow;
             const int img = R / hp;
-            const int ih = R - img * hp - g.pad, iw = pcol - g.pad;
+            const int ih = R - img * hp - g.pad, iw = pcol - g.pad_w;
             if (img < nimg && (unsigned)ih < (unsigned)g.h && (unsigned)iw < (unsigned)g.w)
                 soff[i] = (img - img0) * (int)g.img_stride + ih * (int)g.sh + iw * (int)g.sw;
         }

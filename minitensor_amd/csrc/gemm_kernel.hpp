@@ -82,6 +82,8 @@ enum : int {
 struct ConvGeom {
     int64_t img_stride;
     int c, h, w, kh, kw, stride, pad, ho, wo;
+    int pad_w;            // padding of the w axis (pad: the h axis); either may be
+                          // negative (a window that starts inside the input)
     int64_t sc, sh, sw;   // L_IMR: element strides of a channel, a row, a column
     int hp, pw;           // L_IMH: padded rows per image, (ho-1)*stride + kh, and
                           // padded columns, (wo-1)*stride + kw
@@ -136,8 +138,12 @@ struct GemmParams {
     const float* B; int64_t b_mn, b_k, b_b;   // B(k,n) = B[n*b_mn + k*b_k + b*b_b]
     float* C; int64_t c_m, c_n, c_b;          // C(m,n) = C[m*c_m + col(n) + b*c_b]
     // col(n) = n*c_n when c_n_inner >= N, otherwise
-    // (n / c_n_inner)*c_n_outer + (n % c_n_inner)*c_n (NCHW scatter of a conv GEMM).
+    // (n / c_n_inner)*c_n_outer + (n % c_n_inner)*c_n (NCHW scatter of a conv GEMM),
+    // and with c_n_inner2 > 0 (a multiple of c_n_inner) one more level:
+    // (n / c_n_inner2)*c_n_outer2 + col(n % c_n_inner2) (a stride phase of a
+    // strided convolution's input gradient: image, row, column).
     int64_t c_n_inner, c_n_outer;
+    int64_t c_n_inner2, c_n_outer2;
     const float* bias; int64_t bias_stride; int bias_axis;  // 0 none, 1 per row m, 2 per column n
     float beta;
     float* ws;                                // split-K partials [splits][batch][M][N]
@@ -310,9 +316,17 @@ __device__ __forceinline__ f32x16 mfma_32x32x2(float a, float b, const f32x16& c
 // (c_n_inner < N < 2^31 when the scatter applies: a 32-bit division.)
 __device__ __forceinline__ int64_t col_offset(const GemmParams& p, int n) {
     if (p.c_n_inner >= p.N) return (int64_t)n * p.c_n;
+    int64_t base = 0;
+    unsigned u = (unsigned)n;
+    if (p.c_n_inner2 > 0) {
+        const unsigned inner2 = (unsigned)p.c_n_inner2;
+        const unsigned nb = u / inner2;
+        base = (int64_t)nb * p.c_n_outer2;
+        u -= nb * inner2;
+    }
     const unsigned inner = (unsigned)p.c_n_inner;
-    const unsigned no = (unsigned)n / inner, ni = (unsigned)n - no * inner;
-    return (int64_t)no * p.c_n_outer + (int64_t)ni * p.c_n;
+    const unsigned no = u / inner, ni = u - no * inner;
+    return base + (int64_t)no * p.c_n_outer + (int64_t)ni * p.c_n;
 }
 
 // s_waitcnt immediate (gfx9 encoding): vmcnt(n), lgkmcnt(0), expcnt unconstrained.

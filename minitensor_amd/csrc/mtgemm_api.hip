@@ -811,7 +811,9 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
     // aligned, and (for a scattered output) never straddle a column group.
     p.c_vec = p.c_n == 1 && (N & 3) == 0 && ((uintptr_t)p.C & 15u) == 0 && (p.c_m & 3) == 0 &&
               (batch == 1 || (p.c_b & 3) == 0) &&
-              (p.c_n_inner >= N || ((p.c_n_inner & 3) == 0 && (p.c_n_outer & 3) == 0));
+              (p.c_n_inner >= N || ((p.c_n_inner & 3) == 0 && (p.c_n_outer & 3) == 0 &&
+                                    (p.c_n_inner2 <= 0 ||
+                                     ((p.c_n_inner2 & 3) == 0 && (p.c_n_outer2 & 3) == 0))));
     // Row sums of A are fused only into a direct-to-LDS launch of two
     // mn-contiguous operands without split-K (the caller sees p.rowsum cleared
     // and computes them separately).
@@ -1502,7 +1504,7 @@ int run_conv_implicit(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, const flo
     ConvGeom& g = p.cv;
     g.img_stride = img_stride;
     g.c = (int)c; g.h = (int)d->h; g.w = (int)d->w;
-    g.kh = (int)d->kh; g.kw = (int)d->kw; g.stride = (int)d->stride; g.pad = (int)d->pad;
+    g.kh = (int)d->kh; g.kw = (int)d->kw; g.stride = (int)d->stride; g.pad = g.pad_w = (int)d->pad;
     g.ho = (int)Ho; g.wo = (int)Wo;
     return launch_gemm(p, true, L_KV, L_IM, wsp + iw.xt + iw.wt, ws_bytes - iw.xt - iw.wt, s);
 }
@@ -1544,7 +1546,7 @@ int run_conv_nchw(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, const float* 
     g.img_stride = in_strides[0];
     g.sc = in_strides[1]; g.sh = in_strides[2]; g.sw = in_strides[3];
     g.c = (int)d->c_in; g.h = (int)d->h; g.w = (int)d->w;
-    g.kh = (int)d->kh; g.kw = (int)d->kw; g.stride = (int)d->stride; g.pad = (int)d->pad;
+    g.kh = (int)d->kh; g.kw = (int)d->kw; g.stride = (int)d->stride; g.pad = g.pad_w = (int)d->pad;
     g.ho = (int)Ho; g.wo = (int)Wo;
     set_halo_geometry(g);
     return launch_gemm(p, true, L_KV, L_IMR, workspace, ws_bytes, s);
@@ -1573,6 +1575,238 @@ bool dx_as_forward(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, mt_conv2d_de
 // Bytes of the flipped, transposed weights of the implicit dX.
 size_t flipped_ws(const mt_conv2d_desc* d) {
     return align_up((size_t)d->c_in * d->c_out * d->kh * d->kw * sizeof(float), 256);
+}
+
+// ---- input gradient by stride phase ---------------------------------------------
+// dX[ci][ih][iw] = sum over co and the taps (r, t) with ih + pad - r and
+// iw + pad - t multiples of the stride s of W[co][ci][r][t] ·
+// dY[co][(ih + pad - r)/s][(iw + pad - t)/s].  Split the input pixels by
+// phase (ih % s, iw % s) = (ph, pw).  The taps that reach phase row ph are
+// r = rh0 + s*j, rh0 = (ph + pad) % s, j < jh = ceil((kh - rh0)/s), and for
+// the phase row i' (ih = ph + s*i') they read dY row i' + qh - j, qh =
+// (ph + pad) / s: a stride-1 convolution of dY with the phase's flipped
+// sub-kernel (a = jh - 1 - j), padding jh - 1 - qh -- negative, or unequal
+// between the axes, for some geometries (ConvGeom::pad, pad_w) -- whose
+// hp x wp output pixels (hp = ceil((h - ph)/s)) go to every s-th pixel of dX
+// (the three-level column scatter of GemmParams).  Each phase is one
+// implicit GEMM, C[c_in, n*hp*wp] = Wph[c_in, c_out*jh*jw] · im2col(dY):
+// no column buffer (col2im), and dY is read once per tap, as in the forward
+// convolution.  A phase no tap reaches (jh or jw = 0, e.g. the odd pixels of
+// a 1x1 stride-2 layer) is zero.
+constexpr int kDxMaxStride = 4;
+struct DxPhase {
+    int ph, pw;          // the phase
+    int rh0, rw0;        // its first taps
+    int jh, jw;          // taps of its sub-kernel per axis (0: no tap reaches it)
+    int pad_h, pad_w;    // padding of its stride-1 sub-convolution
+    int hp, wp;          // its output rows / columns
+    int k;               // c_out * jh * jw
+    int64_t woff;        // its weights in the phase-weight block (floats)
+};
+struct DxPhases {
+    int s, n;            // stride, s * s phases
+    DxPhase f[kDxMaxStride * kDxMaxStride];
+};
+
+DxPhases dx_phases(const mt_conv2d_desc* d) {
+    DxPhases t{};
+    const int s = (int)d->stride;
+    t.s = s;
+    t.n = s * s;
+    int64_t woff = 0;
+    for (int ph = 0; ph < s; ++ph)
+        for (int pw = 0; pw < s; ++pw) {
+            DxPhase& f = t.f[ph * s + pw];
+            f.ph = ph; f.pw = pw;
+            f.rh0 = (int)((ph + d->pad) % s);
+            f.rw0 = (int)((pw + d->pad) % s);
+            f.jh = f.rh0 < d->kh ? (int)((d->kh - f.rh0 + s - 1) / s) : 0;
+            f.jw = f.rw0 < d->kw ? (int)((d->kw - f.rw0 + s - 1) / s) : 0;
+            f.pad_h = f.jh - 1 - (int)((ph + d->pad) / s);
+            f.pad_w = f.jw - 1 - (int)((pw + d->pad) / s);
+            f.hp = d->h > ph ? (int)((d->h - ph + s - 1) / s) : 0;
+            f.wp = d->w > pw ? (int)((d->w - pw + s - 1) / s) : 0;
+            f.k = (int)(d->c_out * f.jh * f.jw);
+            f.woff = woff;
+            woff += d->c_in * f.k;   // every tap is in exactly one phase: sum = c_in*c_out*kh*kw
+        }
+    return t;
+}
+
+// The phased dX applies for strides up to kDxMaxStride.  Channels-last
+// (cl): c_out % 16 == 0, dY copied to channels-last once.  Otherwise the
+// NCHW kernel reads dY in place, and every phase's weight rows must be
+// 16-byte vectors (c_out*jh*jw % 4 == 0).  Extents stay inside the 32-bit
+// window arithmetic of the implicit loaders.
+bool dx_phased(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, bool* cl) {
+    if (d->stride > kDxMaxStride || d->c_out <= 0 || d->c_in <= 0 || Ho * Wo >= kMaxDim ||
+        d->c_out * d->kh * d->kw >= kMaxDim ||
+        d->h * d->w >= kMaxDim || d->kh + Ho >= ((int64_t)1 << 29) || d->kw + Wo >= ((int64_t)1 << 29))
+        return false;
+    *cl = (d->c_out & 15) == 0;
+    if (*cl) return true;
+    const DxPhases t = dx_phases(d);
+    for (int i = 0; i < t.n; ++i)
+        if ((t.f[i].k & 3) != 0) return false;
+    return true;
+}
+
+// Sub-kernel weights of every phase from the OIHW weights, one thread per
+// weight: W[co][ci][r][t] belongs to phase ((r - pad) mod s, (t - pad) mod s),
+// tap a = jh - 1 - (r - rh0)/s, b = jw - 1 - (t - rw0)/s of its flipped
+// sub-kernel, stored at f.woff + ci*f.k + k with k = (a*jw + b)*c_out + co for
+// the channels-last kernel (its K order: tap, channel) or (co*jh + a)*jw + b
+// for the NCHW one (OIHW of the sub-convolution).
+__global__ void __launch_bounds__(256)
+dx_phase_weights_f32(const float* W, float* out, DxPhases t, int c_out, int c_in, int kh, int kw,
+                     int pad, int cl) {
+    const int64_t total = (int64_t)c_out * c_in * kh * kw;
+    const int s = t.s;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int tt = (int)(e % kw);
+        const int64_t e1 = e / kw;
+        const int r = (int)(e1 % kh);
+        const int64_t e2 = e1 / kh;
+        const int ci = (int)(e2 % c_in), co = (int)(e2 / c_in);
+        const int ph = ((r - pad) % s + s) % s, pw = ((tt - pad) % s + s) % s;
+        const DxPhase& f = t.f[ph * s + pw];
+        const int a = f.jh - 1 - (r - f.rh0) / s, b = f.jw - 1 - (tt - f.rw0) / s;
+        const int k = cl ? (a * f.jw + b) * c_out + co : (co * f.jh + a) * f.jw + b;
+        out[f.woff + (int64_t)ci * f.k + k] = W[e];
+    }
+}
+
+// Workspace of one implicit-operand GEMM (L_IM / L_IMR: the direct-to-LDS
+// configurations 0-3; L_IMW, imw: all of them, its own efficiency table),
+// including a forced configuration's partials: what launch_gemm may use.
+size_t implicit_gemm_ws(int64_t M, int64_t N, int64_t K, bool imw) {
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    const int cus = device_cu_count();
+    size_t ws = make_plan(M, N, K, 1, cus, true, true, imw, false, imw).ws_bytes;
+    Plan f;
+    if (forced_plan(M, N, K, 1, true, false, imw, &f)) ws = std::max(ws, f.ws_bytes);
+    return ws;
+}
+
+// Layout of the phased dX workspace: [channels-last dY (cl)][phase weights][GEMM].
+struct DxPhasedWs {
+    size_t dyt, wph, gemm;
+};
+DxPhasedWs dx_phased_ws(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, bool cl) {
+    DxPhasedWs w{};
+    w.dyt = cl ? align_up((size_t)d->n * d->c_out * Ho * Wo * sizeof(float), 256) : 0;
+    w.wph = flipped_ws(d);
+    const DxPhases t = dx_phases(d);
+    for (int i = 0; i < t.n; ++i) {
+        const DxPhase& f = t.f[i];
+        if (f.k > 0 && f.hp > 0 && f.wp > 0)
+            w.gemm = std::max(w.gemm, implicit_gemm_ws(d->c_in, d->n * f.hp * f.wp, f.k, false));
+    }
+    return w;
+}
+
+// Workspace of the path mt_conv2d_bwd_input_f32 takes for d.
+size_t dx_ws(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo) {
+    const int64_t kg = d->c_in * d->kh * d->kw, np = d->n * Ho * Wo;
+    if (np == 0 || d->c_out == 0 || d->n * d->c_in * d->h * d->w == 0) return 0;
+    const int64_t nx = d->n * d->h * d->w, kx = d->c_out * d->kh * d->kw;
+    mt_conv2d_desc t;
+    if (dx_as_forward(d, Ho, Wo, &t) && implicit_geometry(&t)) {
+        const ImplicitWs iw = implicit_ws(&t);
+        return iw.xt + iw.wt + implicit_gemm_ws(d->c_in, nx, kx, false);
+    }
+    if (dx_as_forward(d, Ho, Wo, &t) && nchw_implicit(&t))
+        return flipped_ws(d) + implicit_gemm_ws(d->c_in, nx, kx, false);
+    bool cl = false;
+    if (dx_phased(d, Ho, Wo, &cl)) {
+        const DxPhasedWs w = dx_phased_ws(d, Ho, Wo, cl);
+        return w.dyt + w.wph + w.gemm;
+    }
+    return align_up((size_t)kg * np * sizeof(float), 256) +
+           align_up((size_t)d->c_out * np * sizeof(float), 256) +
+           plan_ws(kg, np, d->c_out, 1, device_cu_count());
+}
+
+// Whether the implicit weight gradient reads dY in NCHW (L_KVI) rather than a
+// [c_out][n*hw] copy: whole 16-byte groups of one image per row (and a
+// 16-byte-aligned dY, checked at the call).
+bool dw_reads_dy_nchw(int64_t np, int64_t hw) {
+    return (np & 15) == 0 && (hw & 3) == 0 && np < ((int64_t)1 << 24);
+}
+
+// Workspace of the path of the weight gradient (and the bias gradient it
+// carries) for d, for a 16-byte-aligned dY.
+size_t dw_ws(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo) {
+    const int64_t kg = d->c_in * d->kh * d->kw, np = d->n * Ho * Wo;
+    if (np == 0 || d->c_out == 0 || kg == 0) return 0;
+    const size_t dyt_b = align_up((size_t)d->c_out * np * sizeof(float), 256);
+    if (implicit_dw(d, np)) {
+        const size_t xt_b = align_up((size_t)d->n * d->c_in * d->h * d->w * sizeof(float), 256);
+        return xt_b + (dw_reads_dy_nchw(np, Ho * Wo) ? 0 : dyt_b) +
+               implicit_gemm_ws(d->c_out, kg, np, true);
+    }
+    return align_up((size_t)kg * np * sizeof(float), 256) + dyt_b +
+           plan_ws(d->c_out, kg, np, 1, device_cu_count());
+}
+
+int run_dx_phased(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, bool cl,
+                  const float* grad_out, const float* weight, float* grad_input, void* workspace,
+                  size_t ws_bytes, hipStream_t s) {
+    const DxPhasedWs w = dx_phased_ws(d, Ho, Wo, cl);
+    if (!workspace || ws_bytes < w.dyt + w.wph || ((uintptr_t)workspace & 15u) != 0)
+        return MT_ERR_WORKSPACE;
+    char* wsp = static_cast<char*>(workspace);
+    const DxPhases t = dx_phases(d);
+    const int64_t hw = Ho * Wo;
+    float* dyt = reinterpret_cast<float*>(wsp);
+    float* wph = reinterpret_cast<float*>(wsp + w.dyt);
+    if (cl &&
+        launch_transposes(tjob(grad_out, d->c_out * hw, hw, Wo, 1, Wo, d->c_out, hw, d->n, dyt),
+                          TJob{}, s) != hipSuccess)
+        return MT_ERR_HIP;
+    const int64_t nw = d->c_out * d->c_in * d->kh * d->kw;
+    hipLaunchKernelGGL(dx_phase_weights_f32, dim3(grid_for(nw)), dim3(256), 0, s, weight, wph, t,
+                       (int)d->c_out, (int)d->c_in, (int)d->kh, (int)d->kw, (int)d->pad,
+                       cl ? 1 : 0);
+    if (capture_safe_last_error() != hipSuccess) return MT_ERR_HIP;
+    bool empty = false;   // a phase with pixels that no tap reaches
+    for (int i = 0; i < t.n; ++i)
+        empty |= t.f[i].hp > 0 && t.f[i].wp > 0 && t.f[i].k == 0;
+    if (empty) {
+        const int64_t total = d->n * d->c_in * d->h * d->w;
+        hipLaunchKernelGGL(fill_f32, dim3(grid_for(total)), dim3(256), 0, s, grad_input, total,
+                           0.f);
+        if (capture_safe_last_error() != hipSuccess) return MT_ERR_HIP;
+    }
+    char* gws = wsp + w.dyt + w.wph;
+    const size_t gws_b = ws_bytes - w.dyt - w.wph;
+    for (int i = 0; i < t.n; ++i) {
+        const DxPhase& f = t.f[i];
+        if (f.k == 0 || f.hp == 0 || f.wp == 0) continue;
+        GemmParams p{};
+        p.A = wph + f.woff; p.a_mn = f.k; p.a_k = 1; p.a_b = 0;
+        p.B = cl ? dyt : grad_out;
+        p.C = grad_input + (int64_t)f.ph * d->w + f.pw;
+        p.c_m = d->h * d->w; p.c_n = t.s; p.c_b = 0;
+        p.c_n_inner = f.wp; p.c_n_outer = t.s * d->w;
+        p.c_n_inner2 = (int64_t)f.hp * f.wp; p.c_n_outer2 = d->c_in * d->h * d->w;
+        p.bias = nullptr; p.bias_stride = 0; p.bias_axis = MT_BIAS_NONE;
+        p.beta = 0.f;
+        p.M = (int)d->c_in; p.N = (int)(d->n * f.hp * f.wp); p.K = f.k; p.batch = 1;
+        ConvGeom& g = p.cv;
+        g.img_stride = d->c_out * hw;
+        g.c = (int)d->c_out; g.h = (int)Ho; g.w = (int)Wo;
+        g.kh = f.jh; g.kw = f.jw; g.stride = 1; g.pad = f.pad_h; g.pad_w = f.pad_w;
+        g.ho = f.hp; g.wo = f.wp;
+        if (!cl) {
+            g.sc = hw; g.sh = Wo; g.sw = 1;
+            set_halo_geometry(g);
+        }
+        const int rc = launch_gemm(p, true, L_KV, cl ? L_IM : L_IMR, gws, gws_b, s);
+        if (rc != MT_OK) return rc;
+    }
+    return MT_OK;
 }
 
 }  // namespace
@@ -1679,15 +1913,15 @@ size_t mt_conv2d_workspace_f32(const mt_conv2d_desc* d) {
     if (!conv_dims(d, &Ho, &Wo)) return 0;
     const int64_t kg = d->c_in * d->kh * d->kw, np = d->n * Ho * Wo;
     if (np == 0 || d->c_out == 0) return 0;
-    const size_t gemm = plan_ws(d->c_out, np, kg, 1, device_cu_count());
     if (implicit_geometry(d) && d->h * d->w < kMaxDim) {   // channels-last kernel
         const ImplicitWs iw = implicit_ws(d);
-        return iw.xt + iw.wt + gemm;
+        return iw.xt + iw.wt + implicit_gemm_ws(d->c_out, np, kg, false);
     }
     // the NCHW-view kernel: split-K partials, and room for an aligned copy of
     // the weights (used only when the caller's are not 16-byte aligned)
-    if (nchw_implicit(d)) return nchw_weight_ws(d) + gemm;
-    return align_up((size_t)kg * np * sizeof(float), 256) + gemm;
+    if (nchw_implicit(d)) return nchw_weight_ws(d) + implicit_gemm_ws(d->c_out, np, kg, false);
+    return align_up((size_t)kg * np * sizeof(float), 256) +
+           plan_ws(d->c_out, np, kg, 1, device_cu_count());
 }
 
 int mt_conv2d_fwd_strided_f32(const mt_conv2d_desc* d, const float* input,
@@ -1762,29 +1996,8 @@ int mt_conv2d_fwd_f32(const mt_conv2d_desc* d, const float* input, const float* 
 size_t mt_conv2d_bwd_workspace_f32(const mt_conv2d_desc* d) {
     int64_t Ho, Wo;
     if (!conv_dims(d, &Ho, &Wo)) return 0;
-    const int64_t kg = d->c_in * d->kh * d->kw, np = d->n * Ho * Wo;
-    if (np == 0 || d->c_out == 0 || kg == 0) return 0;
-    const int cus = device_cu_count();
-    const size_t bufs = align_up((size_t)kg * np * sizeof(float), 256) +
-                        align_up((size_t)d->c_out * np * sizeof(float), 256);
-    const size_t g = std::max(plan_ws(d->c_out, kg, np, 1, cus),
-                              plan_ws(kg, np, d->c_out, 1, cus));
-    size_t need = bufs + g;
-    if (implicit_dw(d, np))
-        need = std::max(need, align_up((size_t)d->n * d->c_in * d->h * d->w * sizeof(float), 256) +
-                                  align_up((size_t)d->c_out * np * sizeof(float), 256) +
-                                  plan_ws(d->c_out, kg, np, 1, cus, true));
-    mt_conv2d_desc t;
-    if (dx_as_forward(d, Ho, Wo, &t)) {   // implicit dX (usually smaller than the above)
-        const size_t g = plan_ws(d->c_in, d->n * d->h * d->w, d->c_out * d->kh * d->kw, 1, cus);
-        if (implicit_geometry(&t)) {
-            const ImplicitWs iw = implicit_ws(&t);
-            need = std::max(need, iw.xt + iw.wt + g);
-        } else {
-            need = std::max(need, flipped_ws(d) + g);
-        }
-    }
-    return need;
+    // the paths the dX and the dW (+ db) calls take, one after the other
+    return std::max(dx_ws(d, Ho, Wo), dw_ws(d, Ho, Wo));
 }
 
 }  // extern "C"
@@ -1811,18 +2024,20 @@ int conv_bwd_weight(const mt_conv2d_desc* d, const float* input, const float* gr
         // the B operand gathered from a channels-last copy of the input and the
         // columns scattered to OIHW by the epilogue: col(n) = tap + ci*kh*kw.
         const size_t xt_b = align_up((size_t)d->n * d->c_in * d->h * d->w * sizeof(float), 256);
-        if (!workspace || ws_bytes < xt_b + dyt_b || ((uintptr_t)workspace & 15u) != 0)
+        // dY is read in NCHW by the GEMM (L_KVI) when every 16-byte group of a
+        // row is four pixels of one image and K holds whole chunks; else it is
+        // copied to dYt [c_out][n][hw] (not counted by the workspace query
+        // when only dY's alignment prevents the NCHW read).  x ->
+        // channels-last in the same launch.
+        const bool kvi = dw_reads_dy_nchw(np, hw) && ((uintptr_t)grad_out & 15u) == 0;
+        const size_t dyb = kvi ? 0 : dyt_b;
+        if (!workspace || ws_bytes < xt_b + dyb || ((uintptr_t)workspace & 15u) != 0)
             return MT_ERR_WORKSPACE;
         char* wsp = static_cast<char*>(workspace);
         float* xt = reinterpret_cast<float*>(wsp);
         float* dyt = reinterpret_cast<float*>(wsp + xt_b);
         int64_t st[4];
         dense_strides(d, st);
-        // dY is read in NCHW by the GEMM (L_KVI) when every 16-byte group of a
-        // row is four pixels of one image and K holds whole chunks; else it is
-        // copied to dYt [c_out][n][hw].  x -> channels-last in the same launch.
-        const bool kvi = (np & 15) == 0 && (hw & 3) == 0 && np < ((int64_t)1 << 24) &&
-                         ((uintptr_t)grad_out & 15u) == 0;
         if (launch_transposes(tjob(input, st[0], st[1], st[2], st[3], d->w, d->c_in, d->h * d->w,
                                    d->n, xt),
                               kvi ? TJob{}
@@ -1846,14 +2061,14 @@ int conv_bwd_weight(const mt_conv2d_desc* d, const float* input, const float* gr
         ConvGeom& g = p.cv;
         g.img_stride = d->h * d->w * d->c_in;
         g.c = (int)d->c_in; g.h = (int)d->h; g.w = (int)d->w;
-        g.kh = (int)d->kh; g.kw = (int)d->kw; g.stride = (int)d->stride; g.pad = (int)d->pad;
+        g.kh = (int)d->kh; g.kw = (int)d->kw; g.stride = (int)d->stride; g.pad = g.pad_w = (int)d->pad;
         g.ho = (int)Ho; g.wo = (int)Wo;
         if (grad_bias) {
             p.csum_src = grad_out; p.csum = grad_bias; p.csum_n = (int)d->n;
             p.csum_hw = hw; p.csum_beta = beta_b;
         }
-        const int rc = launch_gemm(p, true, kvi ? L_KVI : L_KV, L_IMW, wsp + xt_b + dyt_b,
-                                   ws_bytes - xt_b - dyt_b, s);
+        const int rc = launch_gemm(p, true, kvi ? L_KVI : L_KV, L_IMW, wsp + xt_b + dyb,
+                                   ws_bytes - xt_b - dyb, s);
         *db_done = rc == MT_OK && p.csum != nullptr;
         return rc;
     }
@@ -1954,6 +2169,9 @@ int mt_conv2d_bwd_input_f32(const mt_conv2d_desc* d, const float* grad_out, cons
         return run_conv_nchw(&t, d->h, d->w, grad_out, st, wf, nullptr, grad_input, wsp + fb,
                              ws_bytes - fb, s);
     }
+    bool cl = false;
+    if (dx_phased(d, Ho, Wo, &cl))   // strided or non-square: one implicit GEMM per phase
+        return run_dx_phased(d, Ho, Wo, cl, grad_out, weight, grad_input, workspace, ws_bytes, s);
     const size_t col_b = align_up((size_t)kg * np * sizeof(float), 256);
     const size_t dyt_b = align_up((size_t)d->c_out * np * sizeof(float), 256);
     if (!workspace || ws_bytes < col_b + dyt_b) return MT_ERR_WORKSPACE;

@@ -624,7 +624,10 @@ def test_conv_dw_dy_layout(dev, n, c, h, wd, co, split, expect):
 
 
 def test_conv_dw_dy_unaligned(dev):
-    """A dY view that is not 16-byte aligned is copied, not read in place."""
+    """A dY view that is not 16-byte aligned is copied, not read in place.  The
+    workspace query assumes 16-byte-aligned tensors, so the copy needs
+    c_out*n*h_out*w_out floats (rounded up to 256 bytes) more; with only the
+    queried size the call refuses (MT_ERR_WORKSPACE) before any launch."""
     n, c, h, wd, co = 4, 8, 6, 6, 24
     x = oracle.normal((n, c, h, wd), 450)
     w = oracle.normal((co, c, 3, 3), 451)
@@ -634,9 +637,14 @@ def test_conv_dw_dy_unaligned(dev):
     dY = buf[1:].view(n, co, h, wd)
     assert dY.data_ptr() % 16 != 0
     d = mt.Conv2dDesc(n, c, h, wd, co, 3, 3, 1, 1)
-    ws = mt.workspace(mt.lib().mt_conv2d_bwd_workspace_f32(ctypes.byref(d)), dev)
+    need = mt.lib().mt_conv2d_bwd_workspace_f32(ctypes.byref(d))
+    copy = (co * n * h * wd * 4 + 255) // 256 * 256
+    ws = mt.workspace(need + copy, dev)
     dW = torch.empty(co, c, 3, 3, device=dev)
     X = g(x, dev)
+    assert mt.lib().mt_conv2d_bwd_weight_f32(ctypes.byref(d), X.data_ptr(),
+                                             dY.data_ptr(), dW.data_ptr(), 0.0, ws.data_ptr(),
+                                             need, None) == mt.MT_ERR_WORKSPACE
     assert mt.lib().mt_conv2d_bwd_weight_f32(ctypes.byref(d), X.data_ptr(),
                                              dY.data_ptr(), dW.data_ptr(), 0.0, ws.data_ptr(),
                                              ws.numel(), None) == 0
