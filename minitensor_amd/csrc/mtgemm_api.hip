@@ -120,6 +120,7 @@ struct Plan {
     int kps = 0;
     int tiles_m = 0, tiles_n = 0;
     size_t ws_bytes = 0;
+    double cycles = 0;  // the cost model's CU cycles for the plan
 };
 
 constexpr int kBK = 16;
@@ -270,6 +271,7 @@ Plan make_plan_uncached(int64_t M, int64_t N, int64_t K, int64_t batch, int cus,
             if (t < best_t) {
                 best_t = t;
                 best = pl;
+                best.cycles = t;
             }
         }
     }
@@ -283,6 +285,7 @@ Plan make_plan_uncached(int64_t M, int64_t N, int64_t K, int64_t batch, int cus,
             if (t < best_t) {
                 best_t = t;
                 best = pl;
+                best.cycles = t;
             }
         }
     }
@@ -1677,6 +1680,47 @@ dx_phase_weights_f32(const float* W, float* out, DxPhases t, int c_out, int c_in
     }
 }
 
+// Whether the phased dX is expected to beat dcol = Wᵀ·dY + col2im for d.
+// Both run the same flops; the phased GEMMs have c_in rows and a phase's
+// pixels as columns (small when c_in is small or the image is), the column
+// GEMM kg = c_in*kh*kw rows, but its column buffer is written and gathered
+// again.  The cost model prices the GEMMs; measured on seven ResNet layers
+// (3x3 stride 2 at 56/28/14, 1x1 stride 2 at 56/28/14, the 7x7 c_in 3
+// stem; batch 32, graph replay), the phase GEMMs ran 1.4-1.9x their modelled
+// time (short K ranges per phase), so they are priced at kDxPhasedFactor
+// times it, plus the dY copy and zero fill at kDxStreamBytes per CU cycle
+// (5 TB/s); the column path's buffer, dY copy and gather ran at about
+// 2 TB/s (kDxGatherBytes).  This picks the faster path on five of the seven
+// layers and loses 5 and 8 % on the two near-ties (the 3x3 at 28, the 1x1
+// at 28), where "always phased" loses up to 4.5x (the stem: 3 rows).
+constexpr double kDxPhasedFactor = 1.7;
+constexpr double kDxStreamBytes = 2083.0;   // device bytes per CU cycle at 5 TB/s, 2.4 GHz
+constexpr double kDxGatherBytes = 833.0;    // ... at 2 TB/s
+bool dx_prefer_phased(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, bool cl) {
+    // a forced direct-to-LDS configuration skips the rule (the tests' hook
+    // onto the phase GEMMs, as for the halo kernel)
+    if (g_forced.family == MT_FAMILY_DL) return true;
+    const int cus = device_cu_count();
+    const DxPhases t = dx_phases(d);
+    const int64_t kg = d->c_in * d->kh * d->kw, np = d->n * Ho * Wo;
+    const double dx_bytes = 4.0 * d->n * d->c_in * d->h * d->w;
+    double phased = 0, stream = cl ? 8.0 * d->c_out * np : 0.0;
+    for (int i = 0; i < t.n; ++i) {
+        const DxPhase& f = t.f[i];
+        if (f.hp == 0 || f.wp == 0) continue;
+        if (f.k == 0) {
+            stream += dx_bytes * f.hp * f.wp / ((double)d->h * d->w);
+            continue;
+        }
+        phased += make_plan(d->c_in, d->n * f.hp * f.wp, f.k, 1, cus, true, true, false, false)
+                      .cycles;
+    }
+    phased = kDxPhasedFactor * phased + stream / kDxStreamBytes;
+    const double col = make_plan(kg, np, d->c_out, 1, cus, true, true, true, true).cycles +
+                       (8.0 * d->c_out * np + 8.0 * kg * np + dx_bytes) / kDxGatherBytes;
+    return phased < col;
+}
+
 // Workspace of one implicit-operand GEMM (L_IM / L_IMR: the direct-to-LDS
 // configurations 0-3; L_IMW, imw: all of them, its own efficiency table),
 // including a forced configuration's partials: what launch_gemm may use.
@@ -1719,7 +1763,7 @@ size_t dx_ws(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo) {
     if (dx_as_forward(d, Ho, Wo, &t) && nchw_implicit(&t))
         return flipped_ws(d) + implicit_gemm_ws(d->c_in, nx, kx, false);
     bool cl = false;
-    if (dx_phased(d, Ho, Wo, &cl)) {
+    if (dx_phased(d, Ho, Wo, &cl) && dx_prefer_phased(d, Ho, Wo, cl)) {
         const DxPhasedWs w = dx_phased_ws(d, Ho, Wo, cl);
         return w.dyt + w.wph + w.gemm;
     }
@@ -2170,7 +2214,8 @@ int mt_conv2d_bwd_input_f32(const mt_conv2d_desc* d, const float* grad_out, cons
                              ws_bytes - fb, s);
     }
     bool cl = false;
-    if (dx_phased(d, Ho, Wo, &cl))   // strided or non-square: one implicit GEMM per phase
+    if (dx_phased(d, Ho, Wo, &cl) && dx_prefer_phased(d, Ho, Wo, cl))
+        // strided or non-square: one implicit GEMM per stride phase
         return run_dx_phased(d, Ho, Wo, cl, grad_out, weight, grad_input, workspace, ws_bytes, s);
     const size_t col_b = align_up((size_t)kg * np * sizeof(float), 256);
     const size_t dyt_b = align_up((size_t)d->c_out * np * sizeof(float), 256);

@@ -50,29 +50,39 @@ CASES = [
 @pytest.mark.parametrize("case", CASES, ids=[f"{c[1]}-{c[4]}-{c[5]}x{c[6]}-s{c[7]}p{c[8]}-{c[9]}"
                                              for c in CASES])
 def test_dx_by_phase(dev, case):
+    # The library picks the phased or the column path by modelled cost (small
+    # layers like these mostly take the column path); a forced direct-to-LDS
+    # configuration skips that rule, so the phase GEMMs run on every case that
+    # they can take, under two tile configurations.
     n, c, h, w, co, kh, kw, stride, pad, path = case
     ho, wo = oracle.conv_out(h, pad, kh, stride), oracle.conv_out(w, pad, kw, stride)
     x = oracle.normal((n, c, h, w), 11 + c)
     wt = oracle.normal((co, c, kh, kw), 12 + co, std=(2.0 / (c * kh * kw)) ** 0.5)
     dy = oracle.normal((n, co, ho, wo), 13 + kh)
     X, W, dY = (torch.from_numpy(t).to(dev) for t in (x, wt, dy))
+    want, _, _ = oracle.conv2d_backward(x, wt, dy, stride, pad)
     dX, _, _ = mt.conv2d_backward(X, W, dY, stride, pad, need_dw=False, need_db=False)
     torch.cuda.synchronize()
-    cfg = mt.last_config()
-    print(f"[config] {case}: {cfg}", flush=True)
-    if path == "cl":
-        assert "b=im2col " in cfg + " ", cfg
-    elif path == "nchw":
-        assert "b=im2col_nchw" in cfg or "b=im2col_halo" in cfg, cfg
-    else:
-        assert "im2col" not in cfg, cfg
-    want, _, _ = oracle.conv2d_backward(x, wt, dy, stride, pad)
-    got = dX.cpu().numpy()
-    assert_close(got, want, co * kh * kw, amax(dy), amax(wt), f"dX {case}")
-    # deterministic: a second call gives the same bits
-    dX2, _, _ = mt.conv2d_backward(X, W, dY, stride, pad, need_dw=False, need_db=False)
-    torch.cuda.synchronize()
-    assert np.array_equal(got.view(np.uint32), dX2.cpu().numpy().view(np.uint32))
+    print(f"[config] {case} auto: {mt.last_config()}", flush=True)
+    assert_close(dX.cpu().numpy(), want, co * kh * kw, amax(dy), amax(wt), f"dX {case} auto")
+    for cfg_i in (1, 3):
+        with mt.forced_config(mt.FAMILY_DL, cfg_i, 1):
+            dX, _, _ = mt.conv2d_backward(X, W, dY, stride, pad, need_dw=False, need_db=False)
+            torch.cuda.synchronize()
+            cfg = mt.last_config()
+            dX2, _, _ = mt.conv2d_backward(X, W, dY, stride, pad, need_dw=False, need_db=False)
+            torch.cuda.synchronize()
+        print(f"[config] {case} forced {cfg_i}: {cfg}", flush=True)
+        if path == "cl":
+            assert "b=im2col " in cfg + " ", cfg
+        elif path == "nchw":
+            assert "b=im2col_nchw" in cfg or "b=im2col_halo" in cfg, cfg
+        else:
+            assert "im2col" not in cfg, cfg
+        got = dX.cpu().numpy()
+        assert_close(got, want, co * kh * kw, amax(dy), amax(wt), f"dX {case} forced {cfg_i}")
+        # deterministic: a second call gives the same bits
+        assert np.array_equal(got.view(np.uint32), dX2.cpu().numpy().view(np.uint32))
 
 
 def test_dx_by_phase_exact_workspace(dev):
