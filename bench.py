@@ -18,12 +18,18 @@ repeats the reference's own protocol (one timed call, then 200 ms / that
 time trials) for comparison; it is not `value`.
 
 Secondary lines (the other benchmark configs: ms and TFLOPS, HBM GB/s for
-the batched one) are reported under "secondary".  Their kernels take
-10-100 us, less than a Python/ctypes call, so `ms` is device time: 20 calls
-are captured into a HIP graph and the graph is replayed between HIP events;
-min / median / mean are over the replays.  `ms_eager_python` is the same
-calls from a Python loop.  Config 3 is also timed with B materialised (a
-strided copy into a dense Bᵀ, then the GEMM) to show what the view saves.
+the batched one and the reference's HBM-bound "skinny" rows) are reported
+under "secondary".  Their kernels take 7-100 us, less than a Python/ctypes
+call, so `ms` is device time: 20 or more calls (about 1 ms of GPU work, at
+most 200) are captured into a HIP graph and the graph is replayed between
+HIP events; min / median / mean are over the replays.  `ms_eager_python` is
+the same calls from a Python loop.  Config 3 is also timed with B
+materialised (a strided copy into a dense Bᵀ, then the GEMM) to show what
+the view saves.
+
+`sustained`: the headline GEMM back to back for --sustained-seconds (2.5 s
+by default), an event after every step, with the driver's clock, power and
+temperature readings over the window (amdsmi, when importable).
 
 CPU baselines (reported baselines only, never the target): the C
 restatement of the reference CPU path in oracle/ (matmul_cpu,
@@ -61,6 +67,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--sustained-seconds", type=float, default=SUSTAINED_S,
+                   help="length of the sustained back-to-back window of the headline GEMM")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run a 256 MiB device copy (rocprof counter calibration)")
     p.add_argument("--only", default="",
@@ -141,13 +149,19 @@ def time_events(fn, iters: int, warmup: int) -> float:
     return start.elapsed_time(stop) / iters
 
 
-def time_graph(fn, calls: int = 20, replays: int = 10, preroll_ms: float = PREROLL_MS / 2) -> list:
+def time_graph(fn, calls: int = 20, replays: int = 10, preroll_ms: float = PREROLL_MS / 2,
+               per_call_ms: float = 0.0) -> list:
     """Device ms per call of fn for each replay: `calls` calls captured into
     one HIP graph, replayed `replays` times with an event around each replay,
     after about preroll_ms of untimed replays (so that every workload is timed
     at the clocks of sustained work, not on the ramp out of the previous
     one's host-side set-up).  Removes the Python/ctypes launch overhead, which
-    exceeds the kernel time of the small configs."""
+    exceeds the kernel time of the small configs.  Given an estimate of the
+    time per call, the graph holds enough calls (up to 200) for about 1 ms of
+    GPU work per replay, so that the host's launch of the next replay never
+    leaves the GPU idle inside a timed interval."""
+    if per_call_ms > 0:
+        calls = max(calls, min(200, int(1.0 / per_call_ms) + 1))
     import torch
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -185,12 +199,65 @@ SECONDARY = ("c1", "c3", "c4", "c5a", "c5b", "skinny")
 SUSTAINED_S = 2.5
 
 
+class ClockSampler:
+    """Reads the GPU's clocks, socket power and hotspot temperature from the
+    driver (amdsmi) every 100 ms on a side thread while a window runs; None
+    when amdsmi is missing or refuses (the measurement never depends on it)."""
+
+    def __init__(self):
+        import threading
+        self.samples, self.err = [], None
+        self._stop = threading.Event()
+        self._th = threading.Thread(target=self._run, daemon=True)
+
+    def _run(self):
+        try:
+            import amdsmi
+            amdsmi.amdsmi_init(amdsmi.AmdSmiInitFlags.INIT_AMD_GPUS)
+            handles = amdsmi.amdsmi_get_processor_handles()
+            if len(handles) != 1:
+                self.err = f"{len(handles)} GPUs visible"
+                return
+            t0 = time.perf_counter()
+            while not self._stop.is_set():
+                m = amdsmi.amdsmi_get_gpu_metrics_info(handles[0])
+                clks = [c for c in (m.get("current_gfxclks") or []) if isinstance(c, int)]
+                # the driver refreshes its table about once a second: the first
+                # second still shows the idle clocks before the window
+                if time.perf_counter() - t0 >= 1.0:
+                    self.samples.append((clks, m.get("current_socket_power"),
+                                         m.get("temperature_hotspot")))
+                self._stop.wait(0.1)
+        except Exception as e:   # noqa: BLE001 -- optional instrumentation
+            self.err = repr(e)[:120]
+
+    def __enter__(self):
+        self._th.start()
+        return self
+
+    def __exit__(self, *exc):
+        self._stop.set()
+        self._th.join(timeout=5)
+
+    def summary(self):
+        if not self.samples:
+            return {"error": self.err} if self.err else None
+        clks = [c for s in self.samples for c in s[0]]
+        pw = [s[1] for s in self.samples if isinstance(s[1], (int, float))]
+        tp = [s[2] for s in self.samples if isinstance(s[2], (int, float))]
+        rng = (lambda v: [min(v), statistics.median(v), max(v)] if v else None)  # noqa: E731
+        return {"samples_after_first_second": len(self.samples),
+                "gfxclk_mhz_per_xcd_min_median_max": rng(clks),
+                "socket_power_w_min_median_max": rng(pw), "hotspot_c_min_median_max": rng(tp)}
+
+
 def sustained(step, flops: float, seconds: float = SUSTAINED_S) -> dict:
     """The headline GEMM back to back for `seconds` of GPU time, an event
     after every step (the queue is kept about 64 steps deep, so the GPU never
     idles): min / median / mean of the per-step times over the whole window,
     the mean over its last second, and the mean of its first 100 steps (the
-    regime of the short timed window)."""
+    regime of the short timed window); the driver's clock, power and
+    temperature readings over the window beside them."""
     import torch
     stream = torch.cuda.current_stream()
     torch.cuda.synchronize()
@@ -202,13 +269,14 @@ def sustained(step, flops: float, seconds: float = SUSTAINED_S) -> dict:
     torch.cuda.synchronize()
     n = max(200, int(seconds * 1e3 / max(t0.elapsed_time(t1), 1e-3)))
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
-    evs[0].record(stream)
-    for i in range(n):
-        step()
-        evs[i + 1].record(stream)
-        if i >= 64:
-            evs[i - 63].synchronize()
-    torch.cuda.synchronize()
+    with ClockSampler() as clocks:
+        evs[0].record(stream)
+        for i in range(n):
+            step()
+            evs[i + 1].record(stream)
+            if i >= 64:
+                evs[i - 63].synchronize()
+        torch.cuda.synchronize()
     per = [evs[i].elapsed_time(evs[i + 1]) for i in range(n)]
     span = evs[0].elapsed_time(evs[-1])
     acc, last = 0.0, []
@@ -220,11 +288,20 @@ def sustained(step, flops: float, seconds: float = SUSTAINED_S) -> dict:
     st = _stats(per)
     first = sum(per[:100]) / 100
     last_mean = sum(last) / len(last)
+    by_second, acc, seg = [], 0.0, []
+    for p in per:   # mean step time of each second of the window
+        seg.append(p)
+        acc += p
+        if acc >= 1000.0:
+            by_second.append(round(sum(seg) / len(seg), 4))
+            acc, seg = 0.0, []
     return {"steps": n, "seconds": round(span / 1e3, 3), "ms_min": st["min"],
             "ms_median": st["median"], "ms_mean": st["mean"],
             "ms_mean_first_100": round(first, 5), "ms_mean_last_second": round(last_mean, 5),
             "tflops_mean": round(flops / st["mean"] / 1e9, 3),
-            "tflops_last_second": round(flops / last_mean / 1e9, 3)}
+            "tflops_last_second": round(flops / last_mean / 1e9, 3),
+            "ms_mean_by_second": by_second[:60],
+            "driver_readings": clocks.summary()}
 
 
 def secondary(dev, only=SECONDARY) -> dict:
@@ -247,7 +324,7 @@ def secondary(dev, only=SECONDARY) -> dict:
     def both(fn, iters, warmup):
         """(per-replay device ms from graph replay, eager ms of the Python call loop)."""
         eager = time_events(fn, iters, warmup)
-        return time_graph(fn), eager
+        return time_graph(fn, per_call_ms=eager), eager
 
     def rec(name, times, flops, bytes_=None, cfg=None):
         per, eager = times
@@ -542,7 +619,7 @@ def main():
             step = headline_step()
             for _ in range(args.warmup):
                 step()
-            res["sustained"] = sustained(step, flops)
+            res["sustained"] = sustained(step, flops, args.sustained_seconds)
             res["sustained"]["kernel"] = mt.last_config()
         if args.copy_probe:
             copy_probe(dev)
@@ -559,7 +636,7 @@ def main():
     st = _stats(per_ms)
     ref_win = reference_window(step)
     ref_win["tflops"] = round(flops / ref_win["ms_mean"] / 1e9, 3)
-    sus = sustained(step, flops)
+    sus = sustained(step, flops, args.sustained_seconds)
 
     if args.copy_probe:
         copy_probe(dev)

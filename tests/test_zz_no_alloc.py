@@ -69,6 +69,29 @@ def test_two_calls_in_a_row_match_the_workspace_entry_point(dev):
         assert_close(got, exp, K, amax(a), amax(b), f"noalloc {M}x{N}x{K}", extra=1e-6)
 
 
+def test_gemv_split_partials_in_the_static_buffer(dev):
+    """The vector-ALU GEMV's split-K partials also go to the static buffer:
+    two calls in a row (the second smaller), each equal to mt_gemm_f32."""
+    for (M, N, K), seed in (((1, 4096, 4096), 3), ((3, 1024, 2048), 4)):
+        a = oracle.uniform((M, K), 10 + seed)
+        b = oracle.uniform((K, N), 20 + seed)
+        A, B = g(a, dev), g(b, dev)
+        C_ref = torch.full((M, N), 3.0, device=dev)
+        C_na = torch.full((M, N), -3.0, device=dev)
+        rc, n = with_workspace(A, B, C_ref)
+        assert rc == mt.MT_OK
+        ref_cfg = mt.last_config()
+        assert 0 < n <= mt.NOALLOC_SCRATCH_BYTES
+        assert noalloc(A, B, C_na) == mt.MT_OK
+        cfg = mt.last_config()
+        print(f"[noalloc] {M}x{N}x{K}: {cfg} (workspace path: {ref_cfg})", flush=True)
+        assert cfg == ref_cfg and cfg.startswith("sk gemv") and "split=1 " not in cfg + " ", cfg
+        torch.cuda.synchronize()
+        got, want = C_na.cpu().numpy(), C_ref.cpu().numpy()
+        assert np.array_equal(got, want), f"{M}x{N}x{K}: differs from mt_gemm_f32"
+        assert_close(got, oracle.matmul(a, b), K, amax(a), amax(b), f"noalloc GEMV {M}x{N}x{K}")
+
+
 def test_plan_without_split_k(dev):
     """Config 1's shape: its plan has no split-K (the wave-split kernel), so the
     buffer is not written, and the result still equals mt_gemm_f32's."""
