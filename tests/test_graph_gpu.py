@@ -145,3 +145,68 @@ def test_graph_conv_replays(dev):
         for name, a, e in zip(("y", "yh", "dx", "dw", "db"), got, outs):
             assert torch.equal(a, e), f"replay {rep}: {name} differs from eager"
         print(f"[graph] conv replay {rep} == eager", flush=True)
+
+
+def test_graph_skinny_and_phased_dx_replays(dev):
+    """The vector-ALU kernels (a split GEMV with its reduction launch, a
+    transposed GEMV, a rank-k product) and a strided convolution's dX by
+    stride phase (dY copy, phase weights, zero fill, one GEMM per phase)
+    captured together; every replay equals the eager calls bit for bit."""
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(8)
+    a = torch.rand(1, 4096, device=dev, generator=gen)
+    B = torch.rand(4096, 2048, device=dev, generator=gen)
+    c = torch.empty(1, 2048, device=dev)
+    ws_g = mt.workspace(mt.lib().mt_gemm_workspace_f32(mt.mat(a), mt.mat(B), mt.mat(c)), dev)
+    At = torch.rand(1000, 512, device=dev, generator=gen)
+    v = torch.rand(512, 3, device=dev, generator=gen)
+    cv = torch.empty(1000, 3, device=dev)
+    ws_t = mt.workspace(mt.lib().mt_gemm_workspace_f32(mt.mat(At), mt.mat(v), mt.mat(cv)), dev)
+    u = torch.rand(2048, 2, device=dev, generator=gen)
+    w2 = torch.rand(2, 1024, device=dev, generator=gen)
+    r = torch.empty(2048, 1024, device=dev)
+    x = torch.randn(4, 32, 28, 28, device=dev, generator=gen)
+    wc = torch.randn(64, 32, 1, 1, device=dev, generator=gen) * 0.1
+    dy = torch.randn(4, 64, 14, 14, device=dev, generator=gen)
+    d = mt.Conv2dDesc(4, 32, 28, 28, 64, 1, 1, 2, 0)
+    dx = torch.empty_like(x)
+
+    with mt.forced_config(mt.FAMILY_DL, 1, 1):   # the phased dX on this small layer
+        ws_c = mt.workspace(mt.lib().mt_conv2d_bwd_workspace_f32(ctypes.byref(d)), dev)
+    cfgs = []
+
+    def step():
+        mt.gemm(a, B, out=c, ws=ws_g)
+        cfgs.append(mt.last_config())
+        mt.gemm(At, v, out=cv, ws=ws_t)
+        cfgs.append(mt.last_config())
+        mt.gemm(u, w2, out=r)
+        cfgs.append(mt.last_config())
+        with mt.forced_config(mt.FAMILY_DL, 1, 1):
+            rc = mt.lib().mt_conv2d_bwd_input_f32(
+                ctypes.byref(d), dy.data_ptr(), wc.data_ptr(), dx.data_ptr(), ws_c.data_ptr(),
+                ws_c.numel(), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+            cfgs.append(mt.last_config())
+        assert rc == mt.MT_OK
+
+    step()
+    torch.cuda.synchronize()
+    print(f"[graph] {cfgs}", flush=True)
+    assert cfgs[0].startswith("sk gemv_mv ") and "split=1 " not in cfgs[0] + " ", cfgs
+    assert cfgs[1].startswith("sk gemv_kv_t ") and cfgs[2].startswith("sk rankk "), cfgs
+    assert "b=im2col " in cfgs[3] + " ", cfgs
+    g = _capture(step)
+    for rep in range(3):
+        a.copy_(torch.rand(1, 4096, device=dev, generator=gen))
+        dy.copy_(torch.randn(4, 64, 14, 14, device=dev, generator=gen))
+        dx.fill_(7.0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = [t.clone() for t in (c, cv, r, dx)]
+        dx.fill_(-7.0)
+        step()
+        torch.cuda.synchronize()
+        for name, x1, e in zip(("gemv", "gemv_t", "rank-k", "dX"), got, (c, cv, r, dx)):
+            assert torch.equal(x1, e), f"replay {rep}: {name} differs from eager"
+        print(f"[graph] skinny + phased dX replay {rep} == eager", flush=True)
