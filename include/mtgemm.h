@@ -250,7 +250,8 @@ enum {
     MT_FAMILY_SKINNY = 4 /* vector-ALU kernels of the HBM-bound shapes:
                             configuration 0 GEMV (at most 8 rows of A against a
                             k- or mn-contiguous B, or at most 8 columns of B
-                            against such an A; `splits` K splits), 1 rank-k
+                            against such an A; `splits` K splits; unforced,
+                            4 against a k-contiguous operand), 1 rank-k
                             (K <= 16, at least 256 columns); no implicit
                             convolution operands, no fused row sums          */
 };

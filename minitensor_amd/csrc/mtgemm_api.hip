@@ -469,6 +469,7 @@ GemmLaunchFn conv_launcher(int cfg, bool nchw) {
 // channel sums: those shapes keep the MFMA kernels.
 enum { SK_NONE = 0, SK_GEMV = 1, SK_RANKK = 2 };
 constexpr int kGemvMinK = 16;
+constexpr int kGemvKvMaxRows = 4;
 constexpr int kRankKMinN = 256;
 constexpr int kGemvMaxSplits = 64;
 constexpr int kGemvWgsPerCu = 4;
@@ -539,8 +540,16 @@ SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int la, i
     if ((!forced || f.cfg == 1) && K <= kRankKMax && N >= kRankKMinN) return rankk_plan(M, N, K, batch);
     if (forced && f.cfg != 0) return none;
     if (K < kGemvMinK) return none;
-    if (M <= kGemvMaxRows && vec_b) return gemv_plan(M, N, K, batch, lb == L_KV, cus, splits);
-    if (N <= kGemvMaxRows && vec_a && !scatter) {
+    // With a k-contiguous B the GEMV kernel reads A's rows from LDS beside
+    // every load of B; past 4 rows that LDS traffic makes it slower than the
+    // MFMA kernels (4096^2: 4 rows 20.7 against 22.8 us, 6 rows 24.4 against
+    // 23.2, 8 rows 26.9 against 23.8), so those shapes keep them (a forced
+    // configuration still reaches the 8-row kernel).
+    const auto rows_ok = [&](int64_t rows, int layout) {
+        return rows <= (layout == L_KV && !forced ? kGemvKvMaxRows : kGemvMaxRows);
+    };
+    if (vec_b && rows_ok(M, lb)) return gemv_plan(M, N, K, batch, lb == L_KV, cus, splits);
+    if (vec_a && rows_ok(N, la) && !scatter) {
         SkinnyPlan s = gemv_plan(N, M, K, batch, la == L_KV, cus, splits);
         s.transpose = true;
         return s;
@@ -555,8 +564,9 @@ size_t skinny_ws(int64_t M, int64_t N, int64_t K, int64_t batch, int cus) {
     const int splits = f.family == MT_FAMILY_SKINNY ? f.splits : 0;
     size_t ws = 0;
     for (bool kv : {false, true}) {
-        if (M <= kGemvMaxRows) ws = std::max(ws, gemv_plan(M, N, K, batch, kv, cus, splits).ws_bytes);
-        if (N <= kGemvMaxRows) ws = std::max(ws, gemv_plan(N, M, K, batch, kv, cus, splits).ws_bytes);
+        const int64_t rows = kv && f.family != MT_FAMILY_SKINNY ? kGemvKvMaxRows : kGemvMaxRows;
+        if (M <= rows) ws = std::max(ws, gemv_plan(M, N, K, batch, kv, cus, splits).ws_bytes);
+        if (N <= rows) ws = std::max(ws, gemv_plan(N, M, K, batch, kv, cus, splits).ws_bytes);
     }
     return ws;
 }

@@ -247,7 +247,8 @@ def _views(a, b, ta, tb, dev):
 
 # Vector-layout operands go to the direct-to-LDS kernel or, for small output
 # tile counts, to the wave-split kernel; the cost model picks.  Shapes with at
-# most 8 rows or columns, or K <= 16, go to the vector-ALU kernels ("sk",
+# most 8 rows or columns (4 against a k-contiguous operand), or K <= 16, go to
+# the vector-ALU kernels ("sk",
 # tests/test_skinny_gpu.py); the direct-to-LDS kernel is then also forced on
 # them (configurations 2 and 5, the plain and the prefetching 64x64 tile),
 # so that its one-row / one-column tails stay covered.  (Every configuration

@@ -45,11 +45,12 @@ def test_gemv_row_major_b(dev, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [
-    (1, 4096, 4096), (1, 1000, 2048), (2, 17, 64), (3, 333, 1028), (8, 4096, 512),
+    (1, 4096, 4096), (1, 1000, 2048), (2, 17, 64), (3, 333, 1028), (4, 4096, 512),
     (6, 1, 12000),
 ])
 def test_gemv_transposed_b(dev, M, N, K):
-    # B = Bt.T: k-contiguous (the Linear layer's x·Wᵀ)
+    # B = Bt.T: k-contiguous (the Linear layer's x·Wᵀ); up to 4 rows (more keep
+    # the MFMA kernels: test_gemv_kv_rows_past_4_keep_mfma)
     a = oracle.uniform((M, K), 300 + M)
     bt = oracle.uniform((N, K), 400 + N)
     c, cfg = gemm(g(a, dev), g(bt, dev).t())
@@ -197,3 +198,20 @@ def test_benchmark_63_rows_keeps_mfma(dev):
     rows = [0, 17, 62]
     want = oracle.matmul_f64_rows(a, b, rows)
     assert_close(c.cpu().numpy()[rows], want, K, 1, 1, "63x4096x4096 sampled rows")
+
+
+def test_gemv_kv_rows_past_4_keep_mfma(dev):
+    # 6 and 8 rows against a k-contiguous B run faster on the MFMA kernels; the
+    # 8-row GEMV kernel is still reached through the forced configuration
+    for M in (6, 8):
+        a = oracle.uniform((M, 1024), 90 + M)
+        bt = oracle.uniform((512, 1024), 91)
+        A, B = g(a, dev), g(bt, dev).t()
+        c, cfg = gemm(A, B)
+        assert not cfg.startswith("sk "), cfg
+        want = oracle.matmul(a, bt.T)
+        assert_close(c.cpu().numpy(), want, 1024, amax(a), amax(bt), f"{M} rows KV auto")
+        with mt.forced_config(mt.FAMILY_SKINNY, 0, 4):
+            c, cfg = gemm(A, B)
+        assert cfg.startswith("sk gemv_kv rows=8 "), cfg
+        assert_close(c.cpu().numpy(), want, 1024, amax(a), amax(bt), f"{M} rows KV forced")
