@@ -206,6 +206,8 @@ struct CostModel {
     double launch_cycles = 17700.0;          // second (reduce) launch
 };
 constexpr int kMaxSplits = 16;
+constexpr int kDlpSmallCfg = 5;          // the 64x64 prefetching configuration
+constexpr double kCoresidentPair = 0.75;
 constexpr int kMaxForcedSplits = 64;
 
 // Tile grid and K split of configuration `cfg` asked for `s` splits (the
@@ -235,7 +237,16 @@ double plan_cycles(const CostModel& cm, const CfgCost& cc, const Plan& pl, int64
     const double work = (double)cc.bm * cc.bn * (double)std::max<int64_t>(pl.kps, kBK) * 2.0 /
                         (256.0 * cc.eff);
     const double epi = (double)cc.bm * cc.bn * 4.0 / cm.epilogue_bytes_per_cycle;
-    double t = per_cu * work + per_cu * epi / cc.occ + rounds * cm.round_latency;
+    // One tile row (M <= 64) on the 4-wave 64x64 prefetching tile, two
+    // workgroups per CU: each SIMD then holds two waves that hide each other's
+    // waits, which the fitted per-workgroup efficiency (mostly from one
+    // workgroup per CU) does not see.  Measured, 63 x 4096 x 4096: split 8
+    // (two per CU) 26.2 us against 29.4 us at split 4; 8-16 rows 24.4 against
+    // 27.2.
+    const double pair = (pl.dl && pl.cfg == kDlpSmallCfg && pl.tiles_m == 1 && per_cu == 2)
+                            ? kCoresidentPair
+                            : 1.0;
+    double t = per_cu * work * pair + per_cu * epi / cc.occ + rounds * cm.round_latency;
     if (pl.splits > 1) {
         const double bytes = (double)(2 * pl.splits + 1) * M * N * batch * 4.0;
         t += bytes / (cm.bytes_per_cycle) + cm.launch_cycles;
