@@ -113,16 +113,24 @@ GemmLaunchFn dl_rowsum_launcher_cfg1();
 GemmLaunchFn dl_rowsum_launcher_cfg2();
 GemmLaunchFn dl_rowsum_launcher_cfg3();
 
-// Wave-split kernel (gemm_ksw_kernel.hpp): tile (32*MB) x (32*NB), W waves
+// Wave-split kernel (gemm_ksw_kernel.hpp): tile (R*MB) x (R*NB) of R x R
+// MFMA blocks (R = 32: gemm_f32_ksw, R = 16: gemm_f32_ksw16), W waves
 // splitting the tile's K range, D chunks in flight per wave.  Any operand
 // layout: VA / VB select 16-byte fragment loads for k-contiguous operands
 // (L_KV) or scalar ones (every other layout).
 template <int CFG> struct KswCfg;
-template <> struct KswCfg<0> { static constexpr int MB = 1, NB = 1, W = 4, D = 6; };
-template <> struct KswCfg<1> { static constexpr int MB = 1, NB = 1, W = 8, D = 4; };
-template <> struct KswCfg<2> { static constexpr int MB = 2, NB = 1, W = 4, D = 4; };
-template <> struct KswCfg<3> { static constexpr int MB = 1, NB = 2, W = 4, D = 4; };
-constexpr int kNumKswCfg = 4;
+template <> struct KswCfg<0> { static constexpr int R = 32, MB = 1, NB = 1, W = 4, D = 6; };
+template <> struct KswCfg<1> { static constexpr int R = 32, MB = 1, NB = 1, W = 8, D = 4; };
+template <> struct KswCfg<2> { static constexpr int R = 32, MB = 2, NB = 1, W = 4, D = 4; };
+template <> struct KswCfg<3> { static constexpr int R = 32, MB = 1, NB = 2, W = 4, D = 4; };
+template <> struct KswCfg<4> { static constexpr int R = 16, MB = 2, NB = 1, W = 4, D = 8; };
+template <> struct KswCfg<5> { static constexpr int R = 16, MB = 1, NB = 2, W = 4, D = 8; };
+template <> struct KswCfg<6> { static constexpr int R = 16, MB = 2, NB = 1, W = 8, D = 4; };
+constexpr int kNumKswCfg = 7;
+template <int CFG> struct KswTile {
+    static constexpr int bm = KswCfg<CFG>::R * KswCfg<CFG>::MB;
+    static constexpr int bn = KswCfg<CFG>::R * KswCfg<CFG>::NB;
+};
 
 // Configuration cfg of the wave-split kernel; va / vb: A / B is L_KV.
 GemmLaunchFn ksw_launcher(int cfg, bool va, bool vb);

@@ -1,5 +1,5 @@
-// gemm_ksw_instances.hip -- instantiates gemm_f32_ksw (the wave-split kernel)
-// for its tile configurations and the 2x2 choices of 16-byte or scalar
+// gemm_ksw_instances.hip -- instantiates the wave-split kernels
+// (gemm_f32_ksw, gemm_f32_ksw16) for their tile configurations and the 2x2 choices of 16-byte or scalar
 // fragment loads for A and B.
 #include "gemm_configs.hpp"
 #include "gemm_ksw_kernel.hpp"
@@ -10,8 +10,12 @@ namespace {
 template <int CFG, bool VA, bool VB>
 hipError_t launch_ksw(const GemmParams& p, unsigned nblocks, hipStream_t s) {
     using C = KswCfg<CFG>;
-    hipLaunchKernelGGL((gemm_f32_ksw<C::MB, C::NB, C::W, VA, VB, C::D>), dim3(nblocks),
-                       dim3(C::W * 64), 0, s, p);
+    if constexpr (C::R == 32)
+        hipLaunchKernelGGL((gemm_f32_ksw<C::MB, C::NB, C::W, VA, VB, C::D>), dim3(nblocks),
+                           dim3(C::W * 64), 0, s, p);
+    else
+        hipLaunchKernelGGL((gemm_f32_ksw16<C::MB, C::NB, C::W, VA, VB, C::D>), dim3(nblocks),
+                           dim3(C::W * 64), 0, s, p);
     return hipGetLastError();
 }
 
@@ -22,16 +26,18 @@ hipError_t launch_ksw(const GemmParams& p, unsigned nblocks, hipStream_t s) {
 }  // namespace
 
 GemmLaunchFn ksw_launcher(int cfg, bool va, bool vb) {
-    static const GemmLaunchFn table[kNumKswCfg][2][2] = {MT_KSW_TABLE(0), MT_KSW_TABLE(1),
-                                                          MT_KSW_TABLE(2), MT_KSW_TABLE(3)};
+    static const GemmLaunchFn table[kNumKswCfg][2][2] = {
+        MT_KSW_TABLE(0), MT_KSW_TABLE(1), MT_KSW_TABLE(2), MT_KSW_TABLE(3),
+        MT_KSW_TABLE(4), MT_KSW_TABLE(5), MT_KSW_TABLE(6)};
     return table[cfg][va][vb];
 }
 
 void ksw_tile(int cfg, int* bm, int* bn) {
-    static const int tiles[kNumKswCfg][2] = {{32 * KswCfg<0>::MB, 32 * KswCfg<0>::NB},
-                                             {32 * KswCfg<1>::MB, 32 * KswCfg<1>::NB},
-                                             {32 * KswCfg<2>::MB, 32 * KswCfg<2>::NB},
-                                             {32 * KswCfg<3>::MB, 32 * KswCfg<3>::NB}};
+    static const int tiles[kNumKswCfg][2] = {
+        {KswTile<0>::bm, KswTile<0>::bn}, {KswTile<1>::bm, KswTile<1>::bn},
+        {KswTile<2>::bm, KswTile<2>::bn}, {KswTile<3>::bm, KswTile<3>::bn},
+        {KswTile<4>::bm, KswTile<4>::bn}, {KswTile<5>::bm, KswTile<5>::bn},
+        {KswTile<6>::bm, KswTile<6>::bn}};
     *bm = tiles[cfg][0];
     *bn = tiles[cfg][1];
 }

@@ -184,12 +184,21 @@ constexpr CfgCost kDlCostImw[kNumDlCfg] = {
 // 6.7 vs 9.4 us, the Linear dX GEMM 14.7 vs 18.4 us, 512^3 6.9 vs 11.2 us.
 // (The model prices the split-K reduction from eager timings, above its cost
 // under graph replay; 0.38 for the 32x32 tile keeps the Linear forward GEMM,
-// 17.1 us with split-K against 18.4 us here, on the split-K plan.)
+// 17.1 us with split-K against 18.4 us here, on the split-K plan.)  The
+// 16x16-block tiles (configurations 4-6, half the work per workgroup) pay
+// where the 32x32 tiles leave CUs idle and the half tiles still fit one
+// round: config 1 (256 x 512 x 512, 256 workgroups) 4.87 us for 16x32
+// against 6.60 for 32x32 on 128, 128 x 512 x 1024 6.47 against 9.53,
+// 256^3 4.17 against 4.51; at 512^3 (512 half tiles, two per CU) 8.3
+// against 6.7, which the per-CU sum of the model reproduces.
 constexpr CfgCost kKswCost[kNumKswCfg] = {
-    {32 * KswCfg<0>::MB, 32 * KswCfg<0>::NB, 0.38, 8},
-    {32 * KswCfg<1>::MB, 32 * KswCfg<1>::NB, 0.37, 4},
-    {32 * KswCfg<2>::MB, 32 * KswCfg<2>::NB, 0.45, 4},
-    {32 * KswCfg<3>::MB, 32 * KswCfg<3>::NB, 0.45, 4}};
+    {KswTile<0>::bm, KswTile<0>::bn, 0.38, 8},
+    {KswTile<1>::bm, KswTile<1>::bn, 0.37, 4},
+    {KswTile<2>::bm, KswTile<2>::bn, 0.45, 4},
+    {KswTile<3>::bm, KswTile<3>::bn, 0.45, 4},
+    {KswTile<4>::bm, KswTile<4>::bn, 0.28, 8},
+    {KswTile<5>::bm, KswTile<5>::bn, 0.325, 8},
+    {KswTile<6>::bm, KswTile<6>::bn, 0.27, 4}};
 
 // Configuration 6 pays off only over long K ranges (short ones, such as the
 // 64-deep batched GEMM of the benchmark, run up to 20 % slower than

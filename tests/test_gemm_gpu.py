@@ -393,8 +393,8 @@ def test_split_k_vector_reduce_bias_beta(dev, axis):
 # ---- maximum sizes: outputs past 2^31 elements (64-bit addressing) ---------------
 
 @pytest.mark.parametrize("path,forced", [("dl", None), ("dl", 4), ("dl", 5), ("rs", None),
-                                         ("ksw", 0)],
-                         ids=["dl", "dl4", "dl5", "rs", "ksw0"])
+                                         ("ksw", 0), ("ksw", 4)],
+                         ids=["dl", "dl4", "dl5", "rs", "ksw0", "ksw4"])
 def test_output_beyond_2pow31_elements(dev, path, forced):
     # C[40000, 60000] = 2.4e9 elements (9.6 GB): rows past 35791 start beyond
     # 2^31, so any 32-bit element index in a kernel or epilogue would alias.

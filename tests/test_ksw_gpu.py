@@ -1,5 +1,6 @@
-"""The wave-split kernel (K split across the waves of one workgroup) against
-the CPU oracle, every configuration forced through mt_gemm_force_config.
+"""The wave-split kernels (K split across the waves of one workgroup, on
+32x32 or 16x16 MFMA blocks) against the CPU oracle, every configuration
+forced through mt_gemm_force_config.
 
 It takes every operand layout (16-byte fragment loads for k-contiguous
 operands, scalar loads for the rest), K ranges with a partial last chunk,
@@ -19,7 +20,7 @@ from util_parity import amax, assert_close
 
 pytestmark = pytest.mark.gpu
 
-KSW = list(range(4))
+KSW = list(range(7))   # 0-3: 32x32 MFMA blocks, 4-6: 16x16 blocks
 
 
 def g(a, dev):
