@@ -493,6 +493,12 @@ constexpr int kGemvKvMaxRows = 4;
 constexpr int kRankKMinN = 256;
 constexpr int kGemvMaxSplits = 64;
 constexpr int kGemvWgsPerCu = 4;
+// An mn-contiguous B of more than 64 MiB: about six workgroups per CU with
+// shorter splits (down to 32 k), up to 128 splits.  Graph-timed: 1 x 4096 x
+// 8192 24.7 against 28.0 us, 1 x 8192 x 4096 24.7 against 26.4; at 64 MiB
+// and below four per CU stay faster (1 x 4096 x 4096 14.9 against 16.1).
+constexpr int64_t kGemvLargeBytes = int64_t(64) << 20;
+constexpr int kGemvWgsPerCuLarge = 6, kGemvMaxSplitsLarge = 128, kGemvMinKpsLarge = 32;
 
 struct SkinnyPlan {
     int kind = SK_NONE;
@@ -509,8 +515,9 @@ struct SkinnyPlan {
 // split count aims at kGemvWgsPerCu workgroups per CU (every workgroup
 // resident at once: the kernels are bound by the loads in flight), with at
 // least 64 k per split (mn-contiguous B) or four 64-deep steps per lane
-// (k-contiguous B), at most kGemvMaxSplits; forced_splits > 0 asks for that
-// many.
+// (k-contiguous B), at most kGemvMaxSplits (the ...Large figures for an
+// mn-contiguous B of more than kGemvLargeBytes); forced_splits > 0 asks for
+// that many.
 SkinnyPlan gemv_plan(int64_t m, int64_t n, int64_t k, int64_t batch, bool kv, int cus,
                      int forced_splits) {
     SkinnyPlan s;
@@ -519,12 +526,16 @@ SkinnyPlan gemv_plan(int64_t m, int64_t n, int64_t k, int64_t batch, bool kv, in
     s.rows = m <= 1 ? 1 : m <= 2 ? 2 : m <= 4 ? 4 : 8;
     const int64_t cols = kv ? kGemvKvCols : kGemvMvCols;
     s.tiles_n = (int)((n + cols - 1) / cols);
-    const int64_t gran = kv ? 64 : 4, min_kps = kv ? 256 : 64;
+    const bool large = !kv && k * n * batch * (int64_t)sizeof(float) > kGemvLargeBytes;
+    const int64_t gran = kv ? 64 : 4;
+    const int64_t min_kps = kv ? 256 : large ? kGemvMinKpsLarge : 64;
+    const int64_t per_cu = large ? kGemvWgsPerCuLarge : kGemvWgsPerCu;
+    const int64_t max_splits = large ? kGemvMaxSplitsLarge : kGemvMaxSplits;
     int64_t want = forced_splits;
     if (want <= 0) {
         const int64_t base = (int64_t)s.tiles_n * batch;
-        want = std::max<int64_t>(1, (kGemvWgsPerCu * (int64_t)cus + base - 1) / base);
-        want = std::min<int64_t>({want, std::max<int64_t>(1, k / min_kps), kGemvMaxSplits});
+        want = std::max<int64_t>(1, (per_cu * (int64_t)cus + base - 1) / base);
+        want = std::min<int64_t>({want, std::max<int64_t>(1, k / min_kps), max_splits});
     }
     int64_t kps = (k + want - 1) / want;
     kps = (kps + gran - 1) / gran * gran;

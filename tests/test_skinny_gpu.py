@@ -44,6 +44,17 @@ def test_gemv_row_major_b(dev, M, N, K):
     assert_close(c.cpu().numpy(), oracle.matmul(a, b), K, amax(a), amax(b), f"{M}x{N}x{K} MV")
 
 
+def test_gemv_large_b_takes_more_splits(dev):
+    # B of 128 MiB (mn-contiguous): more, shorter splits than the 64 MiB rule
+    M, N, K = 2, 4100, 8192
+    a = oracle.uniform((M, K), 81)
+    b = oracle.uniform((K, N), 82)
+    c, cfg = gemm(g(a, dev), g(b, dev))
+    assert cfg.startswith("sk gemv_mv "), cfg
+    assert int(cfg.split("split=")[1].split()[0]) > 64, cfg
+    assert_close(c.cpu().numpy(), oracle.matmul(a, b), K, amax(a), amax(b), "large-B GEMV")
+
+
 @pytest.mark.parametrize("M,N,K", [
     (1, 4096, 4096), (1, 1000, 2048), (2, 17, 64), (3, 333, 1028), (4, 4096, 512),
     (6, 1, 12000),
