@@ -247,8 +247,9 @@ enum {
     MT_FAMILY_DL = 2,    /* direct-to-LDS kernel: k- or mn-contiguous operands  */
     MT_FAMILY_KSW = 3,   /* wave-split kernel: small tiles, K split across the
                             waves of a workgroup; any operand layout;
-                            configurations 0-3 on 32x32 MFMA blocks, 4-6 on
-                            16x16 blocks (32x16, 16x32, 32x16 with 8 waves)  */
+                            configurations 0-3 on 32x32 MFMA blocks, 4-8 on
+                            16x16 blocks (32x16, 16x32, 32x16 with 8 waves,
+                            64x32, 32x64)                                    */
     MT_FAMILY_SKINNY = 4 /* vector-ALU kernels of the HBM-bound shapes:
                             configuration 0 GEMV (at most 8 rows of A against a
                             k- or mn-contiguous B, or at most 8 columns of B

@@ -126,7 +126,11 @@ template <> struct KswCfg<3> { static constexpr int R = 32, MB = 1, NB = 2, W = 
 template <> struct KswCfg<4> { static constexpr int R = 16, MB = 2, NB = 1, W = 4, D = 8; };
 template <> struct KswCfg<5> { static constexpr int R = 16, MB = 1, NB = 2, W = 4, D = 8; };
 template <> struct KswCfg<6> { static constexpr int R = 16, MB = 2, NB = 1, W = 8, D = 4; };
-constexpr int kNumKswCfg = 7;
+// 7, 8: the 64x32 and 32x64 tiles again on 16x16 blocks (eight accumulator
+// chains per wave where configurations 2 and 3 have two).
+template <> struct KswCfg<7> { static constexpr int R = 16, MB = 4, NB = 2, W = 4, D = 4; };
+template <> struct KswCfg<8> { static constexpr int R = 16, MB = 2, NB = 4, W = 4, D = 4; };
+constexpr int kNumKswCfg = 9;
 template <int CFG> struct KswTile {
     static constexpr int bm = KswCfg<CFG>::R * KswCfg<CFG>::MB;
     static constexpr int bn = KswCfg<CFG>::R * KswCfg<CFG>::NB;

@@ -28,7 +28,7 @@ hipError_t launch_ksw(const GemmParams& p, unsigned nblocks, hipStream_t s) {
 GemmLaunchFn ksw_launcher(int cfg, bool va, bool vb) {
     static const GemmLaunchFn table[kNumKswCfg][2][2] = {
         MT_KSW_TABLE(0), MT_KSW_TABLE(1), MT_KSW_TABLE(2), MT_KSW_TABLE(3),
-        MT_KSW_TABLE(4), MT_KSW_TABLE(5), MT_KSW_TABLE(6)};
+        MT_KSW_TABLE(4), MT_KSW_TABLE(5), MT_KSW_TABLE(6), MT_KSW_TABLE(7), MT_KSW_TABLE(8)};
     return table[cfg][va][vb];
 }
 
@@ -37,7 +37,8 @@ void ksw_tile(int cfg, int* bm, int* bn) {
         {KswTile<0>::bm, KswTile<0>::bn}, {KswTile<1>::bm, KswTile<1>::bn},
         {KswTile<2>::bm, KswTile<2>::bn}, {KswTile<3>::bm, KswTile<3>::bn},
         {KswTile<4>::bm, KswTile<4>::bn}, {KswTile<5>::bm, KswTile<5>::bn},
-        {KswTile<6>::bm, KswTile<6>::bn}};
+        {KswTile<6>::bm, KswTile<6>::bn}, {KswTile<7>::bm, KswTile<7>::bn},
+        {KswTile<8>::bm, KswTile<8>::bn}};
     *bm = tiles[cfg][0];
     *bn = tiles[cfg][1];
 }

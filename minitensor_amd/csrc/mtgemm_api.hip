@@ -190,7 +190,13 @@ constexpr CfgCost kDlCostImw[kNumDlCfg] = {
 // round: config 1 (256 x 512 x 512, 256 workgroups) 4.87 us for 16x32
 // against 6.60 for 32x32 on 128, 128 x 512 x 1024 6.47 against 9.53,
 // 256^3 4.17 against 4.51; at 512^3 (512 half tiles, two per CU) 8.3
-// against 6.7, which the per-CU sum of the model reproduces.
+// against 6.7, which the per-CU sum of the model reproduces.  The 64x32 and
+// 32x64 tiles on 16x16 blocks (configurations 7, 8: eight accumulator
+// chains per wave where configurations 2, 3 have two): the Linear dX GEMM
+// 13.2-13.6 us against 14.2, 512 x 1024 x 1024 13.6 against 15.6.  (A 32x32
+// tile of 16x16 blocks, four chains, gained 3-10 % over configuration 0 on
+// some shapes but lost on the Linear forward GEMM, 18.8 against 18.4, where
+// the model then preferred it to the 16.2 us split-K plan: left out.)
 constexpr CfgCost kKswCost[kNumKswCfg] = {
     {KswTile<0>::bm, KswTile<0>::bn, 0.38, 8},
     {KswTile<1>::bm, KswTile<1>::bn, 0.37, 4},
@@ -198,7 +204,9 @@ constexpr CfgCost kKswCost[kNumKswCfg] = {
     {KswTile<3>::bm, KswTile<3>::bn, 0.45, 4},
     {KswTile<4>::bm, KswTile<4>::bn, 0.28, 8},
     {KswTile<5>::bm, KswTile<5>::bn, 0.325, 8},
-    {KswTile<6>::bm, KswTile<6>::bn, 0.27, 4}};
+    {KswTile<6>::bm, KswTile<6>::bn, 0.27, 4},
+    {KswTile<7>::bm, KswTile<7>::bn, 0.47, 4},
+    {KswTile<8>::bm, KswTile<8>::bn, 0.49, 4}};
 
 // Configuration 6 pays off only over long K ranges (short ones, such as the
 // 64-deep batched GEMM of the benchmark, run up to 20 % slower than

@@ -20,7 +20,7 @@ from util_parity import amax, assert_close
 
 pytestmark = pytest.mark.gpu
 
-KSW = list(range(7))   # 0-3: 32x32 MFMA blocks, 4-6: 16x16 blocks
+KSW = list(range(9))   # 0-3: 32x32 MFMA blocks, 4-8: 16x16 blocks
 
 
 def g(a, dev):
