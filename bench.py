@@ -71,6 +71,10 @@ def parse():
                    help="length of the sustained back-to-back window of the headline GEMM")
     p.add_argument("--copy-probe", action="store_true",
                    help="also run a 256 MiB device copy (rocprof counter calibration)")
+    p.add_argument("--audit", default="",
+                   help="SEED:COUNT: instead of the benchmark, time the planner's pick against "
+                        "every forced tile configuration and split on COUNT random row-major "
+                        "shapes (sizes 64-4700, seeded) and print one line per shape and a summary")
     p.add_argument("--only", default="",
                    help="comma list of secondary configs (c1,c3,c4,c5a,c5b,skinny) and/or "
                         "'sustained' (the headline GEMM back to back for 2.5 s): run just those "
@@ -582,6 +586,64 @@ def copy_probe(dev) -> None:
     torch.cuda.synchronize()
 
 
+def planner_audit(dev, seed: int, count: int) -> None:
+    """The cost model's pick against the best forced plan (direct-to-LDS
+    configurations at splits 1-16, wave-split configurations unsplit) on
+    random row-major GEMMs: how far the planner is from the fastest kernel
+    this library has for each shape."""
+    import numpy as np
+    import torch
+    import minitensor_amd as mt
+
+    rng = np.random.default_rng(seed)
+    ws = mt.workspace(1 << 28, dev)
+
+    def med(per):
+        per = sorted(per)
+        return per[len(per) // 2] * 1e3
+
+    def dim():
+        return int(2 ** rng.uniform(6, 12.2)) // 4 * 4
+
+    cands = ([(mt.FAMILY_DL, c, s) for c in range(mt.config_count(mt.FAMILY_DL))
+              for s in (1, 2, 3, 4, 6, 8, 12, 16)] +
+             [(mt.FAMILY_KSW, c, 1) for c in range(mt.config_count(mt.FAMILY_KSW))])
+    ratios = []
+    for _ in range(count):
+        M, N, K = dim(), dim(), dim()
+        if M * N * K > 2 ** 33:
+            K = max(64, 2 ** 33 // (M * N)) // 4 * 4
+        A = torch.rand(M, K, device=dev) - 0.5
+        B = torch.rand(K, N, device=dev) - 0.5
+        C = torch.empty(M, N, device=dev)
+        fn = lambda: mt.gemm(A, B, out=C, ws=ws)
+        fn()
+        torch.cuda.synchronize()
+        auto_t, auto_c = med(time_graph(fn)), mt.last_config()
+        best_t, best_c = auto_t, auto_c
+        for fam, c, s in cands:
+            with mt.forced_config(fam, c, s):
+                try:
+                    fn()
+                    torch.cuda.synchronize()
+                except RuntimeError:
+                    continue
+                name = mt.last_config()
+                if not name.endswith(f"cfg={c}"):
+                    continue   # the family cannot take these operands
+                t = med(time_graph(fn, calls=20, replays=5, preroll_ms=5))
+                if t < best_t:
+                    best_t, best_c = t, name
+        ratios.append(auto_t / best_t)
+        print(f"{M}x{N}x{K}: auto {auto_t:.2f} us [{auto_c}], best {best_t:.2f} us [{best_c}], "
+              f"ratio {auto_t / best_t:.3f}", flush=True)
+    r = np.array(ratios)
+    print(json.dumps({"shapes": count, "seed": seed, "within_5pct": int((r <= 1.05).sum()),
+                      "within_10pct": int((r <= 1.10).sum()),
+                      "geomean_ratio": round(float(np.exp(np.log(r).mean())), 4),
+                      "worst_ratio": round(float(r.max()), 3)}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -607,6 +669,10 @@ def main():
         ws = mt.workspace(mt.lib().mt_gemm_workspace_f32(mt.mat(A), mt.mat(B), mt.mat(C)), dev)
         return lambda: mt.gemm(A, B, out=C, ws=ws)
 
+    if args.audit:
+        seed, count = (int(x) for x in args.audit.split(":"))
+        planner_audit(dev, seed, count)
+        return
     if args.only:
         names = tuple(x.strip() for x in args.only.split(",") if x.strip())
         unknown = [x for x in names if x not in SECONDARY + ("sustained",)]

@@ -224,7 +224,10 @@ struct CostModel {
 };
 constexpr int kMaxSplits = 16;
 constexpr int kDlpSmallCfg = 5;          // the 64x64 prefetching configuration
+constexpr int kDlSmallCfg = 2;           // the 64x64 direct-to-LDS configuration
 constexpr double kCoresidentPair = 0.75;
+constexpr int kAloneMinK = 1024;
+constexpr double kAlonePenalty = 1.3;
 constexpr int kMaxForcedSplits = 64;
 
 // Tile grid and K split of configuration `cfg` asked for `s` splits (the
@@ -263,7 +266,16 @@ double plan_cycles(const CostModel& cm, const CfgCost& cc, const Plan& pl, int64
     const double pair = (pl.dl && pl.cfg == kDlpSmallCfg && pl.tiles_m == 1 && per_cu == 2)
                             ? kCoresidentPair
                             : 1.0;
-    double t = per_cu * work * pair + per_cu * epi / cc.occ + rounds * cm.round_latency;
+    // A 64x64 tile alone on its CU over a long K range (one wave per SIMD,
+    // one accumulator chain per wave): slower than its fitted efficiency,
+    // which comes from CUs holding several.  Measured on random shapes
+    // (bench.py --audit): 1456 x 532 x 2500 at split 1 (207 workgroups) 64.6 us
+    // against 48.0 at split 6; the factor moves such shapes to split-K.
+    const double alone = (pl.dl && (pl.cfg == kDlSmallCfg || pl.cfg == kDlpSmallCfg) &&
+                          per_cu == 1 && pl.kps >= kAloneMinK)
+                             ? kAlonePenalty
+                             : 1.0;
+    double t = per_cu * work * pair * alone + per_cu * epi / cc.occ + rounds * cm.round_latency;
     if (pl.splits > 1) {
         const double bytes = (double)(2 * pl.splits + 1) * M * N * batch * 4.0;
         t += bytes / (cm.bytes_per_cycle) + cm.launch_cycles;
