@@ -2328,11 +2328,26 @@ int mt_axpby_f32(const mt_mat_f32* X, float alpha, const mt_mat_f32* Y, float be
     if ((Y->rows > 1 && Y->row_stride == 0) || (Y->cols > 1 && Y->col_stride == 0) ||
         (Y->batch > 1 && Y->batch_stride == 0))
         return MT_ERR_INVALID;
+    float* const y = const_cast<float*>(Y->base) + Y->offset;
+    // A plain copy of a transposed view (X's rows adjacent, its columns
+    // strided) into dense rows: the LDS-tiled layout change, whose reads run
+    // down X's columns and writes along Y's rows, where the element-wise form
+    // reads one column element per lane (a 2048 x 1024 Bᵀ: 15.7 -> 8.6 us).
+    // alpha = 1 and beta = 0 make it an exact copy, as that form's.
+    if (alpha == 1.f && beta == 0.f && X->row_stride == 1 && X->col_stride > 1 &&
+        Y->col_stride == 1 && Y->row_stride == Y->cols &&
+        (Y->batch == 1 || Y->batch_stride == Y->rows * Y->cols) && Y->rows >= 32 &&
+        Y->cols >= 32 && Y->rows < kMaxDim && Y->cols < kMaxDim && Y->batch < kMaxDim) {
+        const TJob j = tjob(X->base + X->offset, X->batch == 1 ? 0 : X->batch_stride,
+                            X->col_stride, Y->rows, 1, Y->rows, Y->cols, Y->rows, Y->batch, y);
+        return launch_transposes(j, TJob{}, static_cast<hipStream_t>(stream)) == hipSuccess
+                   ? MT_OK
+                   : MT_ERR_HIP;
+    }
     const hipError_t e =
         launch_axpby(X->base + X->offset, X->batch == 1 ? 0 : X->batch_stride, X->row_stride,
-                     X->col_stride, alpha, const_cast<float*>(Y->base) + Y->offset,
-                     Y->batch_stride, Y->row_stride, Y->col_stride, beta, Y->batch, Y->rows,
-                     Y->cols, static_cast<hipStream_t>(stream));
+                     X->col_stride, alpha, y, Y->batch_stride, Y->row_stride, Y->col_stride, beta,
+                     Y->batch, Y->rows, Y->cols, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? MT_OK : MT_ERR_HIP;
 }
 

@@ -36,3 +36,28 @@ def test_axpby_views(dev, kind):
     mt.axpby(x, y, -2.0, 0.0)             # plain scaled copy: beta = 0 ignores y
     torch.cuda.synchronize()
     np.testing.assert_array_equal(y.cpu().numpy(), (-2.0 * x).expand_as(y).cpu().numpy())
+
+
+@pytest.mark.parametrize("rows,cols,batch,off,bcast", [
+    (1024, 2048, 1, 0, False),   # C3's Bᵀ materialised: the tiled 16-byte path
+    (67, 45, 1, 0, False),       # ragged extents: the tiled scalar path
+    (33, 130, 3, 0, False),      # batched
+    (40, 36, 4, 0, True),        # one matrix broadcast over the batch
+    (96, 64, 1, 1, False),       # storage offset by one float: unaligned reads
+    (31, 200, 1, 0, False),      # rows < 32: the element-wise kernel
+])
+def test_axpby_transposed_copy_is_exact(dev, rows, cols, batch, off, bcast):
+    # y = x for x a transposed view (adjacent rows, strided columns) and y dense:
+    # a layout change through LDS tiles, bit for bit the copy
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(rows * 7 + cols)
+    nb = 1 if bcast else batch
+    store = torch.rand(nb * cols * rows + off, device=dev, generator=gen)
+    x = store[off:].view(nb, cols, rows).transpose(1, 2)          # [nb][rows][cols], row stride 1
+    if bcast:
+        x = x.expand(batch, rows, cols)
+    x = x if batch > 1 else x[0]
+    y = torch.full((batch, rows, cols) if batch > 1 else (rows, cols), 7.0, device=dev)
+    mt.axpby(x[:1] if bcast else x, y, 1.0, 0.0)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(y.cpu().numpy(), x.contiguous().cpu().numpy())
