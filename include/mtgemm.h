@@ -244,7 +244,11 @@ const char* mt_last_config(void);
 enum {
     MT_FAMILY_AUTO = 0,  /* the cost model chooses (default)                   */
     MT_FAMILY_RS = 1,    /* register-staged kernel: any operand layout          */
-    MT_FAMILY_DL = 2,    /* direct-to-LDS kernel: k- or mn-contiguous operands  */
+    MT_FAMILY_DL = 2,    /* direct-to-LDS kernel: k- or mn-contiguous operands;
+                            configurations 0-3 gemm_f32_dl, 4-6 with fragment
+                            prefetch (not the channels-last convolution
+                            operand), 7 the channels-last convolution operand
+                            only (64x112 tiles of 16x16 MFMA blocks)          */
     MT_FAMILY_KSW = 3,   /* wave-split kernel: small tiles, K split across the
                             waves of a workgroup; any operand layout;
                             configurations 0-3 on 32x32 MFMA blocks, 4-8 on

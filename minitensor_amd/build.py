@@ -45,6 +45,7 @@ def _units():
         units.append((CSRC / "gemm_dl_instances.hip", OBJDIR / f"gemm_dl_cfg{cfg}.o",
                       [f"-DMT_CFG={cfg}"]))
     units.append((CSRC / "gemm_dlp_instances.hip", OBJDIR / "gemm_dlp.o", []))
+    units.append((CSRC / "gemm_dl16_instances.hip", OBJDIR / "gemm_dl16.o", []))
     units.append((CSRC / "gemm_ksw_instances.hip", OBJDIR / "gemm_ksw.o", []))
     units.append((CSRC / "gemm_skinny_instances.hip", OBJDIR / "gemm_skinny.o", []))
     units.append((CSRC / "mtgemm_api.hip", OBJDIR / "mtgemm_api.o", []))

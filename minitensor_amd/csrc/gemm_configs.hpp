@@ -57,9 +57,23 @@ template <> struct DlCfg<4> { static constexpr int BM = 256, BN = 256, WM = 128,
 template <> struct DlCfg<5> { static constexpr int BM = 64, BN = 64, WM = 32, WN = 32, STAGES = 2, WPE = 8; };
 template <> struct DlCfg<6> { static constexpr int BM = 128, BN = 128, WM = 64, WN = 32, STAGES = 2, WPE = 2; };
 
-constexpr int kNumDlCfg = 7;
-constexpr int kDlpFirstCfg = 4;   // configurations kDlpFirstCfg.. are gemm_f32_dlp
-constexpr bool is_dlp_cfg(int cfg) { return cfg >= kDlpFirstCfg; }
+// Configuration 7 is the convolution kernel on 16x16 MFMA blocks
+// gemm_f32_dl16 (gemm_dl16_kernel.hpp), B = L_IM only: block tile BM x BN,
+// wave tile WM x WN, KG groups of waves splitting the tile's K-chunks, a
+// STAGES-slot ring per group, PRE of a chunk's four MFMA k-steps issued
+// before each barrier.  112 = 7 blocks of 16 divides the pixel count of
+// ResNet layers (multiples of 7*7*16 at even batch sizes).  8 waves: two
+// groups of four 16x112 waves, two waves per SIMD; 72 KB of LDS, two
+// workgroups per CU.
+template <int CFG> struct Dl16Cfg;
+template <> struct Dl16Cfg<0> { static constexpr int BM = 64, BN = 112, WM = 16, WN = 112, KG = 2, STAGES = 3, PRE = 2; };
+constexpr int kNumDl16Cfg = 1;
+
+constexpr int kDlpFirstCfg = 4;    // configurations kDlpFirstCfg.. are gemm_f32_dlp
+constexpr int kDl16FirstCfg = 7;   // configurations kDl16FirstCfg.. are gemm_f32_dl16
+constexpr int kNumDlCfg = kDl16FirstCfg + kNumDl16Cfg;
+constexpr bool is_dlp_cfg(int cfg) { return cfg >= kDlpFirstCfg && cfg < kDl16FirstCfg; }
+constexpr bool is_dl16_cfg(int cfg) { return cfg >= kDl16FirstCfg; }
 
 template <int CFG>
 constexpr int dl_threads() {
@@ -81,6 +95,8 @@ GemmLaunchFn dlp_convw_launcher(int cfg, bool tail);
 // Configurations 4-6 for the weight gradient with A = dY in NCHW (L_KVI).
 GemmLaunchFn dlp_convwi_launcher(int cfg);
 // Implicit-im2col convolution: A = weights (L_KV), B = L_IM (GemmParams::cv).
+GemmLaunchFn dl16_conv_launcher(int cfg16);   // gemm_f32_dl16, Dl16Cfg<cfg16>
+void dl16_tile(int cfg16, int* bm, int* bn);
 GemmLaunchFn dl_conv_launcher_cfg0();
 GemmLaunchFn dl_conv_launcher_cfg1();
 GemmLaunchFn dl_conv_launcher_cfg2();

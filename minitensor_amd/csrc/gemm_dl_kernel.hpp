@@ -49,11 +49,21 @@ struct DlTile {
 };
 
 // Position (in 16-B groups) of k-group g of row r inside a k-contiguous tile
-// is g ^ kswz(r).  gfx950's LDS has 64 banks of 4 B and serves a
-// ds_read_b128 16 lanes (256 B) at a time; a fragment read has those lanes on
-// 16 consecutive rows at the same k-group.  Row r starts at bank 16*(r%4), so
-// XOR-ing the group with (r/4)%4 makes the 16 rows cover all 64 banks once.
+// is g ^ kswz(r).  The 32x32-block fragment read (lane l: row l%32, k-group
+// 2*(l/32) or 2*(l/32)+1) then takes 4 LDS cycles per ds_read_b128 on gfx950,
+// the conflict-free rate (64 lanes x 16 B at 256 B per cycle); without the
+// swizzle it takes 8.
 __device__ __forceinline__ int kswz(int r) { return (r >> 2) & 3; }
+// The 16x16-block fragment read of gemm_f32_dl16 (lane l: row l%16 of a
+// block, k-group l/16: the four 16-lane groups read the four k-groups of the
+// same 16 rows) takes 8 cycles with kswz and 4 with kswz16.  Measured with
+// SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE on read patterns in isolation;
+// no plain bank model (lanes served in fixed groups of 8 or 16, 32 or 64
+// banks) reproduces both results, so the swizzles are chosen by measurement.
+// SW selects kswz16 in the loaders.
+__device__ __forceinline__ int kswz16(int r) { return (r >> 1) & 3; }
+template <int SW>
+__device__ __forceinline__ int kswz_sel(int r) { return SW == 0 ? kswz(r) : kswz16(r); }
 
 // Zero source for lanes whose 16 bytes fall in the padding, beyond N, or past
 // the end of the K range: the DMA writes every lane, so those lanes read 16
@@ -71,7 +81,7 @@ __device__ __forceinline__ int div_by(int n, int d, double rd) {
     return q;
 }
 
-template <int L, int BMN, int NW>
+template <int L, int BMN, int NW, int SW = 0>
 struct DlLoader {
     using T = DlTile<L, BMN, NW>;
     const float* src[T::per_wave];   // this lane's source for each instruction, chunk 0
@@ -89,7 +99,7 @@ struct DlLoader {
             if constexpr (T::kc) {
                 // 16 rows x 4 groups of 4 k per instruction; lane -> (row, slot).
                 const int r = q * 16 + (lane >> 2);
-                const int g = (lane & 3) ^ kswz(r);       // k-group that lands in slot lane&3
+                const int g = (lane & 3) ^ kswz_sel<SW>(r);   // k-group that lands in slot lane&3
                 const int64_t row = min((int64_t)mn0 + r, (int64_t)MN - 1);
                 src[j] = X + row * s_mn + (int64_t)(k0 + g * 4) * s_k;
                 kofs[j] = g * 4;
@@ -222,8 +232,11 @@ struct DlTail {
 // the tap falls in the padding or n >= N.  The tap and channel offset are the
 // same for every lane (scalar registers, the wave index is uniform) and step
 // through (rt, st, ci0) once per chunk; per lane only the bounds test and one
-// address add remain.  Chunks must be issued in order 0, 1, 2, ...
-template <int BMN, int NW>
+// address add remain.  Chunks must be issued in order 0, 1, 2, ... (STEP > 1:
+// each issue advances STEP chunks, for a loader that takes every STEP-th
+// chunk).  Rows at or past VR (a tile padded to whole DMA instructions) read
+// zeros.
+template <int BMN, int NW, int VR = BMN, int STEP = 1, int SW = 0>
 struct DlImLoader {
     using T = DlTile<L_IM, BMN, NW>;
     const float* pix[T::per_wave];   // xt + img*img_stride + (ih0*w + iw0)*c + 4g
@@ -239,11 +252,11 @@ struct DlImLoader {
 #pragma unroll
         for (int j = 0; j < T::per_wave; ++j) {
             const int r = (j * NW + wave) * 16 + (lane >> 2);
-            const int grp = (lane & 3) ^ kswz(r);
+            const int grp = (lane & 3) ^ kswz_sel<SW>(r);
             const int n = n0 + r;
             const int img = n / hw, rem = n - img * hw;
             const int oh = rem / g.wo, ow = rem - oh * g.wo;
-            ih0[j] = n < p.N ? oh * g.stride - g.pad : -(1 << 30);   // past N: zeros
+            ih0[j] = n < p.N && r < VR ? oh * g.stride - g.pad : -(1 << 30);   // past N: zeros
             iw0[j] = ow * g.stride - g.pad_w;
             pix[j] = X + (int64_t)img * g.img_stride +
                      ((int64_t)ih0[j] * g.w + iw0[j]) * g.c + grp * 4;
@@ -266,10 +279,13 @@ struct DlImLoader {
                 (const void __attribute__((address_space(1)))*)src,
                 (void __attribute__((address_space(3)))*)(tile + q * 256), 16, 0, 0);
         }
-        ci0 += 16;                   // next chunk
-        if (ci0 == c) {
-            ci0 = 0;
-            if (++st == kw) { st = 0; ++rt; }
+#pragma unroll
+        for (int a = 0; a < STEP; ++a) {   // next chunk (c % 16 == 0)
+            ci0 += 16;
+            if (ci0 == c) {
+                ci0 = 0;
+                if (++st == kw) { st = 0; ++rt; }
+            }
         }
     }
 };

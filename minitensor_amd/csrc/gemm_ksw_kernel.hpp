@@ -89,11 +89,12 @@ constexpr int ksw_lds_floats() {
 
 // The end of both wave-split kernels: the W partial BM x BN tiles in LDS
 // (rows of BN + 4 floats) are summed in wave order and stored through the
-// shared epilogue (bias and beta*C, or a split-K partial).
-template <int BM, int BN, int W>
+// shared epilogue (bias and beta*C, or a split-K partial) by the NT threads
+// of the workgroup.
+template <int BM, int BN, int W, int NT = 64 * W>
 __device__ __forceinline__ void ksw_store(const GemmParams& p, const TileId& id,
                                           const float* red, int m0, int n0) {
-    constexpr int PITCH = BN + 4, NT = 64 * W;
+    constexpr int PITCH = BN + 4;
     const bool part = p.splits > 1;
     float* const base = part ? p.ws + ((int64_t)id.split * p.batch + id.bz) * (int64_t)p.M * p.N
                              : p.C + (int64_t)id.bz * p.c_b;

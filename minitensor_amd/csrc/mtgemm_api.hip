@@ -150,6 +150,12 @@ constexpr CfgCost kRsCost[kNumCfg] = {      // register-staged kernel, any layou
     {TileCfg<0>::BM, TileCfg<0>::BN, 0.86, 1},
     {TileCfg<1>::BM, TileCfg<1>::BN, 0.75, 2},
     {TileCfg<2>::BM, TileCfg<2>::BN, 0.57, 4}};
+// Configuration 7 (the convolution kernel on 16x16 blocks, 64x112 tiles,
+// channels-last operand only): 0.78 with two workgroups per CU, from graph
+// timings of ResNet-like layers at batch 32 against the plans of
+// configurations 0-3 (28x28x128 3x3: 88.9 against 96.3 us, 56x56x64:
+// 94.2 against 97.0, 14x14 1x1 256 -> 1024: 55.7 against 57.9); never
+// offered where its workgroups would run one per CU (make_plan_uncached).
 constexpr CfgCost kDlCost[kNumDlCfg] = {    // direct-to-LDS kernel, vector layouts
     {DlCfg<0>::BM, DlCfg<0>::BN, 0.90, 1},
     {DlCfg<1>::BM, DlCfg<1>::BN, 0.86, 4},
@@ -157,7 +163,8 @@ constexpr CfgCost kDlCost[kNumDlCfg] = {    // direct-to-LDS kernel, vector layo
     {DlCfg<3>::BM, DlCfg<3>::BN, 0.87, 3},
     {DlCfg<4>::BM, DlCfg<4>::BN, 0.98, 1},
     {DlCfg<5>::BM, DlCfg<5>::BN, 0.72, 8},
-    {DlCfg<6>::BM, DlCfg<6>::BN, 0.90, 3}};
+    {DlCfg<6>::BM, DlCfg<6>::BN, 0.90, 3},
+    {Dl16Cfg<0>::BM, Dl16Cfg<0>::BN, 0.78, 2}};
 // The same kernels with the convolution weight gradient's gathered B operand
 // (L_IMW): its 16-byte gathers cost per chunk whatever the tile's height, so
 // the 256-row tile of configuration 3 amortises them over twice the MFMA work
@@ -174,7 +181,8 @@ constexpr CfgCost kDlCostImw[kNumDlCfg] = {
     {DlCfg<3>::BM, DlCfg<3>::BN, 0.93, 3},
     {DlCfg<4>::BM, DlCfg<4>::BN, 0.98, 1},
     {DlCfg<5>::BM, DlCfg<5>::BN, 0.72, 8},
-    {DlCfg<6>::BM, DlCfg<6>::BN, 0.86, 3}};
+    {DlCfg<6>::BM, DlCfg<6>::BN, 0.86, 3},
+    {Dl16Cfg<0>::BM, Dl16Cfg<0>::BN, 0.78, 2}};   // (configuration 7: L_IM only)
 // Wave-split kernel (configurations of KswCfg): efficiencies from
 // graph-replay timings of every configuration at 1, 2 and 4 K splits on the
 // benchmark's small GEMMs and four neighbouring shapes (one MI355X).  It is
@@ -229,6 +237,7 @@ constexpr double kCoresidentPair = 0.75;
 constexpr int kAloneMinK = 1024;
 constexpr double kAlonePenalty = 1.3;
 constexpr int kMaxForcedSplits = 64;
+constexpr bool kOfferDl16 = true;
 
 // Tile grid and K split of configuration `cfg` asked for `s` splits (the
 // split count can come out lower: every split takes whole 16-deep chunks).
@@ -285,9 +294,10 @@ double plan_cycles(const CostModel& cm, const CfgCost& cc, const Plan& pl, int64
 
 // wide: the prefetching direct-to-LDS configurations (is_dlp_cfg) may be
 // chosen (see wide_ok in launch_gemm); ksw: the wave-split kernel may be;
-// imw: B is the weight-gradient operand (priced by kDlCostImw).
+// imw: B is the weight-gradient operand (priced by kDlCostImw); im16: the
+// convolution kernel on 16x16 blocks (is_dl16_cfg, B = L_IM) may be.
 Plan make_plan_uncached(int64_t M, int64_t N, int64_t K, int64_t batch, int cus,
-                        bool allow_split, bool dl, bool wide, bool ksw, bool imw) {
+                        bool allow_split, bool dl, bool wide, bool ksw, bool imw, bool im16) {
     static const CostModel cm;
     const CfgCost* cfgs = dl ? (imw ? kDlCostImw : kDlCost) : kRsCost;
     const int ncfg = dl ? kNumDlCfg : kNumCfg;
@@ -296,6 +306,7 @@ Plan make_plan_uncached(int64_t M, int64_t N, int64_t K, int64_t batch, int cus,
     double best_t = 1e300;
     for (int cfg = 0; cfg < ncfg; ++cfg) {
         if (dl && is_dlp_cfg(cfg) && !wide) continue;
+        if (dl && is_dl16_cfg(cfg) && !im16) continue;
         const CfgCost& cc = cfgs[cfg];
         for (int s = 1; s <= kMaxSplits; ++s) {
             if (s > 1 && !allow_split) break;
@@ -307,6 +318,11 @@ Plan make_plan_uncached(int64_t M, int64_t N, int64_t K, int64_t batch, int cus,
             const int64_t wgs = (int64_t)pl.tiles_m * pl.tiles_n * batch * pl.splits;
             if (dl && cfg == 6 && k6 < kDlp6MinK && wgs > cus) continue;
             if (wgs * 512 >= ((int64_t)1 << 32)) continue;
+            // The 64x112 tile of 16x16 blocks moves about twice the operand
+            // bytes per flop of the 256x128 one; with one workgroup per CU
+            // (nothing co-resident to hide the fetches) it lost everywhere it
+            // was measured (the 5a layer: 93.2 us against 80.2 at split 5).
+            if (dl && is_dl16_cfg(cfg) && wgs <= cus) continue;
             const double t = plan_cycles(cm, cc, pl, M, N, batch, cus);
             if (t < best_t) {
                 best_t = t;
@@ -341,11 +357,11 @@ Plan make_plan_uncached(int64_t M, int64_t N, int64_t K, int64_t batch, int cus,
 // holds several layers' worth, so the launch that follows a query finds its
 // plan instead of rerunning the cost model.
 Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool allow_split,
-               bool dl, bool wide, bool ksw, bool imw = false) {
+               bool dl, bool wide, bool ksw, bool imw = false, bool im16 = false) {
     struct Entry {
         int64_t M = -1, N = -1, K = -1, batch = -1;
         int cus = 0;
-        bool allow_split = false, dl = false, wide = false, ksw = false, imw = false;
+        bool allow_split = false, dl = false, wide = false, ksw = false, imw = false, im16 = false;
         Plan plan;
     };
     constexpr int kEntries = 128;
@@ -354,12 +370,12 @@ Plan make_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int cus, bool all
     for (const Entry& e : cache)
         if (e.M == M && e.N == N && e.K == K && e.batch == batch && e.cus == cus &&
             e.allow_split == allow_split && e.dl == dl && e.wide == wide && e.ksw == ksw &&
-            e.imw == imw)
+            e.imw == imw && e.im16 == im16)
             return e.plan;
     Entry& e = cache[next];
     next = (next + 1) % kEntries;
-    e = Entry{M, N, K, batch, cus, allow_split, dl, wide, ksw, imw,
-              make_plan_uncached(M, N, K, batch, cus, allow_split, dl, wide, ksw, imw)};
+    e = Entry{M, N, K, batch, cus, allow_split, dl, wide, ksw, imw, im16,
+              make_plan_uncached(M, N, K, batch, cus, allow_split, dl, wide, ksw, imw, im16)};
     return e.plan;
 }
 
@@ -374,9 +390,10 @@ thread_local ForcedConfig g_forced;
 // The plan of the forced configuration, when one is set and its family can
 // take these operands (dl_ok: both operands have direct-to-LDS layouts;
 // rs_ok: no implicit-im2col operand; wide_ok: the prefetching configurations
-// can take them too).
+// can take them too; im16_ok: B is L_IM, which the 16x16-block convolution
+// configurations take).
 bool forced_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dl_ok, bool rs_ok,
-                 bool wide_ok, Plan* out) {
+                 bool wide_ok, Plan* out, bool im16_ok = false) {
     const ForcedConfig f = g_forced;
     if (f.family == MT_FAMILY_KSW && rs_ok) {
         int bm, bn;
@@ -385,7 +402,8 @@ bool forced_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dl_ok, boo
         out->ksw = true;
         return true;
     }
-    if (f.family == MT_FAMILY_DL && dl_ok && (!is_dlp_cfg(f.cfg) || wide_ok)) {
+    if (f.family == MT_FAMILY_DL && dl_ok && (!is_dlp_cfg(f.cfg) || wide_ok) &&
+        (!is_dl16_cfg(f.cfg) || im16_ok)) {
         *out = cfg_plan(kDlCost[f.cfg], f.cfg, true, M, N, K, batch, f.splits);
         return true;
     }
@@ -492,6 +510,7 @@ GemmLaunchFn convh_launcher(int cfg) {
 }
 
 GemmLaunchFn conv_launcher(int cfg, bool nchw) {
+    if (is_dl16_cfg(cfg)) return nchw ? nullptr : dl16_conv_launcher(cfg - kDl16FirstCfg);
     switch (cfg) {
         case 0: return nchw ? dl_convr_launcher_cfg0() : dl_conv_launcher_cfg0();
         case 1: return nchw ? dl_convr_launcher_cfg1() : dl_conv_launcher_cfg1();
@@ -893,7 +912,8 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
     // range.
     const bool wide_ok = dl && lb != L_IM && lb != L_IMR && K > 0;
     Plan plan;
-    const bool forced = forced_plan(M, N, K, batch, dl, !implicit, wide_ok, &plan);
+    const bool im16_ok = dl && lb == L_IM;
+    const bool forced = forced_plan(M, N, K, batch, dl, !implicit, wide_ok, &plan, im16_ok);
     if (forced) {
         if (plan.splits > 1 && (workspace == nullptr || ws_bytes < plan.ws_bytes))
             return MT_ERR_WORKSPACE;
@@ -902,10 +922,10 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
         // convolution operands and the fused row sums
         const bool ksw_ok = !implicit && p.rowsum == nullptr;
         plan = make_plan(M, N, K, batch, device_cu_count(), true, dl, wide_ok, ksw_ok,
-                         lb == L_IMW);
+                         lb == L_IMW, im16_ok && kOfferDl16);
         if (plan.splits > 1 && (workspace == nullptr || ws_bytes < plan.ws_bytes))
             plan = make_plan(M, N, K, batch, device_cu_count(), false, dl, wide_ok, ksw_ok,
-                             lb == L_IMW);
+                             lb == L_IMW, im16_ok && kOfferDl16);
     }
     if (!plan.dl || plan.splits > 1) p.rowsum = nullptr;
     p.splits = plan.splits;
@@ -1789,8 +1809,10 @@ size_t implicit_gemm_ws(int64_t M, int64_t N, int64_t K, bool imw) {
     if (M <= 0 || N <= 0 || K <= 0) return 0;
     const int cus = device_cu_count();
     size_t ws = make_plan(M, N, K, 1, cus, true, true, imw, false, imw).ws_bytes;
+    if (!imw && kOfferDl16)   // the channels-last operand may take the 16x16-block kernel
+        ws = std::max(ws, make_plan(M, N, K, 1, cus, true, true, false, false, false, true).ws_bytes);
     Plan f;
-    if (forced_plan(M, N, K, 1, true, false, imw, &f)) ws = std::max(ws, f.ws_bytes);
+    if (forced_plan(M, N, K, 1, true, false, imw, &f, !imw)) ws = std::max(ws, f.ws_bytes);
     return ws;
 }
 

@@ -159,14 +159,14 @@ def test_python_front_end_errors():
 
 def test_config_counts():
     assert mt.config_count(mt.FAMILY_RS) == 3
-    assert mt.config_count(mt.FAMILY_DL) == 7
+    assert mt.config_count(mt.FAMILY_DL) == 8
     assert mt.config_count(mt.FAMILY_KSW) == 9
     assert mt.config_count(mt.FAMILY_SKINNY) == 2
     assert mt.config_count(mt.FAMILY_AUTO) == 0
 
 
 @pytest.mark.parametrize("family,cfg,splits", [
-    (5, 0, 1), (-1, 0, 1), (mt.FAMILY_RS, 3, 1), (mt.FAMILY_DL, 7, 1), (mt.FAMILY_DL, -1, 1),
+    (5, 0, 1), (-1, 0, 1), (mt.FAMILY_RS, 3, 1), (mt.FAMILY_DL, 8, 1), (mt.FAMILY_DL, -1, 1),
     (mt.FAMILY_KSW, 9, 1), (mt.FAMILY_KSW, -1, 1), (mt.FAMILY_SKINNY, 2, 1),
     (mt.FAMILY_SKINNY, 0, 65),
     (mt.FAMILY_DL, 0, 0), (mt.FAMILY_DL, 0, 65)])
