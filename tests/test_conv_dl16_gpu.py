@@ -143,3 +143,51 @@ def test_cost_model_keeps_the_5a_layer_off_it(dev):
     w = torch.zeros(256, 256, 3, 3, device=dev)
     mt.conv2d(x, w, None, 1, 1)
     assert mt.last_config().startswith("dl 256x128 "), mt.last_config()
+
+
+def test_graph_replays_match_eager(dev):
+    """The 28x28 layer's forward and input gradient (both on this kernel)
+    captured in a HIP graph: every replay, with the inputs changed in place
+    between them, gives the eager result bit for bit."""
+    import ctypes
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(11)
+    x = torch.randn(32, 128, 28, 28, device=dev, generator=gen)
+    w = torch.randn(128, 128, 3, 3, device=dev, generator=gen) * 0.03
+    b = torch.randn(128, device=dev, generator=gen)
+    dy = torch.randn(32, 128, 28, 28, device=dev, generator=gen) * 0.01
+    d = mt.Conv2dDesc(32, 128, 28, 28, 128, 3, 3, 1, 1)
+    ws = mt.workspace(max(mt.lib().mt_conv2d_workspace_f32(ctypes.byref(d)),
+                          mt.lib().mt_conv2d_bwd_workspace_f32(ctypes.byref(d))), dev)
+    y, dx = torch.empty_like(x), torch.empty_like(x)
+    names = []
+
+    def step():
+        y.copy_(mt.conv2d(x, w, b, 1, 1, ws=ws))
+        names.append(mt.last_config())
+        gx, _, _ = mt.conv2d_backward(x, w, dy, 1, 1, need_dw=False, need_db=False, ws=ws)
+        names.append(mt.last_config())
+        dx.copy_(gx)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    assert all(n.endswith(" cfg=7") for n in names[:2]), names[:2]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    torch.cuda.synchronize()
+    for rep in range(3):
+        x.mul_(0.5).add_(0.1)
+        dy.mul_(-1.0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = (y.clone(), dx.clone())
+        step()
+        torch.cuda.synchronize()
+        assert torch.equal(got[0], y) and torch.equal(got[1], dx), f"replay {rep} differs"
+        print(f"[graph] dl16 replay {rep} == eager", flush=True)
