@@ -76,7 +76,8 @@ def parse():
                         "every forced tile configuration and split on COUNT random row-major "
                         "shapes (sizes 64-4700, seeded) and print one line per shape and a summary")
     p.add_argument("--only", default="",
-                   help="comma list of secondary configs (c1,c3,c4,c5a,c5b,skinny) and/or "
+                   help="comma list of secondary configs (c1,c3,c4,c5a,c5b,skinny), 'resnet' "
+                        "(twelve ResNet-like conv layers, not in the default run) and/or "
                         "'sustained' (the headline GEMM back to back for 2.5 s): run just those "
                         "and print their JSON, without the headline and CPU legs "
                         "(per-workload profiles)")
@@ -200,6 +201,14 @@ def time_graph(fn, calls: int = 20, replays: int = 10, preroll_ms: float = PRERO
 
 
 SECONDARY = ("c1", "c3", "c4", "c5a", "c5b", "skinny")
+# Not in the default run (--only resnet): twelve ResNet-like convolution
+# layers at batch 32, 3x3 and 1x1, 7x7 to 56x56 -- where the 64x112
+# convolution tile on 16x16 MFMA blocks is or is not taken.
+EXTRA = ("resnet",)
+RESNET_LAYERS = [(56, 64, 64, 3), (56, 64, 256, 1), (56, 256, 64, 1),
+                 (28, 128, 128, 3), (28, 128, 512, 1), (28, 512, 128, 1),
+                 (14, 256, 256, 3), (14, 256, 1024, 1), (14, 1024, 256, 1),
+                 (7, 512, 512, 3), (7, 512, 2048, 1), (7, 2048, 512, 1)]
 SUSTAINED_S = 2.5
 
 
@@ -428,6 +437,17 @@ def secondary(dev, only=SECONDARY) -> dict:
         ms = both(lambda: mt.gemm(A, B, out=C, ws=ws), 200, 20)
         rec("c5b_bmm_64x512x512x64", ms, 2 * 64 * 512 * 512 * 64,
             4 * 64 * (512 * 64 + 64 * 512 + 512 * 512), mt.last_config())
+
+    if "resnet" in only:  # (hw, c_in, c_out, k): stride 1, "same" padding, batch 32
+        for hw, c, co, k in RESNET_LAYERS:
+            x = n(32, c, hw, hw)
+            w = n(co, c, k, k, std=(2.0 / (c * k * k)) ** 0.5)
+            cb = torch.zeros(co, device=dev)
+            d = mt.Conv2dDesc(32, c, hw, hw, co, k, k, 1, k // 2)
+            cws = mt.workspace(mt.lib().mt_conv2d_workspace_f32(ctypes.byref(d)), dev)
+            ms = both(lambda: mt.conv2d(x, w, cb, 1, k // 2, ws=cws), 50, 5)
+            rec(f"resnet_conv{k}x{k}_{hw}x{hw}_{c}to{co}", ms, 2 * 32 * hw * hw * co * c * k * k,
+                4 * (x.numel() + w.numel() + co + 32 * co * hw * hw), mt.last_config())
 
     if "skinny" in only:
         # The reference's HBM-bound matmul rows (test/benchmark.cpp:732,737-738,
@@ -675,10 +695,10 @@ def main():
         return
     if args.only:
         names = tuple(x.strip() for x in args.only.split(",") if x.strip())
-        unknown = [x for x in names if x not in SECONDARY + ("sustained",)]
+        unknown = [x for x in names if x not in SECONDARY + EXTRA + ("sustained",)]
         if unknown:
             print(f"bench.py: unknown --only entries {unknown}; choose from "
-                  f"{SECONDARY + ('sustained',)}", file=sys.stderr)
+                  f"{SECONDARY + EXTRA + ('sustained',)}", file=sys.stderr)
             sys.exit(2)
         res = {"secondary": secondary(dev, tuple(x for x in names if x != "sustained"))}
         if "sustained" in names:
