@@ -191,3 +191,55 @@ def test_graph_replays_match_eager(dev):
         torch.cuda.synchronize()
         assert torch.equal(got[0], y) and torch.equal(got[1], dx), f"replay {rep} differs"
         print(f"[graph] dl16 replay {rep} == eager", flush=True)
+
+
+def _random_case(rng, i):
+    while True:
+        kh = int(rng.integers(1, 6))
+        kw = kh if rng.random() < 0.5 else int(rng.integers(1, 6))
+        d = dict(n=int(rng.integers(1, 5)), c=16 * int(rng.integers(1, 6)),
+                 co=int(rng.integers(1, 150)), h=int(rng.integers(1, 24)),
+                 w=int(rng.integers(1, 24)), kh=kh, kw=kw, stride=int(rng.integers(1, 4)),
+                 pad=int(rng.integers(0, 3)), split=int(rng.choice([1, 1, 2, 3])),
+                 view=str(rng.choice(["dense", "dense", "channel_slice", "nhwc"])),
+                 bias=bool(rng.random() < 0.6), seed=9100 + 10 * i)
+        if (oracle.conv_out(d["h"], d["pad"], kh, d["stride"]) > 0
+                and oracle.conv_out(d["w"], d["pad"], kw, d["stride"]) > 0):
+            return d
+
+
+N_RANDOM = 24
+_rng = np.random.default_rng(20261204)
+RANDOM_CASES = [_random_case(_rng, i) for i in range(N_RANDOM)]
+
+
+@pytest.mark.parametrize("case", RANDOM_CASES, ids=[f"r{i}" for i in range(N_RANDOM)])
+def test_random_forced(dev, case):
+    """Seeded draws on configuration 7: c_in a multiple of 16 (the channels-last
+    operand), any c_out (ragged tile rows), 1x1 to 5x5 kernels, strides 1-3,
+    padding 0-2, dense, channel-slice or channels-last NCHW views, bias or none,
+    split-K 1-3."""
+    n, c, h, wd, co = case["n"], case["c"], case["h"], case["w"], case["co"]
+    kh, kw, stride, pad, seed = case["kh"], case["kw"], case["stride"], case["pad"], case["seed"]
+    x = oracle.normal((n, c, h, wd), seed)
+    w = oracle.normal((co, c, kh, kw), seed + 1)
+    b = oracle.normal((co,), seed + 2) if case["bias"] else None
+    if case["view"] == "channel_slice":
+        big = np.zeros((n, c + 3, h, wd), np.float32)
+        big[:, 1:1 + c] = x
+        X = torch.from_numpy(big).to(dev)[:, 1:1 + c]
+    elif case["view"] == "nhwc":
+        X = torch.from_numpy(np.ascontiguousarray(x.transpose(0, 2, 3, 1))).to(dev).permute(0, 3, 1, 2)
+    else:
+        X = torch.from_numpy(x).to(dev)
+    W = torch.from_numpy(w).to(dev)
+    Bt = torch.from_numpy(b).to(dev) if b is not None else None
+    with mt.forced_config(mt.FAMILY_DL, 7, case["split"]):
+        y = mt.conv2d(X, W, Bt, stride, pad)
+        name = mt.last_config()
+    torch.cuda.synchronize()
+    print(f"[case] {case} -> {name}", flush=True)
+    assert name.startswith("dl 64x112 ") and name.endswith(" cfg=7"), name
+    extra = 2e-6 * (1.0 + amax(b)) if b is not None else 0.0
+    assert_close(y.cpu().numpy(), oracle.conv2d(x, w, b, stride, pad), c * kh * kw, amax(x),
+                 amax(w), f"dl16 random {case}", extra=extra)
