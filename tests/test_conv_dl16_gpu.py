@@ -243,3 +243,29 @@ def test_random_forced(dev, case):
     extra = 2e-6 * (1.0 + amax(b)) if b is not None else 0.0
     assert_close(y.cpu().numpy(), oracle.conv2d(x, w, b, stride, pad), c * kh * kw, amax(x),
                  amax(w), f"dl16 random {case}", extra=extra)
+
+
+def test_output_beyond_2pow31_elements(dev):
+    """1x1, 16 -> 8320 channels, batch 64, 64x64: 2.18e9 output elements
+    (8.7 GB); image 63 starts past 2^31, so a 32-bit index anywhere in the
+    loaders or the scattered NCHW store would alias.  Sampled channels of the
+    first and last images against the oracle."""
+    n, c, hw, co = 64, 16, 64, 8320
+    x = oracle.normal((n, c, hw, hw), 95)
+    w = oracle.normal((co, c, 1, 1), 96)
+    b = oracle.normal((co,), 97)
+    with mt.forced_config(mt.FAMILY_DL, 7, 1):
+        y = mt.conv2d(torch.from_numpy(x).to(dev), torch.from_numpy(w).to(dev),
+                      torch.from_numpy(b).to(dev), 1, 0)
+        name = mt.last_config()
+    torch.cuda.synchronize()
+    print(f"[config] {name}", flush=True)
+    assert name.endswith(" cfg=7"), name
+    chans = np.array([0, 1, 4095, 4096, 8191, 8318, 8319], np.int64)
+    for img in (0, 63):
+        got = y[img, torch.from_numpy(chans).to(dev)].cpu().numpy()
+        want = oracle.conv2d(x[img:img + 1], w[chans], b[chans], 1, 0)[0]
+        assert_close(got, want, c, amax(x), amax(w), f"img {img} past 2^31",
+                     extra=2e-6 * (1.0 + amax(b)))
+    del y
+    torch.cuda.empty_cache()
