@@ -53,7 +53,8 @@ def test_dx_by_phase(dev, case):
     # The library picks the phased or the column path by modelled cost (small
     # layers like these mostly take the column path); a forced direct-to-LDS
     # configuration skips that rule, so the phase GEMMs run on every case that
-    # they can take, under two tile configurations.
+    # they can take, under three tile configurations (7: the 64x112 tile of
+    # 16x16 blocks, channels-last phases only; elsewhere the cost model's).
     n, c, h, w, co, kh, kw, stride, pad, path = case
     ho, wo = oracle.conv_out(h, pad, kh, stride), oracle.conv_out(w, pad, kw, stride)
     x = oracle.normal((n, c, h, w), 11 + c)
@@ -65,7 +66,7 @@ def test_dx_by_phase(dev, case):
     torch.cuda.synchronize()
     print(f"[config] {case} auto: {mt.last_config()}", flush=True)
     assert_close(dX.cpu().numpy(), want, co * kh * kw, amax(dy), amax(wt), f"dX {case} auto")
-    for cfg_i in (1, 3):
+    for cfg_i in (1, 3, 7):
         with mt.forced_config(mt.FAMILY_DL, cfg_i, 1):
             dX, _, _ = mt.conv2d_backward(X, W, dY, stride, pad, need_dw=False, need_db=False)
             torch.cuda.synchronize()
@@ -74,7 +75,7 @@ def test_dx_by_phase(dev, case):
             torch.cuda.synchronize()
         print(f"[config] {case} forced {cfg_i}: {cfg}", flush=True)
         if path == "cl":
-            assert "b=im2col " in cfg + " ", cfg
+            assert "b=im2col " in cfg + " " and cfg.endswith(f" cfg={cfg_i}"), cfg
         elif path == "nchw":
             assert "b=im2col_nchw" in cfg or "b=im2col_halo" in cfg, cfg
         else:
@@ -119,7 +120,7 @@ def test_dx_by_phase_forced_split(dev):
     dy = oracle.normal((n, co, 8, 7), 23)
     want, _, _ = oracle.conv2d_backward(x, wt, dy, stride, pad)
     X, W, dY = (torch.from_numpy(t).to(dev) for t in (x, wt, dy))
-    for cfg in (1, 2, 3):
+    for cfg in (1, 2, 3, 7):
         with mt.forced_config(mt.FAMILY_DL, cfg, 3):
             dX, _, _ = mt.conv2d_backward(X, W, dY, stride, pad, need_dw=False, need_db=False)
             torch.cuda.synchronize()
