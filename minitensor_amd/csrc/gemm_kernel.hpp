@@ -362,36 +362,77 @@ constexpr int stage_blocks() {
     return jp;
 }
 
+// The epilogue operands of four consecutive output columns n..n+3 of row m:
+// the row bias, the column biases and the old C (for beta), loaded ahead of
+// the stores.  (On gfx950 vmcnt also counts stores in flight, so a load
+// between two stores makes the second wait for the first to complete: an
+// epilogue loop that loads and stores in each pass runs one store round trip
+// per pass.  Loading every pass's operands first keeps the stores back to
+// back.)  Columns past N read nothing (element-wise form).
+struct Epi4 {
+    float brow;
+    f32x4 bcol, cold;
+};
+__device__ __forceinline__ Epi4 epi_load4(const GemmParams& p, const float* base, int64_t rs,
+                                          bool part, bool vec, int bias_axis, float beta, int m,
+                                          int n) {
+    Epi4 e;
+    e.brow = bias_axis == 1 ? p.bias[(int64_t)m * p.bias_stride] : 0.f;
+    e.bcol = f32x4{0.f, 0.f, 0.f, 0.f};
+    e.cold = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (bias_axis == 2)
+#pragma unroll
+        for (int x = 0; x < 4; ++x)
+            if (vec || n + x < p.N) e.bcol[x] = p.bias[(int64_t)(n + x) * p.bias_stride];
+    if (beta != 0.f) {
+        const float* const row = base + (int64_t)m * rs;
+        if (vec) {
+            e.cold = *reinterpret_cast<const f32x4*>(row + (part ? (int64_t)n : col_offset(p, n)));
+        } else {
+#pragma unroll
+            for (int x = 0; x < 4; ++x)
+                if (n + x < p.N) e.cold[x] = row[part ? (int64_t)(n + x) : col_offset(p, n + x)];
+        }
+    }
+    return e;
+}
+
 // Stores four consecutive output columns n..n+3 of row m (v, the bare sums):
 // C = v + bias + beta*C through col(n), 16-byte when `vec`, element by element
 // otherwise (columns past N skipped); or, for a split-K launch (`part`), the
-// raw partial into the split's workspace slab at `base` (row stride rs).
-__device__ __forceinline__ void store_group4(const GemmParams& p, float* base, int64_t rs,
-                                             bool part, bool vec, int bias_axis, float beta,
-                                             int m, int n, f32x4 v) {
+// raw partial into the split's workspace slab at `base` (row stride rs).  The
+// operands come from epi_load4 with the same arguments.
+__device__ __forceinline__ void epi_store4(const GemmParams& p, float* base, int64_t rs,
+                                           bool part, bool vec, int bias_axis, float beta, int m,
+                                           int n, f32x4 v, const Epi4& e) {
     float* const row = base + (int64_t)m * rs;
-    const float brow = bias_axis == 1 ? p.bias[(int64_t)m * p.bias_stride] : 0.f;
     if (vec) {
         f32x4 o;
 #pragma unroll
         for (int x = 0; x < 4; ++x) {
-            o[x] = v[x] + brow;
-            if (bias_axis == 2) o[x] += p.bias[(int64_t)(n + x) * p.bias_stride];
+            o[x] = v[x] + e.brow;
+            if (bias_axis == 2) o[x] += e.bcol[x];
         }
-        f32x4* const dst = reinterpret_cast<f32x4*>(row + (part ? (int64_t)n : col_offset(p, n)));
-        if (beta != 0.f) o += beta * *dst;
-        *dst = o;
+        if (beta != 0.f) o += beta * e.cold;
+        *reinterpret_cast<f32x4*>(row + (part ? (int64_t)n : col_offset(p, n))) = o;
     } else {
 #pragma unroll
         for (int x = 0; x < 4; ++x) {
             if (n + x >= p.N) break;
-            float o = v[x] + brow;
-            if (bias_axis == 2) o += p.bias[(int64_t)(n + x) * p.bias_stride];
-            float* const dst = row + (part ? (int64_t)(n + x) : col_offset(p, n + x));
-            if (beta != 0.f) o += beta * *dst;
-            *dst = o;
+            float o = v[x] + e.brow;
+            if (bias_axis == 2) o += e.bcol[x];
+            if (beta != 0.f) o += beta * e.cold[x];
+            row[part ? (int64_t)(n + x) : col_offset(p, n + x)] = o;
         }
     }
+}
+
+// epi_load4 then epi_store4: one group's loads and store together.
+__device__ __forceinline__ void store_group4(const GemmParams& p, float* base, int64_t rs,
+                                             bool part, bool vec, int bias_axis, float beta,
+                                             int m, int n, f32x4 v) {
+    epi_store4(p, base, rs, part, vec, bias_axis, beta, m, n, v,
+               epi_load4(p, base, rs, part, vec, bias_axis, beta, m, n));
 }
 
 // Epilogue of a workgroup of NW waves (wave tiles WM x WN, WAVES_N per tile

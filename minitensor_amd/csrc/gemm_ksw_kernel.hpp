@@ -103,15 +103,33 @@ __device__ __forceinline__ void ksw_store(const GemmParams& p, const TileId& id,
     const float beta = part ? 0.f : p.beta;
     const bool vec = part ? p.ws_vec : p.c_vec;
     constexpr int GN = BN / 4;
-#pragma unroll 1
-    for (int g = threadIdx.x; g < BM * GN; g += NT) {
-        const int r = g / GN, cn = 4 * (g - r * GN);
-        const int m = m0 + r, n = n0 + cn;
-        if (m >= p.M || n >= p.N) continue;
-        f32x4 v = *reinterpret_cast<const f32x4*>(red + r * PITCH + cn);
+    constexpr int IT = (BM * GN + NT - 1) / NT;   // groups per thread
+    // Every group's epilogue loads (biases, beta*C) before the first store:
+    // a load behind a store waits for that store (vmcnt counts both).
+    int ms[IT], ns[IT], rr[IT], cc[IT];
+    bool ok[IT];
+    Epi4 es[IT];
 #pragma unroll
-        for (int w = 1; w < W; ++w) v += *reinterpret_cast<const f32x4*>(red + (w * BM + r) * PITCH + cn);
-        store_group4(p, base, rs, part, vec, bias_axis, beta, m, n, v);
+    for (int i = 0; i < IT; ++i) {
+        const int g = threadIdx.x + i * NT;
+        rr[i] = g / GN;
+        cc[i] = 4 * (g - rr[i] * GN);
+        ms[i] = m0 + rr[i];
+        ns[i] = n0 + cc[i];
+        ok[i] = g < BM * GN && ms[i] < p.M && ns[i] < p.N;
+        if (ok[i]) es[i] = epi_load4(p, base, rs, part, vec, bias_axis, beta, ms[i], ns[i]);
+    }
+    // those loads landed before the first store (none is in flight yet), so
+    // that the compiler places no wait between two stores
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+        if (!ok[i]) continue;
+        f32x4 v = *reinterpret_cast<const f32x4*>(red + rr[i] * PITCH + cc[i]);
+#pragma unroll
+        for (int w = 1; w < W; ++w)
+            v += *reinterpret_cast<const f32x4*>(red + (w * BM + rr[i]) * PITCH + cc[i]);
+        epi_store4(p, base, rs, part, vec, bias_axis, beta, ms[i], ns[i], v, es[i]);
     }
 }
 

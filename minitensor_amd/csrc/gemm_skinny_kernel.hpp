@@ -224,7 +224,8 @@ __global__ void __launch_bounds__(256) gemv_kv_f32(GemmParams p) {
 
 template <int KMAX>
 __global__ void __launch_bounds__(256) rankk_f32(GemmParams p) {
-    __shared__ float la[kRankKRows * KMAX];
+    static_assert(KMAX % 4 == 0, "A's rows are read from LDS 16 bytes at a time");
+    __shared__ __attribute__((aligned(16))) float la[kRankKRows * KMAX];
     const int t = threadIdx.x;
     const int cb = blockIdx.x % p.tiles_n;
     const int rest = blockIdx.x / p.tiles_n;
@@ -232,32 +233,77 @@ __global__ void __launch_bounds__(256) rankk_f32(GemmParams p) {
     const int m0 = rb * kRankKRows;
     const float* const Ab = p.A + (int64_t)bz * p.a_b;
     const float* const Bb = p.B + (int64_t)bz * p.b_b;
+    const int n = cb * kRankKCols + 4 * t;
+    // B's K x 4 block first, so that its loads are in flight with A's (one
+    // memory round trip before the first store instead of two); one 16-byte
+    // load per k where the four columns are contiguous and aligned.
+    // (Every index into b is a compile-time constant -- whole unrolled loops,
+    // a uniform k < K test instead of a break -- so that b stays in registers:
+    // with a runtime-bounded loop the 16-deep instance kept it in scratch and
+    // took 128 us at K = 16, against 22 us for the MFMA kernel at K = 17.)
+    f32x4 b[KMAX];
+    const bool bvec = p.b_mn == 1 && n + 3 < p.N && ((uintptr_t)(Bb + n) & 15u) == 0 &&
+                      (p.b_k & 3) == 0;
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+        f32x4 x = {0.f, 0.f, 0.f, 0.f};
+        if (k < p.K) {
+            if (bvec) {
+                x = *reinterpret_cast<const f32x4*>(Bb + n + (int64_t)k * p.b_k);
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (n + c < p.N) x[c] = Bb[(int64_t)(n + c) * p.b_mn + (int64_t)k * p.b_k];
+            }
+        }
+        b[k] = x;
+    }
     for (int e = t; e < kRankKRows * KMAX; e += 256) {
         const int r = e / KMAX, k = e % KMAX, m = m0 + r;
         la[e] = (m < p.M && k < p.K) ? Ab[(int64_t)m * p.a_mn + (int64_t)k * p.a_k] : 0.f;
     }
     __syncthreads();
-    const int n = cb * kRankKCols + 4 * t;
     if (n >= p.N) return;
-    f32x4 b[KMAX];
-#pragma unroll
-    for (int k = 0; k < KMAX; ++k) {
-        if (k >= p.K) break;
-#pragma unroll
-        for (int x = 0; x < 4; ++x)
-            b[k][x] = n + x < p.N ? Bb[(int64_t)(n + x) * p.b_mn + (int64_t)k * p.b_k] : 0.f;
-    }
     float* const Cb = p.C + (int64_t)bz * p.c_b;
     const int rows = min(kRankKRows, p.M - m0);
-    for (int r = 0; r < rows; ++r) {
-        const float* const a = la + r * KMAX;
+    // Row r's sum over k in order, A's row read from LDS 16 bytes at a time
+    // (one ds_read_b32 per k per row had made K the kernel's cost: 0.9 us
+    // per unit of K at 2048 x 2048).
+    auto row_sum = [&](int r) {
+        const f32x4* const a4 = reinterpret_cast<const f32x4*>(la + r * KMAX);
         f32x4 v = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int k = 0; k < KMAX; ++k) {
-            if (k >= p.K) break;   // uniform
-            v += a[k] * b[k];
+        for (int q = 0; q < KMAX / 4; ++q) {
+            if (4 * q >= p.K) continue;   // uniform
+            const f32x4 a = a4[q];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (4 * q + e < p.K) v += a[e] * b[4 * q + e];
         }
-        store_group4(p, Cb, p.c_m, false, p.c_vec, p.bias_axis, p.beta, m0 + r, n, v);
+        return v;
+    };
+    // 16-byte stores without a row bias or beta: the only epilogue loads are
+    // the column biases, the same for every row, landed before the first
+    // store.  (A load between two stores waits for the first, since vmcnt
+    // counts both: with the general epilogue each row waited for the
+    // previous row's store, 9.6 us for a 1024 x 4096 output.)
+    if (p.c_vec && p.c_n_inner >= p.N && p.bias_axis != 1 && p.beta == 0.f) {
+        f32x4 bc = {0.f, 0.f, 0.f, 0.f};
+        if (p.bias_axis == 2)
+#pragma unroll
+            for (int x = 0; x < 4; ++x) bc[x] = p.bias[(int64_t)(n + x) * p.bias_stride];
+        float* const c0 = Cb + (int64_t)m0 * p.c_m + n;
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));   // no store is in flight yet
+#pragma unroll
+        for (int r = 0; r < kRankKRows; ++r)
+            if (r < rows) {   // uniform
+                f32x4 o = row_sum(r);
+                if (p.bias_axis == 2) o += bc;
+                *reinterpret_cast<f32x4*>(c0 + (int64_t)r * p.c_m) = o;
+            }
+    } else {
+        for (int r = 0; r < rows; ++r)
+            store_group4(p, Cb, p.c_m, false, p.c_vec, p.bias_axis, p.beta, m0 + r, n, row_sum(r));
     }
 }
 

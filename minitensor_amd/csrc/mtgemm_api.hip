@@ -215,6 +215,13 @@ constexpr CfgCost kKswCost[kNumKswCfg] = {
     {KswTile<6>::bm, KswTile<6>::bn, 0.27, 4},
     {KswTile<7>::bm, KswTile<7>::bn, 0.47, 4},
     {KswTile<8>::bm, KswTile<8>::bn, 0.49, 4}};
+// Its waves split the K-chunks, so a K range of fewer chunks than waves
+// leaves some idle and pays the cross-wave sum for nothing: not offered there
+// (512 x 1024 x 16: 4.1 us on the 32x64 wave-split tile against 3.1 on the
+// 64x64 prefetching one).
+constexpr int kKswWaves[kNumKswCfg] = {KswCfg<0>::W, KswCfg<1>::W, KswCfg<2>::W,
+                                       KswCfg<3>::W, KswCfg<4>::W, KswCfg<5>::W,
+                                       KswCfg<6>::W, KswCfg<7>::W, KswCfg<8>::W};
 
 // Configuration 6 pays off only over long K ranges (short ones, such as the
 // 64-deep batched GEMM of the benchmark, run up to 20 % slower than
@@ -333,6 +340,7 @@ Plan make_plan_uncached(int64_t M, int64_t N, int64_t K, int64_t batch, int cus,
     }
     if (ksw) {
         for (int cfg = 0; cfg < kNumKswCfg; ++cfg) {
+            if (K < (int64_t)kBK * kKswWaves[cfg]) continue;
             Plan pl = cfg_plan(kKswCost[cfg], cfg, false, M, N, K, batch, 1);
             pl.ksw = true;
             const int64_t wgs = (int64_t)pl.tiles_m * pl.tiles_n * batch;
@@ -523,13 +531,15 @@ GemmLaunchFn conv_launcher(int cfg, bool nchw) {
 // ---- HBM-bound shapes on the vector ALUs (gemm_skinny_kernel.hpp) ----------
 // GEMV: at most kGemvMaxRows rows of A against a B that is k- or
 // mn-contiguous (or, transposed, at most that many columns of B against such
-// an A), K >= kGemvMinK; rank-k: 1 <= K <= kRankKMax with at least
-// kRankKMinN columns.  No implicit convolution operand and no fused row or
+// an A), K >= kGemvMinK; rank-k: 1 <= K <= 2 (4) with at least kRankKMinN
+// columns and 2^22 (2^24) output elements, or forced with K <= kRankKMax.  No implicit convolution operand and no fused row or
 // channel sums: those shapes keep the MFMA kernels.
 enum { SK_NONE = 0, SK_GEMV = 1, SK_RANKK = 2 };
 constexpr int kGemvMinK = 16;
 constexpr int kGemvKvMaxRows = 4;
 constexpr int kRankKMinN = 256;
+constexpr int64_t kRankKAutoMn2 = int64_t(1) << 22;   // outputs taking rank-k at K <= 2
+constexpr int64_t kRankKAutoMn4 = int64_t(1) << 24;   // ... and at K <= 4
 constexpr int kGemvMaxSplits = 64;
 constexpr int kGemvWgsPerCu = 4;
 // An mn-contiguous B of more than 64 MiB: about six workgroups per CU with
@@ -607,7 +617,17 @@ SkinnyPlan skinny_plan(int64_t M, int64_t N, int64_t K, int64_t batch, int la, i
     const bool forced = f.family == MT_FAMILY_SKINNY;
     const int splits = forced ? f.splits : 0;
     const bool vec_b = lb == L_MV || lb == L_KV, vec_a = la == L_MV || la == L_KV;
-    if ((!forced || f.cfg == 1) && K <= kRankKMax && N >= kRankKMinN) return rankk_plan(M, N, K, batch);
+    // The rank-k kernel only writes C (its cost is the store stream), the MFMA
+    // kernels also stage a 16-deep chunk: it wins on large outputs with the
+    // smallest K.  Graph-timed against the best forced MFMA plan: 4096^2 K = 1,
+    // 2, 4: 12.3, 12.6, 13.5 against 14.5, 15.7, 14.7 us; 2048^2 K = 1, 2: 5.6,
+    // 6.2 against 7.0, 7.3, but K = 4: 8.0 against 7.1; 256 x 8192 K = 1: 4.9
+    // against 4.5; K >= 8 the MFMA kernels on every shape (4096^2 K = 8: 15.7
+    // against 14.7).  A forced configuration 1 takes any K <= kRankKMax.
+    const int64_t mn = M * N * batch;
+    const bool rk_auto = (K <= 2 && mn >= kRankKAutoMn2) || (K <= 4 && mn >= kRankKAutoMn4);
+    if ((forced ? f.cfg == 1 : rk_auto) && K <= kRankKMax && N >= kRankKMinN)
+        return rankk_plan(M, N, K, batch);
     if (forced && f.cfg != 0) return none;
     if (K < kGemvMinK) return none;
     // With a k-contiguous B the GEMV kernel reads A's rows from LDS beside

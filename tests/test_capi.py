@@ -229,3 +229,21 @@ def test_conv_backward_workspace_is_the_paths_need():
     col = 256 * 9 * 32 * 196 * 4
     xt = 32 * 256 * 196 * 4
     assert xt < need < col, need
+
+
+def test_build_refuses_kernels_with_scratch():
+    """The build raises on a kernel whose resource remark reports scratch
+    (spilled registers): parse of hipcc's -Rpass-analysis=kernel-resource-usage
+    lines."""
+    from minitensor_amd import build
+    out = "\n".join([
+        "x.hpp:1:1: remark: Function Name: _ZN3mtk9rankk_f32ILi16EEEvNS_10GemmParamsE "
+        "[-Rpass-analysis=kernel-resource-usage]",
+        "x.hpp:1:1: remark:     VGPRs: 86 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hpp:1:1: remark:     ScratchSize [bytes/lane]: 272 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hpp:2:1: remark: Function Name: _ZN3mtk9rankk_f32ILi4EEEvNS_10GemmParamsE "
+        "[-Rpass-analysis=kernel-resource-usage]",
+        "x.hpp:2:1: remark:     ScratchSize [bytes/lane]: 0 [-Rpass-analysis=kernel-resource-usage]",
+    ])
+    assert build._scratch_kernels(out) == [("_ZN3mtk9rankk_f32ILi16EEEvNS_10GemmParamsE", 272)]
+    assert build._scratch_kernels("no remarks here") == []

@@ -163,8 +163,8 @@ def test_graph_skinny_and_phased_dx_replays(dev):
     cv = torch.empty(1000, 3, device=dev)
     ws_t = mt.workspace(mt.lib().mt_gemm_workspace_f32(mt.mat(At), mt.mat(v), mt.mat(cv)), dev)
     u = torch.rand(2048, 2, device=dev, generator=gen)
-    w2 = torch.rand(2, 1024, device=dev, generator=gen)
-    r = torch.empty(2048, 1024, device=dev)
+    w2 = torch.rand(2, 2048, device=dev, generator=gen)
+    r = torch.empty(2048, 2048, device=dev)
     x = torch.randn(4, 32, 28, 28, device=dev, generator=gen)
     wc = torch.randn(64, 32, 1, 1, device=dev, generator=gen) * 0.1
     dy = torch.randn(4, 64, 14, 14, device=dev, generator=gen)

@@ -1,5 +1,6 @@
 """GPU parity of the vector-ALU kernels of the HBM-bound shapes (GEMV for at
-most 8 rows of A or columns of B, rank-k for K <= 16) against the CPU oracle
+most 8 rows of A or columns of B, rank-k for K <= 16, forced where the cost model
+prefers the MFMA kernels) against the CPU oracle
 (the reference's matmul_cpu / matmul_cpu_strided restated in oracle/oracle.c).
 
 The shapes include the reference benchmark's skinny rows
@@ -84,17 +85,46 @@ def test_gemv_few_columns(dev, M, N, K, a_t):
     assert_close(c.cpu().numpy(), oracle.matmul(a, b), K, amax(a), amax(b), f"{M}x{N}x{K} T")
 
 
-@pytest.mark.parametrize("M,N,K", [
-    (4096, 4096, 1),   # the reference's outer product row
-    (17, 256, 1), (1, 300, 2), (100, 1024, 3), (33, 2000, 4), (64, 1028, 5), (129, 256, 16),
-    (3, 4097, 9),
+@pytest.mark.parametrize("M,N,K,auto", [
+    (4096, 4096, 1, True),   # the reference's outer product row: the cost model's pick
+    (4096, 4096, 4, True), (2048, 2048, 2, True),
+    # smaller outputs or larger K run the MFMA kernels unless forced
+    (17, 256, 1, False), (1, 300, 2, False), (100, 1024, 3, False), (33, 2000, 4, False),
+    (64, 1028, 5, False), (129, 256, 16, False), (3, 4097, 9, False), (2048, 2048, 16, False),
 ])
-def test_rank_k(dev, M, N, K):
+def test_rank_k(dev, M, N, K, auto):
     a = oracle.uniform((M, K), 700 + K)
     b = oracle.uniform((K, N), 800 + N)
-    c, cfg = gemm(g(a, dev), g(b, dev))
+    if auto:
+        c, cfg = gemm(g(a, dev), g(b, dev))
+    else:
+        with mt.forced_config(mt.FAMILY_SKINNY, 1, 1):
+            c, cfg = gemm(g(a, dev), g(b, dev))
     assert cfg.startswith("sk rankk "), cfg
     assert_close(c.cpu().numpy(), oracle.matmul(a, b), K, amax(a), amax(b), f"{M}x{N}x{K} rank-k")
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 2048, 4), (256, 8192, 1), (4096, 4096, 8), (512, 1024, 2)])
+def test_rank_k_left_to_mfma_where_slower(dev, M, N, K):
+    # measured faster on the MFMA kernels (K >= 8, or outputs under 2^22 /
+    # 2^24 elements at K <= 2 / K <= 4)
+    a = oracle.uniform((M, K), 710 + K)
+    b = oracle.uniform((K, N), 810 + N)
+    c, cfg = gemm(g(a, dev), g(b, dev))
+    assert not cfg.startswith("sk "), cfg
+    assert_close(c.cpu().numpy(), oracle.matmul(a, b), K, amax(a), amax(b), f"{M}x{N}x{K} mfma")
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 1), (2048, 2048, 2), (2050, 2048, 1)])
+def test_rank_k_column_bias(dev, M, N, K):
+    # the 16-byte fast path with a per-column bias (and a partial last row block)
+    a = oracle.uniform((M, K), 720 + K)
+    b = oracle.uniform((K, N), 820 + N)
+    bias = oracle.uniform((N,), 821)
+    c, cfg = gemm(g(a, dev), g(b, dev), bias=g(bias, dev), bias_axis=mt.BIAS_COL)
+    assert cfg.startswith("sk rankk "), cfg
+    assert_close(c.cpu().numpy(), oracle.matmul(a, b) + bias[None, :], K, amax(a), amax(b),
+                 f"{M}x{N}x{K} rank-k + column bias", extra=1e-6 * 4)
 
 
 def test_rank_k_views_bias_beta(dev):
@@ -106,8 +136,10 @@ def test_rank_k_views_bias_beta(dev):
     base = oracle.uniform((M + 2, N + 9), 14)
     C = g(base, dev)
     win = C[1:M + 1, 3:N + 3]
-    gemm(g(np.ascontiguousarray(a.T), dev).t(), g(np.ascontiguousarray(b.T), dev).t(), out=win,
-         bias=g(bias, dev), bias_axis=mt.BIAS_ROW, beta=1.0)
+    with mt.forced_config(mt.FAMILY_SKINNY, 1, 1):
+        _, cfg = gemm(g(np.ascontiguousarray(a.T), dev).t(), g(np.ascontiguousarray(b.T), dev).t(),
+                      out=win, bias=g(bias, dev), bias_axis=mt.BIAS_ROW, beta=1.0)
+    assert cfg.startswith("sk rankk "), cfg
     got = C.cpu().numpy()
     want = base.copy()
     want[1:M + 1, 3:N + 3] = oracle.matmul(a, b) + bias[:, None] + base[1:M + 1, 3:N + 3]
@@ -193,7 +225,8 @@ def test_special_values(dev):
     # rank-k: an outer product with a signed zero
     a1 = np.array([[-0.0], [2.0]], np.float32)
     b1 = np.full((1, 256), 3.0, np.float32)
-    c1, cfg = gemm(g(a1, dev), g(b1, dev))
+    with mt.forced_config(mt.FAMILY_SKINNY, 1, 1):
+        c1, cfg = gemm(g(a1, dev), g(b1, dev))
     assert cfg.startswith("sk rankk"), cfg
     np.testing.assert_array_equal(c1.cpu().numpy(), oracle.matmul(a1, b1))
     assert not np.any(np.signbit(c1.cpu().numpy()))
