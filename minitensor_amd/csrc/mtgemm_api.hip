@@ -1048,9 +1048,21 @@ int run_gemm(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C, int6
         p.rowsum = rows->out;
         p.rowsum_stride = rows->stride;
         p.rowsum_beta = rows->beta;
+        // A split-K plan cannot fuse them into the GEMM; its reduction launch
+        // sums them instead when A is a transposed contiguous matrix (the
+        // Linear dW = dYᵀ·X with dY [K][M]): the channel sums with K images of
+        // one position.  (A separate column sum had one workgroup per 64
+        // columns: 216 us for db of an 8192 x 512 dY.)
+        if (batch == 1 && p.a_mn == 1 && p.a_k == M && rows->stride == 1) {
+            p.csum_src = p.A;
+            p.csum = rows->out;
+            p.csum_n = (int)K;
+            p.csum_hw = 1;
+            p.csum_beta = rows->beta;
+        }
     }
     rc = launch_gemm(p, dl, la, lb, workspace, ws_bytes, stream);
-    if (rows) rows->done = rc == MT_OK && p.rowsum != nullptr;
+    if (rows) rows->done = rc == MT_OK && (p.rowsum != nullptr || p.csum != nullptr);
     return rc;
 }
 
@@ -1082,22 +1094,59 @@ size_t gemm_ws(const mt_mat_f32* A, const mt_mat_f32* B, const mt_mat_f32* C) {
 }
 
 // ---- column sums (Linear bias gradient) ------------------------------------
-// 64 columns per workgroup, 4 row groups summed in a fixed order.
+// A workgroup takes 64 columns as 16 groups of 4 (16-byte loads when the
+// columns are contiguous and aligned) and 16 row slices; slice g sums the
+// rows g, g+16, ... with four accumulators in flight (rows g + 16*(4i + u)
+// into accumulator u), then the accumulators and the slices are added in a
+// fixed order: deterministic.  (One load in flight per thread and 4 slices
+// had taken 216 us for an 8192 x 512 input.)
 __global__ void __launch_bounds__(256)
 colsum_f32(const float* X, int64_t rs, int64_t cs, int R, int Cn, float* out, int64_t os,
            float beta) {
-    __shared__ float part[4][64];
-    const int cl = threadIdx.x & 63, g = threadIdx.x >> 6;
-    const int c = blockIdx.x * 64 + cl;
-    float s = 0.f;
-    if (c < Cn)
-        for (int r = g; r < R; r += 4) s += X[(int64_t)r * rs + (int64_t)c * cs];
-    part[g][cl] = s;
+    __shared__ f32x4 part[16][16];
+    const int cq = threadIdx.x & 15, g = threadIdx.x >> 4;
+    const int c0 = blockIdx.x * 64 + 4 * cq;
+    const bool vec = cs == 1 && c0 + 3 < Cn && (rs & 3) == 0 && ((uintptr_t)(X + c0) & 15u) == 0;
+    auto row = [&](int r) {
+        const float* q = X + (int64_t)r * rs;
+        f32x4 x = {0.f, 0.f, 0.f, 0.f};
+        if (vec) {
+            x = *reinterpret_cast<const f32x4*>(q + c0);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (c0 + e < Cn) x[e] = q[(int64_t)(c0 + e) * cs];
+        }
+        return x;
+    };
+    f32x4 acc[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (c0 < Cn) {
+        int r = g;
+        for (; r + 48 < R; r += 64) {
+            f32x4 x[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) x[u] = row(r + 16 * u);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc[u] += x[u];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (r + 16 * u < R) acc[u] += row(r + 16 * u);
+    }
+    part[g][cq] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
     __syncthreads();
-    if (g == 0 && c < Cn) {
-        const float v = ((part[0][cl] + part[1][cl]) + part[2][cl]) + part[3][cl];
-        float* d = out + (int64_t)c * os;
-        *d = (beta != 0.f ? beta * *d : 0.f) + v;
+    if (g == 0 && c0 < Cn) {
+        f32x4 v = part[0][cq];
+#pragma unroll
+        for (int w = 1; w < 16; ++w) v += part[w][cq];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if (c0 + e >= Cn) break;
+            float* d = out + (int64_t)(c0 + e) * os;
+            *d = (beta != 0.f ? beta * *d : 0.f) + v[e];
+        }
     }
 }
 

@@ -100,7 +100,10 @@ def test_golden_matmul_vectors(dev):
 
 
 def test_colsum_shapes(dev):
-    for R, C in [(1, 1), (256, 1000), (1000, 3), (7, 130), (0, 5)]:
+    # tall inputs (row slices, four loads in flight), ragged column groups,
+    # a single row, an empty one
+    for R, C in [(1, 1), (256, 1000), (1000, 3), (7, 130), (0, 5), (8192, 512), (4099, 70),
+                 (63, 64), (65, 4)]:
         x = oracle.normal((R, C), R + C)
         got = sync_np(mt.colsum(g(x, dev)))
         assert_close(got, oracle.colsum(x) if R else np.zeros(C, np.float32), R, amax(x) if R else 0,
@@ -108,6 +111,32 @@ def test_colsum_shapes(dev):
     x = oracle.normal((64, 48), 1)
     X = g(x, dev).t()  # transposed view [48,64]
     assert_close(sync_np(mt.colsum(X)), oracle.colsum(x.T), 48, amax(x), 1.0, "colsum view")
+    # an unaligned column window (scalar loads) and beta
+    big = oracle.normal((300, 37), 2)
+    prev = oracle.normal((33,), 3)
+    out = g(prev, dev)
+    mt.colsum(g(big, dev)[:, 1:34], out=out, beta=0.5)
+    want = oracle.colsum(np.ascontiguousarray(big[:, 1:34])).astype(np.float64) + 0.5 * prev
+    assert_close(sync_np(out), want, 300, amax(big), 1.0, "colsum window + beta", extra=1e-6)
+
+
+@pytest.mark.parametrize("B,fi,fo", [(8192, 512, 512), (4096, 256, 384)])
+def test_linear_backward_db_in_split_k_reduction(dev, B, fi, fo):
+    # tall batches: dW = dYᵀ·X takes split-K, and db rides on its reduction
+    x = oracle.normal((B, fi), 31)
+    w = oracle.normal((fo, fi), 32)
+    dy = oracle.normal((B, fo), 33)
+    prev = oracle.normal((fo,), 34)
+    db = g(prev, dev)
+    dX, dW, db = mt.linear_backward(g(dy, dev), g(x, dev), g(w, dev), db=db, beta_b=1.0)
+    torch.cuda.synchronize()
+    print(f"[config] {mt.last_config()}", flush=True)
+    assert "split=1 " not in mt.last_config() + " ", mt.last_config()
+    assert_close(sync_np(dW), oracle.matmul(np.ascontiguousarray(dy.T), x), B, amax(dy), amax(x),
+                 "dW")
+    assert_close(sync_np(db), oracle.colsum(dy).astype(np.float64) + prev, B, amax(dy), 1.0, "db",
+                 extra=1e-6)
+    assert_close(sync_np(dX), oracle.matmul(dy, w), fo, amax(dy), amax(w), "dX")
 
 
 def seq(shape, start, step):
