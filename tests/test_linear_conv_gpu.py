@@ -215,6 +215,58 @@ def test_conv_backward_shapes(dev, n, c, h, wd, co, kh, kw, stride, pad):
     assert_close(db, wdb, n * ho * wo, amax(dy), 1.0, "conv db")
 
 
+@pytest.mark.parametrize("n,co,ho,wo,off", [
+    (32, 64, 112, 112, 0),   # the ResNet stem's dY (102 MB): 16-byte loads
+    (32, 64, 56, 56, 1),     # dY one float off 16-byte alignment: scalar loads
+    (5, 3, 7, 7, 0),         # odd positions per image: scalar loads
+    (1, 300, 1, 3, 0),       # fewer items than threads
+])
+def test_conv_bias_grad_shapes(dev, n, co, ho, wo, off):
+    """mt_conv2d_bwd_bias_f32 against the oracle's column sums of dY laid out
+    [(img, position)][channel], with beta = 0.5 into an existing gradient, and
+    bit-identical on a repeat."""
+    dy = oracle.normal((n, co, ho, wo), 21)
+    db0 = oracle.normal((co,), 22)
+    flat = torch.empty(dy.size + off, device=dev)
+    flat[off:] = g(dy.reshape(-1), dev)
+    d = mt.Conv2dDesc(n, 1, ho, wo, co, 1, 1, 1, 0)
+    outs = []
+    for _ in range(2):
+        dB = g(db0, dev)
+        assert mt.lib().mt_conv2d_bwd_bias_f32(ctypes.byref(d), flat[off:].data_ptr(),
+                                               dB.data_ptr(), 0.5, None) == 0
+        outs.append(sync_np(dB))
+    assert np.array_equal(outs[0], outs[1])
+    want = oracle.colsum(np.ascontiguousarray(dy.transpose(0, 2, 3, 1).reshape(-1, co)))
+    assert_close(outs[0], 0.5 * db0.astype(np.float64) + want, n * ho * wo, amax(dy), 1.0,
+                 "conv db", extra=1e-6)
+
+
+def test_conv_bias_grad_near_2_31_items(dev):
+    """2·(2^30 − 1) positions per channel, 17 GB of dY; the entry takes
+    n·h_out·w_out < 2^31, and this close to the limit the channel sum runs its
+    64-bit, image-by-image path.  Channel 0 holds 1, channel 1 holds 3, so the
+    sums are n·hw and three times that; each thread's share is an exact
+    integer in fp32 and only the final tree of 1024 partials rounds (relative
+    error below 2^-20)."""
+    n, hw = 2, (1 << 30) - 1
+    free, _ = torch.cuda.mem_get_info(dev)
+    if free < 20 << 30:
+        pytest.skip("needs 20 GB of free device memory")
+    dY = torch.empty(n, 2, hw, device=dev)
+    dY[:, 0].fill_(1.0)
+    dY[:, 1].fill_(3.0)
+    d = mt.Conv2dDesc(n, 1, 1, hw, 2, 1, 1, 1, 0)
+    dB = torch.tensor([5.0, 7.0], device=dev)
+    assert mt.lib().mt_conv2d_bwd_bias_f32(ctypes.byref(d), dY.data_ptr(), dB.data_ptr(), 0.5,
+                                           None) == 0
+    got = sync_np(dB).astype(np.float64)
+    want = np.array([2.5 + n * hw, 3.5 + 3.0 * n * hw])
+    del dY
+    torch.cuda.empty_cache()
+    assert np.all(np.abs(got - want) <= want * 2.0 ** -20), (got, want)
+
+
 @pytest.mark.parametrize("n,c,h,wd,co,stride,pad", [
     (4, 16, 10, 10, 24, 1, 1),    # implicit weight path (split-K: db in its reduction)
     (3, 8, 9, 11, 40, 2, 1),      # implicit, stride 2
