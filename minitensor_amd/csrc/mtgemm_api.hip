@@ -238,6 +238,14 @@ struct CostModel {
     double launch_cycles = 17700.0;          // second (reduce) launch
 };
 constexpr int kMaxSplits = 256;
+// The cost model was fitted on splits 1-16.  Beyond 16, a split must keep at
+// least kMinKpsBeyondFit of K: on random GEMMs (K <= 4700) the model's picks
+// of 19-59 splits at 64-208 per split ran 2-12 % slower than 16 splits (it
+// misses a per-workgroup cost of short K ranges), while the weight gradients
+// of 64- and 128-channel convolutions (K = n*h_out*w_out = 25088-401408,
+// 496-2368 per split) ran 1.2-3.4x faster than at 16.
+constexpr int kFittedSplits = 16;
+constexpr int kMinKpsBeyondFit = 256;
 constexpr int kDlpSmallCfg = 5;          // the 64x64 prefetching configuration
 constexpr int kDlSmallCfg = 2;           // the 64x64 direct-to-LDS configuration
 constexpr double kCoresidentPair = 0.75;
@@ -319,6 +327,7 @@ Plan make_plan_uncached(int64_t M, int64_t N, int64_t K, int64_t batch, int cus,
             if (s > 1 && !allow_split) break;
             const Plan pl = cfg_plan(cc, cfg, dl, M, N, K, batch, s);
             if (s > 1 && pl.kps < 64) break;
+            if (s > kFittedSplits && pl.kps < kMinKpsBeyondFit) break;
             const int64_t k6 = std::min<int64_t>(pl.kps, K);
             if (dl && cfg == 6 && k6 < kDlp6MinKOneRound) break;
             if (pl.splits != s) continue;
