@@ -242,6 +242,32 @@ def test_conv_bias_grad_shapes(dev, n, co, ho, wo, off):
                  "conv db", extra=1e-6)
 
 
+@pytest.mark.parametrize("n,c,hw,co,k,stride,pad", [
+    (16, 8, 56, 16, 3, 1, 1),    # one output tile, K = 50176: implicit path, split-K reduction + db
+    (16, 3, 112, 16, 7, 2, 3),   # c_in = 3: column-buffer path, db on its own
+])
+def test_conv_dw_many_splits(dev, n, c, hw, co, k, stride, pad):
+    """Weight gradients with one or two output tiles and a long K = n·h_out·w_out
+    take more than 16 splits (the workgroups would not fill the chip with 16);
+    dW and db against the oracle, bit-identical on a repeat."""
+    x = oracle.normal((n, c, hw, hw), 41)
+    w = oracle.normal((co, c, k, k), 42)
+    ho = oracle.conv_out(hw, pad, k, stride)
+    dy = oracle.normal((n, co, ho, ho), 43)
+    X, W, dY = g(x, dev), g(w, dev), g(dy, dev)
+    outs = []
+    for _ in range(2):
+        _, dw, db = mt.conv2d_backward(X, W, dY, stride, pad, need_dx=False)
+        outs.append((sync_np(dw), sync_np(db)))
+    cfg = mt.last_config()
+    print(f"[config] {cfg}", flush=True)
+    assert int(cfg.split("split=")[1].split()[0]) > 16, cfg
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+    _, wdw, wdb = oracle.conv2d_backward(x, w, dy, stride, pad)
+    assert_close(outs[0][0], wdw, n * ho * ho, amax(dy), amax(x), "dW")
+    assert_close(outs[0][1], wdb, n * ho * ho, amax(dy), 1.0, "db")
+
+
 def test_conv_bias_grad_near_2_31_items(dev):
     """2·(2^30 − 1) positions per channel, 17 GB of dY; the entry takes
     n·h_out·w_out < 2^31, and this close to the limit the channel sum runs its
