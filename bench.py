@@ -77,7 +77,9 @@ def parse():
                         "shapes (sizes 64-4700, seeded) and print one line per shape and a summary")
     p.add_argument("--only", default="",
                    help="comma list of secondary configs (c1,c3,c4,c5a,c5b,skinny), 'resnet' "
-                        "(twelve ResNet-like conv layers, not in the default run) and/or "
+                        "(twelve ResNet-like conv layers, not in the default run), "
+                        "'resnet_bwd' (their backward, two downsampling layers and the "
+                        "stem) and/or "
                         "'sustained' (the headline GEMM back to back for 2.5 s): run just those "
                         "and print their JSON, without the headline and CPU legs "
                         "(per-workload profiles)")
@@ -204,11 +206,15 @@ SECONDARY = ("c1", "c3", "c4", "c5a", "c5b", "skinny")
 # Not in the default run (--only resnet): twelve ResNet-like convolution
 # layers at batch 32, 3x3 and 1x1, 7x7 to 56x56 -- where the 64x112
 # convolution tile on 16x16 MFMA blocks is or is not taken.
-EXTRA = ("resnet",)
+EXTRA = ("resnet", "resnet_bwd")
 RESNET_LAYERS = [(56, 64, 64, 3), (56, 64, 256, 1), (56, 256, 64, 1),
                  (28, 128, 128, 3), (28, 128, 512, 1), (28, 512, 128, 1),
                  (14, 256, 256, 3), (14, 256, 1024, 1), (14, 1024, 256, 1),
                  (7, 512, 512, 3), (7, 512, 2048, 1), (7, 2048, 512, 1)]
+# --only resnet_bwd: the backward (dX; dW + db in one call) of the same twelve
+# layers, two downsampling layers and the 7x7 stem: (hw, c_in, c_out, k, stride, pad)
+RESNET_BWD_LAYERS = [(hw, c, co, k, 1, k // 2) for hw, c, co, k in RESNET_LAYERS] + [
+    (56, 128, 128, 3, 2, 1), (56, 256, 512, 1, 2, 0), (224, 3, 64, 7, 2, 3)]
 SUSTAINED_S = 2.5
 
 
@@ -448,6 +454,24 @@ def secondary(dev, only=SECONDARY) -> dict:
             ms = both(lambda: mt.conv2d(x, w, cb, 1, k // 2, ws=cws), 50, 5)
             rec(f"resnet_conv{k}x{k}_{hw}x{hw}_{c}to{co}", ms, 2 * 32 * hw * hw * co * c * k * k,
                 4 * (x.numel() + w.numel() + co + 32 * co * hw * hw), mt.last_config())
+
+    if "resnet_bwd" in only:  # batch 32; dX and dW + db of each layer
+        for hw, c, co, k, st, pd in RESNET_BWD_LAYERS:
+            ho = (hw + 2 * pd - k) // st + 1
+            x = n(32, c, hw, hw)
+            w = n(co, c, k, k, std=(2.0 / (c * k * k)) ** 0.5)
+            dy = n(32, co, ho, ho, std=0.01)
+            d = mt.Conv2dDesc(32, c, hw, hw, co, k, k, st, pd)
+            bws = mt.workspace(mt.lib().mt_conv2d_bwd_workspace_f32(ctypes.byref(d)), dev)
+            dwb = torch.empty_like(w)
+            f = 2 * 32 * ho * ho * co * c * k * k
+            tag = f"resnet_bwd_conv{k}x{k}s{st}_{hw}x{hw}_{c}to{co}"
+            ms = both(lambda: mt.conv2d_backward(x, w, dy, st, pd, need_dw=False, need_db=False,
+                                                 ws=bws), 50, 5)
+            rec(f"{tag}_dx", ms, f, None, mt.last_config())
+            ms = both(lambda: mt.conv2d_backward(x, w, dy, st, pd, need_dx=False, ws=bws,
+                                                 dw=dwb), 50, 5)
+            rec(f"{tag}_dw_db", ms, f, None, mt.last_config())
 
     if "skinny" in only:
         # The reference's HBM-bound matmul rows (test/benchmark.cpp:732,737-738,

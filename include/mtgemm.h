@@ -155,13 +155,19 @@ typedef struct mt_conv2d_desc {
     int64_t stride, pad;
 } mt_conv2d_desc;
 
+/* A 1x1 kernel with stride 1 and no padding, c_in and h*w multiples of 4:
+ * one product per image, Y_b[c_out][h*w] = W · X_b[c_in][h*w], over the NCHW
+ * tensors themselves. */
 int mt_conv2d_fwd_f32(const mt_conv2d_desc* d, const float* input, const float* weight,
                       const float* bias, float* output, void* workspace, size_t ws_bytes,
                       void* stream);
 size_t mt_conv2d_workspace_f32(const mt_conv2d_desc* d);
 /* Same, for an input given as any NCHW view: in_strides = element strides of
  * (n, c, h, w), e.g. a channel slice or an NHWC-stored tensor, read in place
- * (weight and output stay dense).  Replaces conv2d_gpu_strided +
+ * (weight and output stay dense).  The 1x1 product above takes views whose
+ * (h, w) fold into one index (in_strides[2] == w * in_strides[3]); other
+ * views of such a layer take the NCHW-view kernel, and the workspace query
+ * covers both.  Replaces conv2d_gpu_strided +
  * conv2d_forward_kernel_strided (reference src/gpu_ops.cpp:2328-2399;
  * declared include/TensorOps.hpp:709), which conv2d() takes for
  * non-contiguous operands (include/TensorOps.hpp:1088-1097). */
@@ -170,7 +176,11 @@ int mt_conv2d_fwd_strided_f32(const mt_conv2d_desc* d, const float* input,
                               const float* bias, float* output, void* workspace,
                               size_t ws_bytes, void* stream);
 
-/* Conv2D backward as GEMMs (dense NCHW tensors, same descriptor as forward):
+/* Conv2D backward as GEMMs (dense NCHW tensors, same descriptor as forward).
+ * 1x1, stride 1, no padding, c_in and h_out*w_out multiples of 4: dX_b =
+ * Wᵀ · dY_b per image, and dW = Σ_b dY_b · X_bᵀ as per-image partial
+ * products in the workspace, summed (with beta·dW, and db as the channel
+ * sums of dY) by the split-K reduction launch.  Other geometries:
  *   weight: dW[c_out, c_in*kh*kw] = dY[c_out, n*h_out*w_out] · colᵀ (+ beta·dW);
  *           when c_in % 4 == 0 and n*h_out*w_out % 4 == 0, colᵀ is gathered by
  *           the kernel from a channels-last copy of the input (no column

@@ -151,6 +151,9 @@ struct GemmParams {
     int splits, k_per_split;                  // k_per_split is a multiple of BK
     int c_vec;    // C takes 16-byte stores of 4 consecutive columns (c_n == 1, aligned)
     int ws_vec;   // the split-K workspace takes 16-byte stores (N % 4 == 0, aligned)
+    // Raw partials into ws even with one split: a batch-summed product
+    // C = sum_b A_b·B_b, whose reduction launch sums all splits x batch slabs.
+    int part;
     ConvGeom cv;  // B = implicit im2col of the input at B (layout L_IM only)
     // Optional fused row sums of A (direct-to-LDS kernel, splits == 1 only):
     // rowsum[m*rowsum_stride] = rowsum_beta*rowsum[...] + sum_k A(m, k).  In
@@ -453,7 +456,7 @@ __device__ __forceinline__ void store_tile_lds(const GemmParams& p, const f32x16
     constexpr int U = 4;
     const int t = threadIdx.x;
     const int h = lane >> 5, c = lane & 31;
-    const bool part = p.splits > 1;
+    const bool part = p.splits > 1 || p.part;
     float* const base = part ? p.ws + ((int64_t)split * p.batch + bz) * (int64_t)p.M * p.N
                              : p.C + (int64_t)bz * p.c_b;
     const int64_t rs = part ? (int64_t)p.N : p.c_m;

@@ -95,7 +95,7 @@ template <int BM, int BN, int W, int NT = 64 * W>
 __device__ __forceinline__ void ksw_store(const GemmParams& p, const TileId& id,
                                           const float* red, int m0, int n0) {
     constexpr int PITCH = BN + 4;
-    const bool part = p.splits > 1;
+    const bool part = p.splits > 1 || p.part;
     float* const base = part ? p.ws + ((int64_t)id.split * p.batch + id.bz) * (int64_t)p.M * p.N
                              : p.C + (int64_t)id.bz * p.c_b;
     const int64_t rs = part ? (int64_t)p.N : p.c_m;

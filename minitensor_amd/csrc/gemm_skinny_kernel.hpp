@@ -122,7 +122,7 @@ __global__ void __launch_bounds__(64 * gemv_mv_waves<MR>()) gemv_mv_f32(GemmPara
 #pragma unroll
     for (int m = 0; m < MR; ++m) red[(wave * MR + m) * 64 + lane] = acc[m];
     __syncthreads();
-    const bool part = p.splits > 1;
+    const bool part = p.splits > 1 || p.part;
     float* const base = part ? p.ws + ((int64_t)split * p.batch + bz) * (int64_t)p.M * p.N
                              : p.C + (int64_t)bz * p.c_b;
     const int64_t rs = part ? (int64_t)p.N : p.c_m;
@@ -205,7 +205,7 @@ __global__ void __launch_bounds__(256) gemv_kv_f32(GemmParams p) {
         for (int x = 8; x >= 1; x >>= 1) s[m] += __shfl_xor(s[m], x, 16);
     }
     if (gl != 0 || n >= p.N) return;
-    const bool part = p.splits > 1;
+    const bool part = p.splits > 1 || p.part;
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
         if (m >= p.M) break;

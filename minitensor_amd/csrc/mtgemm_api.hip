@@ -272,6 +272,12 @@ Plan cfg_plan(const CfgCost& cc, int cfg, bool dl, int64_t M, int64_t N, int64_t
     return pl;
 }
 
+// Workspace of a batch-summed launch (GemmParams::part): one M x N slab per
+// split and batch entry, one split included.
+size_t part_ws_bytes(const Plan& pl, int64_t M, int64_t N, int64_t batch) {
+    return (size_t)std::max(pl.splits, 1) * batch * M * N * sizeof(float);
+}
+
 // Modelled cycles of one plan (see CostModel).
 double plan_cycles(const CostModel& cm, const CfgCost& cc, const Plan& pl, int64_t M, int64_t N,
                    int64_t batch, int cus) {
@@ -996,7 +1002,8 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
     // and computes them separately).
     if (batch != 1 || la != L_MV || lb != L_MV) p.rowsum = nullptr;
     // The HBM-bound shapes (few rows or columns, or K <= 16) on the vector ALUs.
-    if (!implicit && la != L_KVI && p.rowsum == nullptr && p.csum == nullptr) {
+    if (p.part) p.rowsum = nullptr;
+    if (!implicit && la != L_KVI && p.rowsum == nullptr && p.csum == nullptr && !p.part) {
         const SkinnyPlan sp =
             skinny_plan(M, N, K, batch, la, lb, p.c_n_inner < N, device_cu_count());
         if (sp.kind != SK_NONE) return launch_skinny(p, sp, workspace, ws_bytes, stream);
@@ -1008,8 +1015,13 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
     Plan plan;
     const bool im16_ok = dl && lb == L_IM;
     const bool forced = forced_plan(M, N, K, batch, dl, !implicit, wide_ok, &plan, im16_ok);
+    // workspace a plan writes: split-K partials, or with p.part a slab per
+    // split and batch entry even at one split
+    auto need = [&](const Plan& pl) {
+        return p.part ? part_ws_bytes(pl, M, N, batch) : pl.splits > 1 ? pl.ws_bytes : 0;
+    };
     if (forced) {
-        if (plan.splits > 1 && (workspace == nullptr || ws_bytes < plan.ws_bytes))
+        if (need(plan) > 0 && (workspace == nullptr || ws_bytes < need(plan)))
             return MT_ERR_WORKSPACE;
     } else {
         // the wave-split kernel takes every operand form but the implicit
@@ -1017,9 +1029,11 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
         const bool ksw_ok = !implicit && p.rowsum == nullptr;
         plan = make_plan(M, N, K, batch, device_cu_count(), true, dl, wide_ok, ksw_ok,
                          lb == L_IMW, im16_ok && kOfferDl16);
-        if (plan.splits > 1 && (workspace == nullptr || ws_bytes < plan.ws_bytes))
+        if (need(plan) > 0 && (workspace == nullptr || ws_bytes < need(plan)))
             plan = make_plan(M, N, K, batch, device_cu_count(), false, dl, wide_ok, ksw_ok,
                              lb == L_IMW, im16_ok && kOfferDl16);
+        if (need(plan) > 0 && (workspace == nullptr || ws_bytes < need(plan)))
+            return MT_ERR_WORKSPACE;
     }
     if (!plan.dl || plan.splits > 1) p.rowsum = nullptr;
     p.splits = plan.splits;
@@ -1027,10 +1041,12 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
     p.tiles_m = plan.tiles_m;
     p.tiles_n = plan.tiles_n;
     p.group_m = 4;
-    p.ws = plan.splits > 1 ? static_cast<float*>(workspace) : nullptr;
+    const bool reduce = plan.splits > 1 || p.part;
+    p.ws = reduce ? static_cast<float*>(workspace) : nullptr;
     p.ws_vec = p.ws != nullptr && ((uintptr_t)p.ws & 15u) == 0 && (N & 3) == 0;
-    // Channel sums ride on the vector reduction only (one row per workgroup row)
-    if (!p.ws_vec || batch != 1) p.csum = nullptr;
+    // Channel sums ride on the vector reduction only (one row per workgroup
+    // row; a batch-summed product reduces to a single matrix)
+    if (!p.ws_vec || (batch != 1 && !p.part)) p.csum = nullptr;
 
     const int64_t nblocks = (int64_t)plan.tiles_m * plan.tiles_n * plan.splits * batch;
     if (nblocks >= ((int64_t)1 << 31)) return MT_ERR_UNSUPPORTED;
@@ -1040,10 +1056,10 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
                       halo_fits(p.cv, (int)(N / ((int64_t)p.cv.ho * p.cv.wo)), plan.cfg,
                                 p.k_per_split, !forced);
     std::snprintf(g_last_config, sizeof g_last_config,
-                  "%s %dx%d a=%s b=%s split=%d wgs=%lld cfg=%d",
+                  "%s %dx%d a=%s b=%s split=%d wgs=%lld cfg=%d%s",
                   plan.ksw ? "ksw" : plan.dl ? "dl" : "rs", plan.bm,
                   plan.bn, layout_name(la), layout_name(halo ? L_IMH : lb), plan.splits,
-                  (long long)nblocks, plan.cfg);
+                  (long long)nblocks, plan.cfg, p.part ? " batch-summed" : "");
 
     GemmLaunchFn fn = halo ? convh_launcher(plan.cfg)
                       : lb == L_IM || lb == L_IMR ? conv_launcher(plan.cfg, lb == L_IMR)
@@ -1054,22 +1070,29 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
     hipError_t e = fn(p, (unsigned)nblocks, stream);
     if (e == hipErrorStreamCaptureUnsupported) e = hipSuccess;
     if (e != hipSuccess) return MT_ERR_HIP;
-    if (plan.splits > 1) {
-        if (p.ws_vec) {
-            const int nt = p.csum ? csum_threads((int64_t)p.csum_n * p.csum_hw) : 256;
+    if (reduce) {
+        // A batch-summed product reduces splits x batch slabs into one C.
+        GemmParams q = p;
+        if (p.part) {
+            q.splits = plan.splits * (int)batch;
+            q.batch = 1;
+            q.c_b = 0;
+        }
+        if (q.ws_vec) {
+            const int nt = q.csum ? csum_threads((int64_t)q.csum_n * q.csum_hw) : 256;
             const dim3 grid((unsigned)std::min<int64_t>((N / 4 + nt - 1) / nt, 64),
-                            (unsigned)std::min<int64_t>(M * batch, 65535));
-            if (p.csum && nt == 1024)
+                            (unsigned)std::min<int64_t>(M * q.batch, 65535));
+            if (q.csum && nt == 1024)
                 hipLaunchKernelGGL((splitk_reduce_vec_f32<true, 1024>), grid, dim3(nt), 0, stream,
-                                   p);
-            else if (p.csum)
-                hipLaunchKernelGGL(splitk_reduce_vec_f32<true>, grid, dim3(nt), 0, stream, p);
+                                   q);
+            else if (q.csum)
+                hipLaunchKernelGGL(splitk_reduce_vec_f32<true>, grid, dim3(nt), 0, stream, q);
             else
-                hipLaunchKernelGGL(splitk_reduce_vec_f32<false>, grid, dim3(nt), 0, stream, p);
+                hipLaunchKernelGGL(splitk_reduce_vec_f32<false>, grid, dim3(nt), 0, stream, q);
         } else {
-            const int64_t total = M * N * batch;
+            const int64_t total = M * N * q.batch;
             const int64_t blocks = std::min<int64_t>((total + 255) / 256, 65536);
-            hipLaunchKernelGGL(splitk_reduce_f32, dim3((unsigned)blocks), dim3(256), 0, stream, p);
+            hipLaunchKernelGGL(splitk_reduce_f32, dim3((unsigned)blocks), dim3(256), 0, stream, q);
         }
         if (capture_safe_last_error() != hipSuccess) return MT_ERR_HIP;
     }
@@ -1697,6 +1720,33 @@ int run_conv_implicit(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, const flo
 // Its window test adds a tap to the window origin in 32-bit arithmetic, so
 // the padded extents stay below 2^30 (a tap never exceeds them when an
 // output exists).
+// 1x1 kernel, stride 1, no padding, c_in and the positions per image
+// multiples of 4: the convolution is one product per image over the NCHW
+// tensors themselves (Y_b = W·X_b, dX_b = Wᵀ·dY_b, dW = Σ_b dY_b·X_bᵀ), with
+// no layout copy and no scattered output.  Against the channels-last implicit
+// path (which transposes the input or dY first), graph-timed at batch 32:
+// 56x56 256->64 forward 38.1 against 74.3 us, dX 41.0 against 62.2, dW +
+// db about 37 against 92.4.
+bool pointwise(const mt_conv2d_desc* d) {
+    return d->kh == 1 && d->kw == 1 && d->stride == 1 && d->pad == 0 && d->c_in > 0 &&
+           (d->c_in & 3) == 0 && ((d->h * d->w) & 3) == 0 && d->h * d->w < kMaxDim;
+}
+
+// Workspace of a batch-summed product (GemmParams::part) under any plan the
+// launcher can take for it.
+size_t part_plan_ws(int64_t M, int64_t N, int64_t K, int64_t batch, int cus) {
+    size_t ws = 0;
+    for (bool dl : {false, true})
+        for (bool wide : {false, true})
+            for (bool ksw : {false, true})
+                ws = std::max(ws, part_ws_bytes(make_plan(M, N, K, batch, cus, true, dl, wide, ksw),
+                                                M, N, batch));
+    Plan forced;
+    if (forced_plan(M, N, K, batch, true, true, true, &forced))
+        ws = std::max(ws, part_ws_bytes(forced, M, N, batch));
+    return align_up(ws, 256);
+}
+
 bool nchw_implicit(const mt_conv2d_desc* d) {
     const int64_t kg = d->c_in * d->kh * d->kw;
     constexpr int64_t kWin = (int64_t)1 << 30;
@@ -1936,6 +1986,7 @@ size_t dx_ws(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo) {
     const int64_t kg = d->c_in * d->kh * d->kw, np = d->n * Ho * Wo;
     if (np == 0 || d->c_out == 0 || d->n * d->c_in * d->h * d->w == 0) return 0;
     const int64_t nx = d->n * d->h * d->w, kx = d->c_out * d->kh * d->kw;
+    if (pointwise(d)) return plan_ws(d->c_in, d->h * d->w, d->c_out, d->n, device_cu_count());
     mt_conv2d_desc t;
     if (dx_as_forward(d, Ho, Wo, &t) && implicit_geometry(&t)) {
         const ImplicitWs iw = implicit_ws(&t);
@@ -1965,6 +2016,7 @@ bool dw_reads_dy_nchw(int64_t np, int64_t hw) {
 size_t dw_ws(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo) {
     const int64_t kg = d->c_in * d->kh * d->kw, np = d->n * Ho * Wo;
     if (np == 0 || d->c_out == 0 || kg == 0) return 0;
+    if (pointwise(d)) return part_plan_ws(d->c_out, d->c_in, Ho * Wo, d->n, device_cu_count());
     const size_t dyt_b = align_up((size_t)d->c_out * np * sizeof(float), 256);
     if (implicit_dw(d, np)) {
         const size_t xt_b = align_up((size_t)d->n * d->c_in * d->h * d->w * sizeof(float), 256);
@@ -2138,6 +2190,11 @@ size_t mt_conv2d_workspace_f32(const mt_conv2d_desc* d) {
     if (!conv_dims(d, &Ho, &Wo)) return 0;
     const int64_t kg = d->c_in * d->kh * d->kw, np = d->n * Ho * Wo;
     if (np == 0 || d->c_out == 0) return 0;
+    // one product per image; a strided input whose (h, w) do not fold into one
+    // index takes the NCHW-view kernel instead
+    if (pointwise(d))
+        return std::max(plan_ws(d->c_out, d->h * d->w, d->c_in, d->n, device_cu_count()),
+                        nchw_weight_ws(d) + implicit_gemm_ws(d->c_out, np, kg, false));
     if (implicit_geometry(d) && d->h * d->w < kMaxDim) {   // channels-last kernel
         const ImplicitWs iw = implicit_ws(d);
         return iw.xt + iw.wt + implicit_gemm_ws(d->c_out, np, kg, false);
@@ -2161,12 +2218,24 @@ int mt_conv2d_fwd_strided_f32(const mt_conv2d_desc* d, const float* input,
     if (!output || (kg > 0 && (!input || !weight))) return MT_ERR_INVALID;
     hipStream_t s = static_cast<hipStream_t>(stream);
 
+    // 1x1, stride 1, no padding: Y_b[c_out][hw] = W[c_out][c_in] · X_b[c_in][hw]
+    // for each image b, over the input view itself when its (h, w) fold into
+    // one position index (NCHW, NHWC, channel slices).
+    if (pointwise(d) && (d->h == 1 || in_strides[2] == d->w * in_strides[3])) {
+        const mt_mat_f32 A{weight, 0, d->c_out, d->c_in, d->c_in, 1, d->n, 0};
+        const mt_mat_f32 B{input, 0, d->c_in, hw, in_strides[1], in_strides[3], d->n,
+                           in_strides[0]};
+        const mt_mat_f32 C{output, 0, d->c_out, hw, hw, 1, d->n, d->c_out * hw};
+        const mt_epilogue_f32 ep{bias, 1, bias ? MT_BIAS_ROW : MT_BIAS_NONE, 0.f};
+        return run_gemm(&A, &B, &C, 0, 0, &ep, workspace, ws_bytes, s);
+    }
+
     // c_in % 16 == 0: the channels-last kernel (16-byte DMA gathers) on a
     // channels-last copy of the input (the input itself when it is one) and
     // OHWI weights.  Its 16-byte gathers beat the NCHW-view kernels (4-byte
     // gathers or halo patches) by more than the layout launch costs
     // (benchmark layer, forward: 79.5 us against 84.5 with halo patches).
-    if (implicit_geometry(d) && d->h * d->w < kMaxDim) {
+    if (implicit_geometry(d) && d->h * d->w < kMaxDim && !pointwise(d)) {
         const ImplicitWs iw = implicit_ws(d);
         if (!workspace || ws_bytes < iw.xt + iw.wt || ((uintptr_t)workspace & 15u) != 0)
             return MT_ERR_WORKSPACE;
@@ -2244,6 +2313,30 @@ int conv_bwd_weight(const mt_conv2d_desc* d, const float* input, const float* gr
     const size_t col_b = align_up((size_t)kg * np * sizeof(float), 256);
     const size_t dyt_b = align_up((size_t)d->c_out * np * sizeof(float), 256);
     if (np > 0 && (!input || !grad_out)) return MT_ERR_INVALID;
+    if (pointwise(d) && np > 0) {
+        // dW[c_out][c_in] = Σ_b dY_b[c_out][hw] · X_b[c_in][hw]ᵀ: one product per
+        // image into the workspace, summed (with beta·dW, and db as the channel
+        // sums of dY) by the reduction launch.
+        GemmParams p{};
+        p.A = grad_out; p.a_mn = hw; p.a_k = 1; p.a_b = d->c_out * hw;
+        p.B = input; p.b_mn = hw; p.b_k = 1; p.b_b = d->c_in * hw;
+        p.C = grad_weight; p.c_m = d->c_in; p.c_n = 1; p.c_b = 0;
+        p.c_n_inner = d->c_in; p.c_n_outer = 0;
+        p.bias = nullptr; p.bias_stride = 0; p.bias_axis = MT_BIAS_NONE;
+        p.beta = beta;
+        p.M = (int)d->c_out; p.N = (int)d->c_in; p.K = (int)hw; p.batch = (int)d->n;
+        p.part = 1;
+        if (grad_bias) {
+            p.csum_src = grad_out; p.csum = grad_bias; p.csum_n = (int)d->n;
+            p.csum_hw = hw; p.csum_beta = beta_b;
+        }
+        const int la = classify(p.A, p.a_mn, p.a_k, p.M, p.K, p.a_b, p.batch > 1);
+        const int lb = classify(p.B, p.b_mn, p.b_k, p.N, p.K, p.b_b, p.batch > 1);
+        const bool dl = (la == L_KV || la == L_MV) && (lb == L_KV || lb == L_MV);
+        const int rc = launch_gemm(p, dl, la, lb, workspace, ws_bytes, s);
+        *db_done = rc == MT_OK && p.csum != nullptr;
+        return rc;
+    }
     if (implicit_dw(d, np)) {
         // Implicit GEMM dW[c_out, (r,s,ci)] = dYt[c_out, np] · im2colᵀ(xt)[np, (r,s,ci)],
         // the B operand gathered from a channels-last copy of the input and the
@@ -2357,6 +2450,12 @@ int mt_conv2d_bwd_input_f32(const mt_conv2d_desc* d, const float* grad_out, cons
         return capture_safe_last_error() == hipSuccess ? MT_OK : MT_ERR_HIP;
     }
     if (!grad_out || !weight) return MT_ERR_INVALID;
+    if (pointwise(d)) {   // dX_b[c_in][hw] = Wᵀ[c_in][c_out] · dY_b[c_out][hw]
+        const mt_mat_f32 A{weight, 0, d->c_in, d->c_out, 1, d->c_in, d->n, 0};
+        const mt_mat_f32 B{grad_out, 0, d->c_out, hw, hw, 1, d->n, d->c_out * hw};
+        const mt_mat_f32 C{grad_input, 0, d->c_in, hw, hw, 1, d->n, d->c_in * hw};
+        return run_gemm(&A, &B, &C, 0, 0, nullptr, workspace, ws_bytes, s);
+    }
     mt_conv2d_desc t;
     if (dx_as_forward(d, Ho, Wo, &t) && implicit_geometry(&t)) {
         // Channels-last implicit GEMM of dY with the weights transposed to

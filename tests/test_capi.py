@@ -231,6 +231,22 @@ def test_conv_backward_workspace_is_the_paths_need():
     assert xt < need < col, need
 
 
+def test_pointwise_conv_workspace():
+    """1x1, stride 1, n 2, 32 -> 64 channels, 8x8 (K = 64 positions or fewer
+    channels: no plan splits K).  Backward: dW's per-image partial products,
+    2 x 64 x 32 floats (16384 B); dX needs nothing.  Forward: the batched
+    product needs nothing, the NCHW-view kernel (which takes views whose
+    (h, w) do not fold) room for an aligned weight copy, 64 x 32 floats."""
+    import ctypes
+    lib = mt.lib()
+    d = mt.Conv2dDesc(2, 32, 8, 8, 64, 1, 1, 1, 0)
+    assert lib.mt_conv2d_bwd_workspace_f32(ctypes.byref(d)) == 16384
+    assert lib.mt_conv2d_workspace_f32(ctypes.byref(d)) == 8192
+    # 7x7 positions (not a multiple of 4): the channels-last path and its copies
+    d = mt.Conv2dDesc(2, 32, 7, 7, 64, 1, 1, 1, 0)
+    assert lib.mt_conv2d_workspace_f32(ctypes.byref(d)) >= 2 * 32 * 49 * 4
+
+
 def test_build_refuses_kernels_with_scratch():
     """The build raises on a kernel whose resource remark reports scratch
     (spilled registers): parse of hipcc's -Rpass-analysis=kernel-resource-usage

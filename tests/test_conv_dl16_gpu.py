@@ -31,7 +31,7 @@ SHAPES = [
     (1, 16, 17, 17, 48, 5, 2, 2),     # 48 output channels: a partial tile row
     (3, 64, 7, 7, 80, 1, 1, 0),       # 1x1, 147 pixels
     (2, 16, 9, 11, 40, 3, 1, 1),      # K = 144: 9 chunks (odd)
-    (4, 16, 6, 6, 64, 1, 1, 0),       # K = 16: one chunk, other groups idle
+    (4, 16, 5, 5, 64, 1, 1, 0),       # K = 16: one chunk, other groups idle
     (1, 128, 8, 8, 96, 3, 2, 1),      # K = 1152, stride 2
 ]
 
@@ -246,11 +246,11 @@ def test_random_forced(dev, case):
 
 
 def test_output_beyond_2pow31_elements(dev):
-    """1x1, 16 -> 8320 channels, batch 64, 64x64: 2.18e9 output elements
-    (8.7 GB); image 63 starts past 2^31, so a 32-bit index anywhere in the
-    loaders or the scattered NCHW store would alias.  Sampled channels of the
-    first and last images against the oracle."""
-    n, c, hw, co = 64, 16, 64, 8320
+    """1x1, 16 -> 8320 channels, batch 64, 65x65: 2.25e9 output elements
+    (9.0 GB); images 62 and 63 start past 2^31, so a 32-bit index anywhere in
+    the loaders or the scattered NCHW store would alias.  Sampled channels of
+    the first and last images against the oracle."""
+    n, c, hw, co = 64, 16, 65, 8320
     x = oracle.normal((n, c, hw, hw), 95)
     w = oracle.normal((co, c, 1, 1), 96)
     b = oracle.normal((co,), 97)

@@ -383,12 +383,12 @@ def test_config5a_conv_backward_adjoint(dev):
 # and split-K are covered.  Other channel counts take the explicit im2col path.
 
 @pytest.mark.parametrize("n,c,h,wd,co,kh,kw,stride,pad", [
-    (2, 16, 8, 8, 32, 1, 1, 1, 0),     # 1x1
+    (2, 16, 7, 7, 32, 1, 1, 1, 0),     # 1x1 (49 positions; a multiple of 4 takes the per-image product)
     (2, 16, 9, 7, 6, 3, 3, 1, 1),
     (3, 32, 11, 10, 6, 3, 2, 2, 2),    # 3x2 kernel, stride 2, pad 2
     (1, 16, 17, 13, 8, 5, 5, 3, 1),    # 5x5, stride 3
     (2, 16, 5, 5, 4, 7, 7, 1, 3),      # 7x7 on a 5x5 image: mostly padding
-    (1, 48, 6, 6, 5, 1, 1, 1, 0),      # three chunks per tap
+    (1, 48, 5, 7, 5, 1, 1, 1, 0),      # three chunks per tap
     (1, 512, 7, 7, 64, 3, 3, 1, 1),    # kg = 4608, np = 49: split-K, scalar reduce
     (1, 512, 8, 8, 64, 3, 3, 1, 1),    # np = 64: split-K, vector reduce + row bias
     (4, 16, 13, 13, 130, 3, 3, 1, 1),  # c_out tail (clamped weight rows), np = 676
@@ -448,7 +448,7 @@ NCHW_PATHS = ("b=im2col_nchw", "b=im2col_halo")
 @pytest.mark.parametrize("n,c,h,wd,co,kh,kw,stride,pad", [
     (2, 4, 9, 9, 8, 3, 3, 1, 1),       # kg = 36: a partial last chunk
     (1, 12, 7, 7, 10, 5, 5, 2, 2),     # kg = 300, stride 2
-    (2, 8, 6, 6, 5, 1, 1, 1, 0),       # kg = 8: less than one chunk
+    (2, 8, 5, 5, 5, 1, 1, 1, 0),       # kg = 8: less than one chunk (1x1, 25 positions)
     (1, 20, 11, 9, 7, 3, 2, 1, 1),     # 3x2 kernel
     (3, 4, 10, 12, 66, 3, 3, 3, 0),    # stride 3, no padding, c_out tail
 ])
@@ -560,7 +560,7 @@ def test_conv_halo_repeat_bitwise(dev):
 
 
 @pytest.mark.parametrize("n,c,h,wd,co,kh,kw,stride,pad", [
-    (2, 8, 6, 6, 5, 1, 1, 1, 0),        # one tap: no patch reuse
+    (2, 8, 5, 5, 5, 1, 1, 1, 0),        # one tap: no patch reuse
     (1, 4, 5, 200, 6, 3, 3, 1, 1),      # 202 padded columns: the band is too wide
     (2, 8, 20, 20, 16, 3, 3, 1, 1),     # K 72: less than one patch, not worth it
 ])
@@ -654,7 +654,7 @@ def test_linear_bias_grad_with_split_k_dw(dev):
 @pytest.mark.parametrize("n,c,h,wd,co,k,pad", [
     (2, 5, 9, 7, 16, 3, 1),
     (1, 3, 8, 8, 32, 5, 2),
-    (2, 4, 6, 6, 16, 1, 0),     # 1x1: pad' = 0
+    (2, 4, 5, 7, 16, 1, 0),     # 1x1: pad' = 0 (35 positions)
     (1, 2, 7, 7, 16, 3, 0),     # pad 0: pad' = 2, output grows back to 7x7
     (1, 8, 5, 6, 16, 5, 4),     # pad = kh-1: pad' = 0
     (3, 7, 11, 10, 48, 3, 1),   # c_in tail (odd), three chunks per tap
