@@ -1865,6 +1865,22 @@ DxPhases dx_phases(const mt_conv2d_desc* d) {
     return t;
 }
 
+// A strided 1x1 kernel without padding (strides 2-4, c_in and h_out*w_out
+// multiples of 4): only the pixels of phase (0, 0) see a tap, and there
+// dX_b = Wᵀ·dY_b per image, over dY in NCHW.  The product runs batched into
+// the compact phase buffer and the interleave writes dX (zeros elsewhere):
+// no dY copy, no phase weights, and the batch fills the chip where the
+// phase's single implicit GEMM had 196 workgroups of 256x128 (56x56,
+// 256 -> 512 channels).
+bool pointwise_strided(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo) {
+    return d->kh == 1 && d->kw == 1 && d->pad == 0 && d->stride >= 2 &&
+           d->stride <= kDxMaxStride && d->c_in > 0 && (d->c_in & 3) == 0 &&
+           ((Ho * Wo) & 3) == 0 && Ho * Wo < kMaxDim && d->h * d->w < kMaxDim;
+}
+size_t pointwise_strided_zb(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo) {
+    return align_up((size_t)d->n * d->c_in * Ho * Wo * sizeof(float), 256);
+}
+
 // The phased dX applies for strides up to kDxMaxStride.  Channels-last
 // (cl): c_out % 16 == 0, dY copied to channels-last once.  Otherwise the
 // NCHW kernel reads dY in place, and every phase's weight rows must be
@@ -1909,6 +1925,70 @@ dx_phase_weights_f32(const float* W, float* out, DxPhases t, int c_out, int c_in
     }
 }
 
+// The compact outputs of the phased dX: phase f = ph*s + pw holds the pixels
+// ih = ph + s*i, iw = pw + s*j as z[f][img*c_in + ci][i][j] (hp[f] x wp[f]);
+// null where no tap reaches the phase (its pixels are zero).
+struct DxPhaseOut {
+    const float* z[kDxMaxStride * kDxMaxStride];
+    int hp[kDxMaxStride * kDxMaxStride], wp[kDxMaxStride * kDxMaxStride];
+};
+
+// dX[plane][ih][iw] = z[(ih%S)*S + iw%S][plane][ih/S][iw/S], plane = img*c_in
+// + ci: blockIdx.y walks planes, threads walk items of V pixels of one row,
+// stored as one 16-byte vector when V == 4 (W % 4 == 0, aligned).  The phase
+// is chosen by compares against every index (an indexed read of the argument
+// arrays would go through scratch).  Reads and writes dX's bytes once each.
+template <int S, int V>
+__global__ void __launch_bounds__(256)
+dx_interleave_f32(DxPhaseOut o, float* dx, int64_t planes, int H, int W) {
+    const int wq = W / V;
+    const int per = H * wq;
+    for (int64_t plane = blockIdx.y; plane < planes; plane += gridDim.y) {
+        float* dplane = dx + plane * H * W;
+        for (int q = blockIdx.x * blockDim.x + threadIdx.x; q < per; q += gridDim.x * blockDim.x) {
+            const int ih = q / wq, iw0 = (q - ih * wq) * V;
+            const int ph = ih % S, i = ih / S;
+            float v[V];
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+                const int iw = iw0 + e;
+                const int f = ph * S + iw % S;
+                const float* z = o.z[0];
+                int hp = o.hp[0], wp = o.wp[0];
+#pragma unroll
+                for (int c = 1; c < S * S; ++c)
+                    if (f == c) {
+                        z = o.z[c];
+                        hp = o.hp[c];
+                        wp = o.wp[c];
+                    }
+                v[e] = z ? z[(plane * hp + i) * wp + iw / S] : 0.f;
+            }
+            float* dst = dplane + (int64_t)ih * W + iw0;
+            if constexpr (V == 4)
+                *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
+            else
+                dst[0] = v[0];
+        }
+    }
+}
+
+// For strides 2-4 (at stride 1 the one phase is dX itself).
+hipError_t launch_dx_interleave(const DxPhaseOut& o, int s, float* dx, int64_t planes, int H,
+                                int W, hipStream_t st) {
+    if (s < 2 || s > kDxMaxStride) return hipErrorInvalidValue;
+    const bool vec = (W & 3) == 0 && ((uintptr_t)dx & 15u) == 0;
+    const int per = H * (vec ? W / 4 : W);
+    const dim3 grid((unsigned)std::min<int64_t>((per + 255) / 256, 1024),
+                    (unsigned)std::min<int64_t>(planes, 65535));
+    if (planes == 0 || per == 0) return hipSuccess;
+    auto k = s == 2 ? (vec ? dx_interleave_f32<2, 4> : dx_interleave_f32<2, 1>)
+             : s == 3 ? (vec ? dx_interleave_f32<3, 4> : dx_interleave_f32<3, 1>)
+                      : (vec ? dx_interleave_f32<4, 4> : dx_interleave_f32<4, 1>);
+    hipLaunchKernelGGL(k, grid, dim3(256), 0, st, o, dx, planes, H, W);
+    return capture_safe_last_error();
+}
+
 // Whether the phased dX is expected to beat dcol = Wᵀ·dY + col2im for d.
 // Both run the same flops; the phased GEMMs have c_in rows and a phase's
 // pixels as columns (small when c_in is small or the image is), the column
@@ -1922,6 +2002,11 @@ dx_phase_weights_f32(const float* W, float* out, DxPhases t, int c_out, int c_in
 // 2 TB/s (kDxGatherBytes).  This picks the faster path on five of the seven
 // layers and loses 5 and 8 % on the two near-ties (the 3x3 at 28, the 1x1
 // at 28), where "always phased" loses up to 4.5x (the stem: 3 rows).
+// Re-checked after the phases moved to compact outputs and one interleave
+// (priced as 2 x dX bytes in the stream term), on eight layers (3x3 stride 2
+// at 112/56/28/14 with 64-512 channels, the 1x1 at 14, the stem): 1.7 picks
+// the faster path on seven and loses 9 % on the 3x3 at 28 with 256 channels
+// (151.6 against 138.8 us); factors 1.0-1.4 lose on two.
 constexpr double kDxPhasedFactor = 1.7;
 constexpr double kDxStreamBytes = 2083.0;   // device bytes per CU cycle at 5 TB/s, 2.4 GHz
 constexpr double kDxGatherBytes = 833.0;    // ... at 2 TB/s
@@ -1933,14 +2018,12 @@ bool dx_prefer_phased(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, bool cl) 
     const DxPhases t = dx_phases(d);
     const int64_t kg = d->c_in * d->kh * d->kw, np = d->n * Ho * Wo;
     const double dx_bytes = 4.0 * d->n * d->c_in * d->h * d->w;
-    double phased = 0, stream = cl ? 8.0 * d->c_out * np : 0.0;
+    // the dY copy, and for strides above 1 the interleave (compact phase
+    // outputs read, every dX pixel written, zeros included)
+    double phased = 0, stream = (cl ? 8.0 * d->c_out * np : 0.0) + (t.s > 1 ? 2.0 * dx_bytes : 0.0);
     for (int i = 0; i < t.n; ++i) {
         const DxPhase& f = t.f[i];
-        if (f.hp == 0 || f.wp == 0) continue;
-        if (f.k == 0) {
-            stream += dx_bytes * f.hp * f.wp / ((double)d->h * d->w);
-            continue;
-        }
+        if (f.hp == 0 || f.wp == 0 || f.k == 0) continue;
         phased += make_plan(d->c_in, d->n * f.hp * f.wp, f.k, 1, cus, true, true, false, false)
                       .cycles;
     }
@@ -1964,9 +2047,12 @@ size_t implicit_gemm_ws(int64_t M, int64_t N, int64_t K, bool imw) {
     return ws;
 }
 
-// Layout of the phased dX workspace: [channels-last dY (cl)][phase weights][GEMM].
+// Layout of the phased dX workspace: [channels-last dY (cl)][phase weights]
+// [compact phase outputs (strides 2-4)][GEMM].  zoff: each phase's output, in
+// floats from the start of its block (aligned to 256 bytes).
 struct DxPhasedWs {
-    size_t dyt, wph, gemm;
+    size_t dyt, wph, z, gemm;
+    int64_t zoff[kDxMaxStride * kDxMaxStride];
 };
 DxPhasedWs dx_phased_ws(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, bool cl) {
     DxPhasedWs w{};
@@ -1975,8 +2061,13 @@ DxPhasedWs dx_phased_ws(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, bool cl
     const DxPhases t = dx_phases(d);
     for (int i = 0; i < t.n; ++i) {
         const DxPhase& f = t.f[i];
-        if (f.k > 0 && f.hp > 0 && f.wp > 0)
+        w.zoff[i] = (int64_t)(w.z / sizeof(float));
+        if (f.k > 0 && f.hp > 0 && f.wp > 0) {
+            // stride 1: the one phase is dX itself, written in place
+            if (t.s > 1)
+                w.z += align_up((size_t)d->n * d->c_in * f.hp * f.wp * sizeof(float), 256);
             w.gemm = std::max(w.gemm, implicit_gemm_ws(d->c_in, d->n * f.hp * f.wp, f.k, false));
+        }
     }
     return w;
 }
@@ -1987,6 +2078,9 @@ size_t dx_ws(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo) {
     if (np == 0 || d->c_out == 0 || d->n * d->c_in * d->h * d->w == 0) return 0;
     const int64_t nx = d->n * d->h * d->w, kx = d->c_out * d->kh * d->kw;
     if (pointwise(d)) return plan_ws(d->c_in, d->h * d->w, d->c_out, d->n, device_cu_count());
+    if (pointwise_strided(d, Ho, Wo))
+        return pointwise_strided_zb(d, Ho, Wo) +
+               plan_ws(d->c_in, Ho * Wo, d->c_out, d->n, device_cu_count());
     mt_conv2d_desc t;
     if (dx_as_forward(d, Ho, Wo, &t) && implicit_geometry(&t)) {
         const ImplicitWs iw = implicit_ws(&t);
@@ -1997,7 +2091,7 @@ size_t dx_ws(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo) {
     bool cl = false;
     if (dx_phased(d, Ho, Wo, &cl) && dx_prefer_phased(d, Ho, Wo, cl)) {
         const DxPhasedWs w = dx_phased_ws(d, Ho, Wo, cl);
-        return w.dyt + w.wph + w.gemm;
+        return w.dyt + w.wph + w.z + w.gemm;
     }
     return align_up((size_t)kg * np * sizeof(float), 256) +
            align_up((size_t)d->c_out * np * sizeof(float), 256) +
@@ -2031,7 +2125,7 @@ int run_dx_phased(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, bool cl,
                   const float* grad_out, const float* weight, float* grad_input, void* workspace,
                   size_t ws_bytes, hipStream_t s) {
     const DxPhasedWs w = dx_phased_ws(d, Ho, Wo, cl);
-    if (!workspace || ws_bytes < w.dyt + w.wph || ((uintptr_t)workspace & 15u) != 0)
+    if (!workspace || ws_bytes < w.dyt + w.wph + w.z || ((uintptr_t)workspace & 15u) != 0)
         return MT_ERR_WORKSPACE;
     char* wsp = static_cast<char*>(workspace);
     const DxPhases t = dx_phases(d);
@@ -2047,27 +2141,29 @@ int run_dx_phased(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, bool cl,
                        (int)d->c_out, (int)d->c_in, (int)d->kh, (int)d->kw, (int)d->pad,
                        cl ? 1 : 0);
     if (capture_safe_last_error() != hipSuccess) return MT_ERR_HIP;
-    bool empty = false;   // a phase with pixels that no tap reaches
-    for (int i = 0; i < t.n; ++i)
-        empty |= t.f[i].hp > 0 && t.f[i].wp > 0 && t.f[i].k == 0;
-    if (empty) {
-        const int64_t total = d->n * d->c_in * d->h * d->w;
-        hipLaunchKernelGGL(fill_f32, dim3(grid_for(total)), dim3(256), 0, s, grad_input, total,
-                           0.f);
-        if (capture_safe_last_error() != hipSuccess) return MT_ERR_HIP;
-    }
-    char* gws = wsp + w.dyt + w.wph;
-    const size_t gws_b = ws_bytes - w.dyt - w.wph;
+    // Each phase's GEMM writes its pixels compactly, [img][c_in][hp][wp] (whole
+    // 16-byte stores where hp*wp % 4 == 0), and one launch interleaves the
+    // phases into dX, zeros where no tap reaches.  Storing straight into dX
+    // at stride s cost more than the GEMM (4-byte stores s floats apart: the
+    // 1-tap phase of a 3x3 stride-2 layer at 56x56, 128 channels, 32 us).
+    float* zb = reinterpret_cast<float*>(wsp + w.dyt + w.wph);
+    DxPhaseOut o{};
+    char* gws = wsp + w.dyt + w.wph + w.z;
+    const size_t gws_b = ws_bytes - w.dyt - w.wph - w.z;
     for (int i = 0; i < t.n; ++i) {
         const DxPhase& f = t.f[i];
+        o.hp[i] = f.hp;
+        o.wp[i] = f.wp;
         if (f.k == 0 || f.hp == 0 || f.wp == 0) continue;
+        float* z = t.s == 1 ? grad_input : zb + w.zoff[i];
+        o.z[i] = z;
+        const int64_t php = (int64_t)f.hp * f.wp;
         GemmParams p{};
         p.A = wph + f.woff; p.a_mn = f.k; p.a_k = 1; p.a_b = 0;
         p.B = cl ? dyt : grad_out;
-        p.C = grad_input + (int64_t)f.ph * d->w + f.pw;
-        p.c_m = d->h * d->w; p.c_n = t.s; p.c_b = 0;
-        p.c_n_inner = f.wp; p.c_n_outer = t.s * d->w;
-        p.c_n_inner2 = (int64_t)f.hp * f.wp; p.c_n_outer2 = d->c_in * d->h * d->w;
+        p.C = z;
+        p.c_m = php; p.c_n = 1; p.c_b = 0;
+        p.c_n_inner = php; p.c_n_outer = d->c_in * php;
         p.bias = nullptr; p.bias_stride = 0; p.bias_axis = MT_BIAS_NONE;
         p.beta = 0.f;
         p.M = (int)d->c_in; p.N = (int)(d->n * f.hp * f.wp); p.K = f.k; p.batch = 1;
@@ -2083,7 +2179,11 @@ int run_dx_phased(const mt_conv2d_desc* d, int64_t Ho, int64_t Wo, bool cl,
         const int rc = launch_gemm(p, true, L_KV, cl ? L_IM : L_IMR, gws, gws_b, s);
         if (rc != MT_OK) return rc;
     }
-    return MT_OK;
+    if (t.s == 1) return MT_OK;
+    return launch_dx_interleave(o, t.s, grad_input, d->n * d->c_in, (int)d->h, (int)d->w, s) ==
+                   hipSuccess
+               ? MT_OK
+               : MT_ERR_HIP;
 }
 
 }  // namespace
@@ -2455,6 +2555,29 @@ int mt_conv2d_bwd_input_f32(const mt_conv2d_desc* d, const float* grad_out, cons
         const mt_mat_f32 B{grad_out, 0, d->c_out, hw, hw, 1, d->n, d->c_out * hw};
         const mt_mat_f32 C{grad_input, 0, d->c_in, hw, hw, 1, d->n, d->c_in * hw};
         return run_gemm(&A, &B, &C, 0, 0, nullptr, workspace, ws_bytes, s);
+    }
+    if (pointwise_strided(d, Ho, Wo)) {   // phase (0, 0): Z_b = Wᵀ · dY_b, then interleave
+        const size_t zb = pointwise_strided_zb(d, Ho, Wo);
+        if (!workspace || ws_bytes < zb || ((uintptr_t)workspace & 15u) != 0)
+            return MT_ERR_WORKSPACE;
+        float* z = static_cast<float*>(workspace);
+        const mt_mat_f32 A{weight, 0, d->c_in, d->c_out, 1, d->c_in, d->n, 0};
+        const mt_mat_f32 B{grad_out, 0, d->c_out, hw, hw, 1, d->n, d->c_out * hw};
+        const mt_mat_f32 C{z, 0, d->c_in, hw, hw, 1, d->n, d->c_in * hw};
+        const int rc = run_gemm(&A, &B, &C, 0, 0, nullptr, static_cast<char*>(workspace) + zb,
+                                ws_bytes - zb, s);
+        if (rc != MT_OK) return rc;
+        const DxPhases t = dx_phases(d);
+        DxPhaseOut o{};
+        for (int i = 0; i < t.n; ++i) {
+            o.hp[i] = t.f[i].hp;
+            o.wp[i] = t.f[i].wp;
+        }
+        o.z[0] = z;
+        return launch_dx_interleave(o, t.s, grad_input, d->n * d->c_in, (int)d->h, (int)d->w,
+                                    s) == hipSuccess
+                   ? MT_OK
+                   : MT_ERR_HIP;
     }
     mt_conv2d_desc t;
     if (dx_as_forward(d, Ho, Wo, &t) && implicit_geometry(&t)) {

@@ -207,20 +207,24 @@ def test_gemv_split_partials_in_the_workspace_query():
 
 def test_conv_backward_workspace_is_the_paths_need():
     """mt_conv2d_bwd_workspace_f32 reports what the dX and dW (+ db) paths use
-    (the larger of the two), not a column buffer they never touch.  Shapes
-    small enough that no GEMM splits K (K <= 64, or the cost model's
-    single-split plans), so every term is a buffer:
+    (the larger of the two), not buffers they never touch.  Shapes small
+    enough that no GEMM splits K, so every term is a buffer:
     3x3 stride 2, n 1, 16 -> 16 channels, 8x8 -> 4x4:
-      dX by stride phase (channels-last): dY copy 1*16*4*4 floats (1024 B)
-      + the phases' sub-kernel weights 16*16*9 floats (9216 B);
+      dX by the column path (the cost model's pick at this size): column
+      buffer 144*16 floats (9216 B) + dY copy 16*16 floats (1024 B);
+      forced onto the phased path: dY copy (1024 B) + the phases' sub-kernel
+      weights 16*16*9 floats (9216 B) + four compact phase outputs of
+      1*16*4*4 floats (4 x 1024 B);
       dW implicit: channels-last x 16*8*8 floats (4096 B), dY read in NCHW;
     1x1 stride 2, n 2, 32 -> 64 channels, 8x8 -> 4x4:
-      dX: dY copy 2*64*16 floats (8192 B) + weights 64*32 (8192 B);
+      dX: the per-image product's phase-(0, 0) output 2*32*16 floats (4096 B);
       dW: x copy 2*32*64 floats (16384 B)."""
     import ctypes
     lib = mt.lib()
     d = mt.Conv2dDesc(1, 16, 8, 8, 16, 3, 3, 2, 1)
-    assert lib.mt_conv2d_bwd_workspace_f32(ctypes.byref(d)) == 1024 + 9216
+    assert lib.mt_conv2d_bwd_workspace_f32(ctypes.byref(d)) == 9216 + 1024
+    with mt.forced_config(mt.FAMILY_DL, 1, 1):
+        assert lib.mt_conv2d_bwd_workspace_f32(ctypes.byref(d)) == 1024 + 9216 + 4 * 1024
     d = mt.Conv2dDesc(2, 32, 8, 8, 64, 1, 1, 2, 0)
     assert lib.mt_conv2d_bwd_workspace_f32(ctypes.byref(d)) == 16384
     # the benchmark's 5a layer: far below its 57.8 MB column buffer

@@ -30,7 +30,9 @@ CASES = [
     (2, 64, 28, 28, 64, 3, 3, 2, 1, "cl"),       # ResNet 3x3 stride-2 (layer2 at 1/2 scale)
     (2, 128, 28, 28, 128, 3, 3, 2, 1, "cl"),
     (2, 256, 14, 14, 256, 3, 3, 2, 1, "cl"),
-    (2, 64, 28, 28, 128, 1, 1, 2, 0, "cl"),      # 1x1 stride-2 shortcut: 3 of 4 phases zero
+    (2, 64, 26, 26, 128, 1, 1, 2, 0, "cl"),      # 1x1 stride-2 shortcut: 3 of 4 phases zero
+    # (a 1x1 layer whose output has a multiple of 4 positions per image takes
+    # the per-image product instead, tests/test_conv_pointwise_gpu.py)
     (2, 256, 14, 14, 512, 1, 1, 2, 0, "cl"),
     (3, 32, 15, 13, 48, 3, 3, 2, 1, "cl"),       # odd extents
     (2, 16, 11, 12, 32, 3, 3, 2, 0, "cl"),       # unequal padding per axis in a phase

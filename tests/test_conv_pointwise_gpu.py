@@ -251,3 +251,31 @@ def test_pointwise_workspace_is_exact_and_graph_replays(dev):
         graph.replay()
         for got, want in zip((Y, dX, dW, dB), eager):
             assert np.array_equal(sync_np(got), want)
+
+
+@pytest.mark.parametrize("n,c,h,w,co,stride", [
+    (2, 16, 8, 8, 24, 2),      # 4x4 output
+    (3, 32, 11, 7, 20, 3),     # ragged: 4x3 output, rows and columns past the last phase
+    (1, 12, 13, 13, 40, 4),    # 4x4 output, 13 = 3*4 + 1
+    (4, 64, 28, 28, 128, 2),   # a ResNet downsampling shortcut, batch 4
+])
+def test_pointwise_strided_dx(dev, n, c, h, w, co, stride):
+    """dX of a strided 1x1 layer without padding: the product Wᵀ·dY_b per
+    image into the phase-(0, 0) buffer, then the interleave writes dX with
+    zeros on every pixel no tap reaches; against the oracle, bit-identical on
+    a repeat."""
+    x = oracle.normal((n, c, h, w), 51)
+    wt = oracle.normal((co, c, 1, 1), 52)
+    ho, wo = oracle.conv_out(h, 0, 1, stride), oracle.conv_out(w, 0, 1, stride)
+    dy = oracle.normal((n, co, ho, wo), 53)
+    X, Wt, dY = g(x, dev), g(wt, dev), g(dy, dev)
+    outs = []
+    for _ in range(2):
+        dX, _, _ = mt.conv2d_backward(X, Wt, dY, stride, 0, need_dw=False, need_db=False)
+        outs.append(sync_np(dX))
+    cfg = mt.last_config()
+    print(f"[config] {cfg}", flush=True)
+    assert "im2col" not in cfg and "a=mv b=mv" in cfg, cfg
+    assert np.array_equal(outs[0], outs[1])
+    wdx, _, _ = oracle.conv2d_backward(x, wt, dy, stride, 0)
+    assert_close(outs[0], wdx, co, amax(dy), amax(wt), f"1x1 stride {stride} dX")

@@ -149,9 +149,11 @@ def test_graph_conv_replays(dev):
 
 def test_graph_skinny_and_phased_dx_replays(dev):
     """The vector-ALU kernels (a split GEMV with its reduction launch, a
-    transposed GEMV, a rank-k product) and a strided convolution's dX by
-    stride phase (dY copy, phase weights, zero fill, one GEMM per phase)
-    captured together; every replay equals the eager calls bit for bit."""
+    transposed GEMV, a rank-k product), a strided convolution's dX by stride
+    phase (dY copy, phase weights, one GEMM per phase into compact outputs,
+    the interleave) and a strided 1x1 layer's dX (the per-image product, the
+    interleave) captured together; every replay equals the eager calls bit
+    for bit."""
     gen = torch.Generator(device=dev)
     gen.manual_seed(8)
     a = torch.rand(1, 4096, device=dev, generator=gen)
@@ -165,11 +167,16 @@ def test_graph_skinny_and_phased_dx_replays(dev):
     u = torch.rand(2048, 2, device=dev, generator=gen)
     w2 = torch.rand(2, 2048, device=dev, generator=gen)
     r = torch.empty(2048, 2048, device=dev)
-    x = torch.randn(4, 32, 28, 28, device=dev, generator=gen)
+    x = torch.randn(4, 32, 26, 26, device=dev, generator=gen)
     wc = torch.randn(64, 32, 1, 1, device=dev, generator=gen) * 0.1
-    dy = torch.randn(4, 64, 14, 14, device=dev, generator=gen)
-    d = mt.Conv2dDesc(4, 32, 28, 28, 64, 1, 1, 2, 0)
+    dy = torch.randn(4, 64, 13, 13, device=dev, generator=gen)
+    d = mt.Conv2dDesc(4, 32, 26, 26, 64, 1, 1, 2, 0)
     dx = torch.empty_like(x)
+    # 28x28 -> 14x14 (196 positions, a multiple of 4): the per-image product
+    dy2 = torch.randn(4, 64, 14, 14, device=dev, generator=gen)
+    d2 = mt.Conv2dDesc(4, 32, 28, 28, 64, 1, 1, 2, 0)
+    dx2 = torch.empty(4, 32, 28, 28, device=dev)
+    ws_c2 = mt.workspace(mt.lib().mt_conv2d_bwd_workspace_f32(ctypes.byref(d2)), dev)
 
     with mt.forced_config(mt.FAMILY_DL, 1, 1):   # the phased dX on this small layer
         ws_c = mt.workspace(mt.lib().mt_conv2d_bwd_workspace_f32(ctypes.byref(d)), dev)
@@ -188,6 +195,12 @@ def test_graph_skinny_and_phased_dx_replays(dev):
                 ws_c.numel(), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
             cfgs.append(mt.last_config())
         assert rc == mt.MT_OK
+        rc = mt.lib().mt_conv2d_bwd_input_f32(
+            ctypes.byref(d2), dy2.data_ptr(), wc.data_ptr(), dx2.data_ptr(),
+            mt._ptr(ws_c2), 0 if ws_c2 is None else ws_c2.numel(),
+            ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        cfgs.append(mt.last_config())
+        assert rc == mt.MT_OK
 
     step()
     torch.cuda.synchronize()
@@ -195,18 +208,23 @@ def test_graph_skinny_and_phased_dx_replays(dev):
     assert cfgs[0].startswith("sk gemv_mv ") and "split=1 " not in cfgs[0] + " ", cfgs
     assert cfgs[1].startswith("sk gemv_kv_t ") and cfgs[2].startswith("sk rankk "), cfgs
     assert "b=im2col " in cfgs[3] + " ", cfgs
+    assert "a=mv b=mv" in cfgs[4] and "im2col" not in cfgs[4], cfgs
     g = _capture(step)
     for rep in range(3):
         a.copy_(torch.rand(1, 4096, device=dev, generator=gen))
-        dy.copy_(torch.randn(4, 64, 14, 14, device=dev, generator=gen))
+        dy.copy_(torch.randn(4, 64, 13, 13, device=dev, generator=gen))
+        dy2.copy_(torch.randn(4, 64, 14, 14, device=dev, generator=gen))
         dx.fill_(7.0)
+        dx2.fill_(7.0)
         torch.cuda.synchronize()
         g.replay()
         torch.cuda.synchronize()
-        got = [t.clone() for t in (c, cv, r, dx)]
+        got = [t.clone() for t in (c, cv, r, dx, dx2)]
         dx.fill_(-7.0)
+        dx2.fill_(-7.0)
         step()
         torch.cuda.synchronize()
-        for name, x1, e in zip(("gemv", "gemv_t", "rank-k", "dX"), got, (c, cv, r, dx)):
+        for name, x1, e in zip(("gemv", "gemv_t", "rank-k", "dX", "dX 1x1 s2"), got,
+                               (c, cv, r, dx, dx2)):
             assert torch.equal(x1, e), f"replay {rep}: {name} differs from eager"
         print(f"[graph] skinny + phased dX replay {rep} == eager", flush=True)
