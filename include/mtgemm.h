@@ -190,13 +190,16 @@ int mt_conv2d_fwd_strided_f32(const mt_conv2d_desc* d, const float* input,
  *           implicit-GEMM forward convolution of dY with the weights
  *           transposed to [c_in][c_out] and flipped, padding kh-1-pad (no
  *           column buffer; channels-last when c_out % 16 == 0, else from
- *           the NCHW dY); other strides up to 4 (and other stride-1 kernels):
+ *           the NCHW dY); a strided 1x1 kernel without padding (c_in and
+ *           h_out*w_out multiples of 4): Wᵀ · dY_b per image into the
+ *           workspace, then one launch writes dX (zeros where no tap
+ *           reaches); other strides up to 4 (and other stride-1 kernels):
  *           one implicit GEMM per stride phase (ih % s, iw % s) of dX, a
  *           stride-1 convolution of dY with that phase's flipped sub-kernel
- *           scattered to every s-th pixel (channels-last dY when
- *           c_out % 16 == 0, else dY read in place when every phase's
- *           c_out*taps % 4 == 0); otherwise dcol = Wᵀ · dY, then a
- *           deterministic col2im gather into dX
+ *           into the workspace, then one launch interleaves the phases into
+ *           dX (channels-last dY when c_out % 16 == 0, else dY read in
+ *           place when every phase's c_out*taps % 4 == 0); otherwise
+ *           dcol = Wᵀ · dY, then a deterministic col2im gather into dX
  *           replaces conv2d_backward_input_gpu + fused_backward_input_kernel
  *           (reference src/gpu_ops.cpp:2499-2550, 861-907)
  *   bias:   db[c] = Σ_{n,y,x} dY[n,c,y,x] (+ beta·db)
