@@ -89,7 +89,7 @@ GemmLaunchFn dl_launcher_cfg3(int la, int lb);
 // not a multiple of 16.
 GemmLaunchFn dlp_launcher(int cfg, bool tail, int la, int lb);
 // Configurations 4-6 with the row sums of A (GemmParams::rowsum); A and B L_MV.
-GemmLaunchFn dlp_rowsum_launcher(int cfg, bool tail);
+GemmLaunchFn dlp_rowsum_launcher(int cfg, bool tail, bool kv);
 // Configurations 4-6 for the convolution weight gradient (A L_KV, B L_IMW).
 GemmLaunchFn dlp_convw_launcher(int cfg, bool tail);
 // Configurations 4-6 for the weight gradient with A = dY in NCHW (L_KVI).
@@ -124,10 +124,10 @@ GemmLaunchFn dl_convwi_launcher_cfg1();
 GemmLaunchFn dl_convwi_launcher_cfg2();
 GemmLaunchFn dl_convwi_launcher_cfg3();
 // A and B mn-contiguous, with the row sums of A (GemmParams::rowsum).
-GemmLaunchFn dl_rowsum_launcher_cfg0();
-GemmLaunchFn dl_rowsum_launcher_cfg1();
-GemmLaunchFn dl_rowsum_launcher_cfg2();
-GemmLaunchFn dl_rowsum_launcher_cfg3();
+GemmLaunchFn dl_rowsum_launcher_cfg0(bool kv);
+GemmLaunchFn dl_rowsum_launcher_cfg1(bool kv);
+GemmLaunchFn dl_rowsum_launcher_cfg2(bool kv);
+GemmLaunchFn dl_rowsum_launcher_cfg3(bool kv);
 
 // Wave-split kernel (gemm_ksw_kernel.hpp): tile (R*MB) x (R*NB) of R x R
 // MFMA blocks (R = 32: gemm_f32_ksw, R = 16: gemm_f32_ksw16), W waves

@@ -54,7 +54,9 @@ GemmLaunchFn dl_convr_launcher_cfg0() { return launch_dl<0, L_KV, L_IMR>; }
 GemmLaunchFn dl_convh_launcher_cfg0() { return launch_dlh<0>; }
 GemmLaunchFn dl_convw_launcher_cfg0() { return launch_dl<0, L_KV, L_IMW>; }
 GemmLaunchFn dl_convwi_launcher_cfg0() { return launch_dl<0, L_KVI, L_IMW>; }
-GemmLaunchFn dl_rowsum_launcher_cfg0() { return launch_dl<0, L_MV, L_MV, true>; }
+GemmLaunchFn dl_rowsum_launcher_cfg0(bool kv) {
+    return kv ? launch_dl<0, L_KV, L_KV, true> : launch_dl<0, L_MV, L_MV, true>;
+}
 #elif MT_CFG == 1
 GemmLaunchFn dl_launcher_cfg1(int la, int lb) {
     static const GemmLaunchFn table[2][2] = MT_DL_TABLE(1);
@@ -65,7 +67,9 @@ GemmLaunchFn dl_convr_launcher_cfg1() { return launch_dl<1, L_KV, L_IMR>; }
 GemmLaunchFn dl_convh_launcher_cfg1() { return launch_dlh<1>; }
 GemmLaunchFn dl_convw_launcher_cfg1() { return launch_dl<1, L_KV, L_IMW>; }
 GemmLaunchFn dl_convwi_launcher_cfg1() { return launch_dl<1, L_KVI, L_IMW>; }
-GemmLaunchFn dl_rowsum_launcher_cfg1() { return launch_dl<1, L_MV, L_MV, true>; }
+GemmLaunchFn dl_rowsum_launcher_cfg1(bool kv) {
+    return kv ? launch_dl<1, L_KV, L_KV, true> : launch_dl<1, L_MV, L_MV, true>;
+}
 #elif MT_CFG == 2
 GemmLaunchFn dl_launcher_cfg2(int la, int lb) {
     static const GemmLaunchFn table[2][2] = MT_DL_TABLE(2);
@@ -76,7 +80,9 @@ GemmLaunchFn dl_convr_launcher_cfg2() { return launch_dl<2, L_KV, L_IMR>; }
 GemmLaunchFn dl_convh_launcher_cfg2() { return launch_dlh<2>; }
 GemmLaunchFn dl_convw_launcher_cfg2() { return launch_dl<2, L_KV, L_IMW>; }
 GemmLaunchFn dl_convwi_launcher_cfg2() { return launch_dl<2, L_KVI, L_IMW>; }
-GemmLaunchFn dl_rowsum_launcher_cfg2() { return launch_dl<2, L_MV, L_MV, true>; }
+GemmLaunchFn dl_rowsum_launcher_cfg2(bool kv) {
+    return kv ? launch_dl<2, L_KV, L_KV, true> : launch_dl<2, L_MV, L_MV, true>;
+}
 #elif MT_CFG == 3
 GemmLaunchFn dl_launcher_cfg3(int la, int lb) {
     static const GemmLaunchFn table[2][2] = MT_DL_TABLE(3);
@@ -87,7 +93,9 @@ GemmLaunchFn dl_convr_launcher_cfg3() { return launch_dl<3, L_KV, L_IMR>; }
 GemmLaunchFn dl_convh_launcher_cfg3() { return launch_dlh<3>; }
 GemmLaunchFn dl_convw_launcher_cfg3() { return launch_dl<3, L_KV, L_IMW>; }
 GemmLaunchFn dl_convwi_launcher_cfg3() { return launch_dl<3, L_KVI, L_IMW>; }
-GemmLaunchFn dl_rowsum_launcher_cfg3() { return launch_dl<3, L_MV, L_MV, true>; }
+GemmLaunchFn dl_rowsum_launcher_cfg3(bool kv) {
+    return kv ? launch_dl<3, L_KV, L_KV, true> : launch_dl<3, L_MV, L_MV, true>;
+}
 #else
 #error "unknown MT_CFG"
 #endif

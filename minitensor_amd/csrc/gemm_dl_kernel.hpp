@@ -680,8 +680,12 @@ gemm_f32_dl(GemmParams p) {
             const float tot = rsum[i] + __shfl_xor(rsum[i], 32);
             const int m = m0 + ra + i * 32 + (lane & 31);
             if (lane < 32 && m < p.M) {
-                float* d = p.rowsum + (int64_t)m * p.rowsum_stride;
-                *d = (p.rowsum_beta != 0.f ? p.rowsum_beta * *d : 0.f) + tot;
+                if (p.splits > 1 || p.part) {   // this (split, batch entry)'s partial
+                    p.rowsum[((int64_t)id.split * p.batch + id.bz) * p.M + m] = tot;
+                } else {
+                    float* d = p.rowsum + (int64_t)m * p.rowsum_stride;
+                    *d = (p.rowsum_beta != 0.f ? p.rowsum_beta * *d : 0.f) + tot;
+                }
             }
         }
     }

@@ -39,12 +39,16 @@ GemmLaunchFn dlp_convwi_launcher(int cfg) {
     return table[cfg - 4];
 }
 
-GemmLaunchFn dlp_rowsum_launcher(int cfg, bool tail) {
-    static const GemmLaunchFn table[3][2] = {
-        {launch_dlp<4, false, L_MV, L_MV, true>, launch_dlp<4, true, L_MV, L_MV, true>},
-        {launch_dlp<5, false, L_MV, L_MV, true>, launch_dlp<5, true, L_MV, L_MV, true>},
-        {launch_dlp<6, false, L_MV, L_MV, true>, launch_dlp<6, true, L_MV, L_MV, true>}};
-    return table[cfg - 4][tail];
+GemmLaunchFn dlp_rowsum_launcher(int cfg, bool tail, bool kv) {
+    static const GemmLaunchFn table[3][2][2] = {
+        {{launch_dlp<4, false, L_MV, L_MV, true>, launch_dlp<4, true, L_MV, L_MV, true>},
+         {launch_dlp<4, false, L_KV, L_KV, true>, launch_dlp<4, true, L_KV, L_KV, true>}},
+        {{launch_dlp<5, false, L_MV, L_MV, true>, launch_dlp<5, true, L_MV, L_MV, true>},
+         {launch_dlp<5, false, L_KV, L_KV, true>, launch_dlp<5, true, L_KV, L_KV, true>}},
+        {{launch_dlp<6, false, L_MV, L_MV, true>, launch_dlp<6, true, L_MV, L_MV, true>},
+         {launch_dlp<6, false, L_KV, L_KV, true>, launch_dlp<6, true, L_KV, L_KV, true>}}};
+    if (cfg < 4 || cfg > 6) return nullptr;
+    return table[cfg - 4][kv][tail];
 }
 
 GemmLaunchFn dlp_launcher(int cfg, bool tail, int la, int lb) {

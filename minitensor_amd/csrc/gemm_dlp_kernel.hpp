@@ -144,7 +144,8 @@ gemm_f32_dlp(GemmParams p) {
     // Fused row sums of A: the waves of the first wave column of the first
     // tile column see every A fragment of their rows exactly once (a partial
     // last chunk holds zeros past K; re-fetched chunks are not multiplied).
-    static_assert(!RS || (LA == L_MV && LB == L_MV), "row sums: two mn-contiguous operands");
+    static_assert(!RS || (LA == L_MV && LB == L_MV) || (LA == L_KV && LB == L_KV),
+                  "row sums: two mn-contiguous or two k-contiguous operands");
     const bool do_rs = RS && id.tn == 0 && (wave % WAVES_N) == 0;
     float rsum[MB];
 #pragma unroll
@@ -240,8 +241,12 @@ gemm_f32_dlp(GemmParams p) {
             const float tot = rsum[i] + __shfl_xor(rsum[i], 32);
             const int m = m0 + ra + i * 32 + (lane & 31);
             if (lane < 32 && m < p.M) {
-                float* d = p.rowsum + (int64_t)m * p.rowsum_stride;
-                *d = (p.rowsum_beta != 0.f ? p.rowsum_beta * *d : 0.f) + tot;
+                if (p.splits > 1 || p.part) {   // this (split, batch entry)'s partial
+                    p.rowsum[((int64_t)id.split * p.batch + id.bz) * p.M + m] = tot;
+                } else {
+                    float* d = p.rowsum + (int64_t)m * p.rowsum_stride;
+                    *d = (p.rowsum_beta != 0.f ? p.rowsum_beta * *d : 0.f) + tot;
+                }
             }
         }
     }

@@ -155,9 +155,11 @@ struct GemmParams {
     // C = sum_b A_b·B_b, whose reduction launch sums all splits x batch slabs.
     int part;
     ConvGeom cv;  // B = implicit im2col of the input at B (layout L_IM only)
-    // Optional fused row sums of A (direct-to-LDS kernel, splits == 1 only):
+    // Optional fused row sums of A (direct-to-LDS kernels):
     // rowsum[m*rowsum_stride] = rowsum_beta*rowsum[...] + sum_k A(m, k).  In
     // dW = dYᵀ·X this is the bias gradient db = sum over the batch of dY.
+    // With split-K or part, each (split, batch entry) writes its row sums to
+    // rowsum[(split*batch + b)*M + m] instead, for the reduction (csum_rows).
     float* rowsum; int64_t rowsum_stride; float rowsum_beta;
     // Optional channel sums (the convolution bias gradient db from dY [n][M][hw]),
     // computed by the vector split-K reduction, one workgroup per row m:
@@ -165,6 +167,9 @@ struct GemmParams {
     // csum_src[(img*M + m)*csum_hw + q].  The launcher clears csum when the
     // plan has no such reduction (the caller then sums separately).
     const float* csum_src; float* csum; int csum_n; int64_t csum_hw; float csum_beta;
+    // With csum_rows set, the channel sums are csum_beta*csum[m] + the sum over
+    // slabs of csum_rows[slab*M + m] (the GEMM's row-sum partials) instead.
+    const float* csum_rows;
     int tiles_m, tiles_n, group_m;
 };
 

@@ -273,9 +273,10 @@ Plan cfg_plan(const CfgCost& cc, int cfg, bool dl, int64_t M, int64_t N, int64_t
 }
 
 // Workspace of a batch-summed launch (GemmParams::part): one M x N slab per
-// split and batch entry, one split included.
+// split and batch entry, one split included, then M row sums per slab (the
+// fused bias gradient's partials).
 size_t part_ws_bytes(const Plan& pl, int64_t M, int64_t N, int64_t batch) {
-    return (size_t)std::max(pl.splits, 1) * batch * M * N * sizeof(float);
+    return (size_t)std::max(pl.splits, 1) * batch * M * (N + 1) * sizeof(float);
 }
 
 // Modelled cycles of one plan (see CostModel).
@@ -441,13 +442,14 @@ bool forced_plan(int64_t M, int64_t N, int64_t K, int64_t batch, bool dl_ok, boo
 // never picks the prefetching configurations for it (nullptr is a safety
 // net).  The row-sum form and the weight-gradient operand (L_IMW) exist for
 // all.
-GemmLaunchFn rowsum_launcher(int cfg, bool tail) {
+// kv: two k-contiguous operands (else two mn-contiguous ones).
+GemmLaunchFn rowsum_launcher(int cfg, bool tail, bool kv) {
     switch (cfg) {
-        case 0: return dl_rowsum_launcher_cfg0();
-        case 1: return dl_rowsum_launcher_cfg1();
-        case 2: return dl_rowsum_launcher_cfg2();
-        case 3: return dl_rowsum_launcher_cfg3();
-        default: return dlp_rowsum_launcher(cfg, tail);
+        case 0: return dl_rowsum_launcher_cfg0(kv);
+        case 1: return dl_rowsum_launcher_cfg1(kv);
+        case 2: return dl_rowsum_launcher_cfg2(kv);
+        case 3: return dl_rowsum_launcher_cfg3(kv);
+        default: return dlp_rowsum_launcher(cfg, tail, kv);
     }
 }
 
@@ -871,8 +873,22 @@ inline int csum_threads(int64_t per_channel) { return per_channel >= kCsumWideIt
 // csum[m] of GemmParams (the convolution, or Linear, bias gradient).
 template <int NT>
 __device__ __forceinline__ void channel_sum(const GemmParams& p, int m, float* red) {
-    const float r =
-        block_channel_sum<NT, kCsumLoads>(p.csum_src, p.M, m, p.csum_n, p.csum_hw, red);
+    float r;
+    if (p.csum_rows) {   // the GEMM's row-sum partials: splits slabs of M, fixed order
+        float v = 0.f;
+        for (int sl = threadIdx.x; sl < p.splits; sl += NT)
+            v += p.csum_rows[(int64_t)sl * p.M + m];
+        red[threadIdx.x] = v;
+        __syncthreads();
+        for (int w = NT / 2; w > 0; w >>= 1) {
+            if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+            __syncthreads();
+        }
+        r = red[0];
+        __syncthreads();
+    } else {
+        r = block_channel_sum<NT, kCsumLoads>(p.csum_src, p.M, m, p.csum_n, p.csum_hw, red);
+    }
     if (threadIdx.x == 0) p.csum[m] = (p.csum_beta != 0.f ? p.csum_beta * p.csum[m] : 0.f) + r;
 }
 
@@ -1000,9 +1016,11 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
     // Row sums of A are fused only into a direct-to-LDS launch of two
     // mn-contiguous operands without split-K (the caller sees p.rowsum cleared
     // and computes them separately).
-    if (batch != 1 || la != L_MV || lb != L_MV) p.rowsum = nullptr;
+    // A batch-summed product of two k-contiguous operands fuses them too, as
+    // partials per (split, batch entry) that its reduction sums for csum.
+    const bool rs_part = p.part && la == L_KV && lb == L_KV && p.csum != nullptr;
+    if (!rs_part && (batch != 1 || la != L_MV || lb != L_MV || p.part)) p.rowsum = nullptr;
     // The HBM-bound shapes (few rows or columns, or K <= 16) on the vector ALUs.
-    if (p.part) p.rowsum = nullptr;
     if (!implicit && la != L_KVI && p.rowsum == nullptr && p.csum == nullptr && !p.part) {
         const SkinnyPlan sp =
             skinny_plan(M, N, K, batch, la, lb, p.c_n_inner < N, device_cu_count());
@@ -1035,7 +1053,7 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
         if (need(plan) > 0 && (workspace == nullptr || ws_bytes < need(plan)))
             return MT_ERR_WORKSPACE;
     }
-    if (!plan.dl || plan.splits > 1) p.rowsum = nullptr;
+    if (!plan.dl || (plan.splits > 1 && !rs_part) || is_dl16_cfg(plan.cfg)) p.rowsum = nullptr;
     p.splits = plan.splits;
     p.k_per_split = plan.splits > 1 ? plan.kps : (int)std::max<int64_t>(K, 1);
     p.tiles_m = plan.tiles_m;
@@ -1047,6 +1065,15 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
     // Channel sums ride on the vector reduction only (one row per workgroup
     // row; a batch-summed product reduces to a single matrix)
     if (!p.ws_vec || (batch != 1 && !p.part)) p.csum = nullptr;
+    // The fused row sums of a batch-summed product: partials after the slabs,
+    // summed by the reduction in place of a second pass over csum_src.
+    if (rs_part && p.rowsum != nullptr && p.csum != nullptr) {
+        float* rows = p.ws + (int64_t)plan.splits * batch * M * N;
+        p.rowsum = rows;
+        p.csum_rows = rows;
+    } else if (rs_part) {
+        p.rowsum = nullptr;
+    }
 
     const int64_t nblocks = (int64_t)plan.tiles_m * plan.tiles_n * plan.splits * batch;
     if (nblocks >= ((int64_t)1 << 31)) return MT_ERR_UNSUPPORTED;
@@ -1059,12 +1086,13 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
                   "%s %dx%d a=%s b=%s split=%d wgs=%lld cfg=%d%s",
                   plan.ksw ? "ksw" : plan.dl ? "dl" : "rs", plan.bm,
                   plan.bn, layout_name(la), layout_name(halo ? L_IMH : lb), plan.splits,
-                  (long long)nblocks, plan.cfg, p.part ? " batch-summed" : "");
+                  (long long)nblocks, plan.cfg,
+                  p.part ? (p.csum_rows ? " batch-summed rows" : " batch-summed") : "");
 
     GemmLaunchFn fn = halo ? convh_launcher(plan.cfg)
                       : lb == L_IM || lb == L_IMR ? conv_launcher(plan.cfg, lb == L_IMR)
                       : lb == L_IMW ? convw_launcher(plan.cfg, (K & 15) != 0, la == L_KVI)
-                      : p.rowsum != nullptr ? rowsum_launcher(plan.cfg, (K & 15) != 0)
+                      : p.rowsum != nullptr ? rowsum_launcher(plan.cfg, (K & 15) != 0, la == L_KV)
                                             : pick_launcher(plan, la, lb, (K & 15) != 0);
     if (fn == nullptr) return MT_ERR_UNSUPPORTED;
     hipError_t e = fn(p, (unsigned)nblocks, stream);
@@ -1079,7 +1107,8 @@ int launch_gemm(GemmParams& p, bool dl, int la, int lb, void* workspace, size_t 
             q.c_b = 0;
         }
         if (q.ws_vec) {
-            const int nt = q.csum ? csum_threads((int64_t)q.csum_n * q.csum_hw) : 256;
+            const int nt =
+                q.csum && !q.csum_rows ? csum_threads((int64_t)q.csum_n * q.csum_hw) : 256;
             const dim3 grid((unsigned)std::min<int64_t>((N / 4 + nt - 1) / nt, 64),
                             (unsigned)std::min<int64_t>(M * q.batch, 65535));
             if (q.csum && nt == 1024)
@@ -2429,6 +2458,9 @@ int conv_bwd_weight(const mt_conv2d_desc* d, const float* input, const float* gr
         if (grad_bias) {
             p.csum_src = grad_out; p.csum = grad_bias; p.csum_n = (int)d->n;
             p.csum_hw = hw; p.csum_beta = beta_b;
+            // the GEMM's A is dY itself: its fused row sums give db without a
+            // second pass over dY where the plan can take them
+            p.rowsum = grad_bias;
         }
         const int la = classify(p.A, p.a_mn, p.a_k, p.M, p.K, p.a_b, p.batch > 1);
         const int lb = classify(p.B, p.b_mn, p.b_k, p.N, p.K, p.b_b, p.batch > 1);

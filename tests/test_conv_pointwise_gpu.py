@@ -135,7 +135,9 @@ def _forced_cases():
 def test_pointwise_dw_every_family(dev, fam, name, cfg, splits):
     """The batch-summed dW through every tile configuration at one and three
     splits: each family's epilogue writes per-image partials, and the
-    reduction sums splits x images of them (with db)."""
+    reduction sums splits x images of them.  db: the direct-to-LDS kernels
+    fuse it as row sums of dY per (split, image) that the reduction sums
+    ("rows"); the other families leave it to the reduction's pass over dY."""
     n, c, h, w, co = 3, 24, 12, 12, 40
     x = oracle.normal((n, c, h, w), 21)
     wt = oracle.normal((co, c, 1, 1), 22)
@@ -153,6 +155,7 @@ def test_pointwise_dw_every_family(dev, fam, name, cfg, splits):
         cfg_s = mt.last_config()
     print(f"[config] {cfg_s}", flush=True)
     assert cfg_s.startswith(name) and "batch-summed" in cfg_s, cfg_s
+    assert cfg_s.endswith(" rows") == (fam == mt.FAMILY_DL), cfg_s
     _, wdw, wdb = oracle.conv2d_backward(x, wt, dy, 1, 0)
     K = n * h * w
     assert_close(sync_np(dW), wdw, K, amax(dy), amax(x), f"dW {cfg_s}")
