@@ -237,14 +237,15 @@ def test_conv_backward_workspace_is_the_paths_need():
 
 def test_pointwise_conv_workspace():
     """1x1, stride 1, n 2, 32 -> 64 channels, 8x8 (K = 64 positions or fewer
-    channels: no plan splits K).  Backward: dW's per-image partial products,
-    2 x 64 x 32 floats (16384 B); dX needs nothing.  Forward: the batched
+    channels: no plan splits K).  Backward: dW's per-image partial products
+    and their fused row sums (db), 2 x 64 x (32 + 1) floats (16896 B); dX
+    needs nothing.  Forward: the batched
     product needs nothing, the NCHW-view kernel (which takes views whose
     (h, w) do not fold) room for an aligned weight copy, 64 x 32 floats."""
     import ctypes
     lib = mt.lib()
     d = mt.Conv2dDesc(2, 32, 8, 8, 64, 1, 1, 1, 0)
-    assert lib.mt_conv2d_bwd_workspace_f32(ctypes.byref(d)) == 16384
+    assert lib.mt_conv2d_bwd_workspace_f32(ctypes.byref(d)) == 16896
     assert lib.mt_conv2d_workspace_f32(ctypes.byref(d)) == 8192
     # 7x7 positions (not a multiple of 4): the channels-last path and its copies
     d = mt.Conv2dDesc(2, 32, 7, 7, 64, 1, 1, 1, 0)
