@@ -282,3 +282,60 @@ def test_pointwise_strided_dx(dev, n, c, h, w, co, stride):
     assert np.array_equal(outs[0], outs[1])
     wdx, _, _ = oracle.conv2d_backward(x, wt, dy, stride, 0)
     assert_close(outs[0], wdx, co, amax(dy), amax(wt), f"1x1 stride {stride} dX")
+
+
+def _random_cases(seed=20261202, count=24):
+    """Seeded 1x1 layers that take the per-image paths: c_in a multiple of 4,
+    positions per image (of the output) a multiple of 4, stride 1-4."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < count:
+        s = int(rng.choice([1, 1, 2, 3, 4]))
+        n = int(rng.integers(1, 5))
+        c = 4 * int(rng.integers(1, 33))
+        co = int(rng.integers(1, 97))
+        h, w = int(rng.integers(1, 30)), int(rng.integers(1, 30))
+        ho, wo = (h - 1) // s + 1, (w - 1) // s + 1
+        if (ho * wo) % 4:
+            continue
+        out.append((n, c, h, w, co, s, float(rng.choice([0.0, 1.0, 0.5]))))
+    return out
+
+
+@pytest.mark.parametrize("case", _random_cases(), ids=lambda c: "n{}c{}h{}w{}o{}s{}b{}".format(*c))
+def test_pointwise_random(dev, case):
+    """Forward (stride 1) with bias, dX, and dW + db accumulated with beta
+    into existing gradients, against the oracle."""
+    n, c, h, w, co, s, beta = case
+    ho, wo = (h - 1) // s + 1, (w - 1) // s + 1
+    seed = n * 1000 + c * 10 + co
+    x = oracle.normal((n, c, h, w), seed)
+    wt = oracle.normal((co, c, 1, 1), seed + 1)
+    b = oracle.normal((co,), seed + 2)
+    dy = oracle.normal((n, co, ho, wo), seed + 3)
+    dw0 = oracle.normal((co, c, 1, 1), seed + 4)
+    db0 = oracle.normal((co,), seed + 5)
+    X, Wt, dY = g(x, dev), g(wt, dev), g(dy, dev)
+    if s == 1:
+        y = mt.conv2d(X, Wt, g(b, dev), 1, 0)
+        print(f"[config] fwd {mt.last_config()}", flush=True)
+        assert_close(sync_np(y), oracle.conv2d(x, wt, b, 1, 0), c, amax(x), amax(wt), "fwd",
+                     extra=2e-6 * (1.0 + amax(b)))
+    dX, _, _ = mt.conv2d_backward(X, Wt, dY, s, 0, need_dw=False, need_db=False)
+    print(f"[config] dX {mt.last_config()}", flush=True)
+    d = mt.Conv2dDesc(n, c, h, w, co, 1, 1, s, 0)
+    ws = mt.workspace(mt.lib().mt_conv2d_bwd_workspace_f32(ctypes.byref(d)), dev)
+    dW, dB = g(dw0, dev), g(db0, dev)
+    rc = mt.lib().mt_conv2d_bwd_weight_bias_f32(ctypes.byref(d), X.data_ptr(), dY.data_ptr(),
+                                                dW.data_ptr(), beta, dB.data_ptr(), beta,
+                                                mt._ptr(ws), 0 if ws is None else ws.numel(),
+                                                None)
+    assert rc == 0, mt.lib().mt_strerror(rc).decode()
+    print(f"[config] dW {mt.last_config()}", flush=True)
+    wdx, wdw, wdb = oracle.conv2d_backward(x, wt, dy, s, 0)
+    K = n * ho * wo
+    assert_close(sync_np(dX), wdx, co, amax(dy), amax(wt), "dX")
+    assert_close(sync_np(dW), beta * dw0.astype(np.float64) + wdw, K, amax(dy), amax(x), "dW",
+                 extra=1e-5)
+    assert_close(sync_np(dB), beta * db0.astype(np.float64) + wdb, K, amax(dy), 1.0, "db",
+                 extra=1e-5)
