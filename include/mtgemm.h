@@ -184,7 +184,9 @@ int mt_conv2d_fwd_strided_f32(const mt_conv2d_desc* d, const float* input,
  *   weight: dW[c_out, c_in*kh*kw] = dY[c_out, n*h_out*w_out] · colᵀ (+ beta·dW);
  *           when c_in % 4 == 0 and n*h_out*w_out % 4 == 0, colᵀ is gathered by
  *           the kernel from a channels-last copy of the input (no column
- *           buffer), otherwise im2col fills one first
+ *           buffer); c_in 3, 6, 7, 10, ... (rounding up to 4 adds at most a
+ *           third) the same on the input padded with zero channels in the
+ *           workspace; otherwise im2col fills one first
  *           replaces conv2d_backward_weight_gpu (reference src/gpu_ops.cpp:2623-2713)
  *   input:  stride 1, square kernel, pad <= kh-1, c_out*kh*kw % 4 == 0: the
  *           implicit-GEMM forward convolution of dY with the weights

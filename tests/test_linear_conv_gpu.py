@@ -215,6 +215,47 @@ def test_conv_backward_shapes(dev, n, c, h, wd, co, kh, kw, stride, pad):
     assert_close(db, wdb, n * ho * wo, amax(dy), 1.0, "conv db")
 
 
+@pytest.mark.parametrize("n,c,hw,co,k,stride,pad,padded", [
+    (4, 3, 112, 64, 7, 2, 3, True),    # the RGB stem at batch 4: 3 -> 4 channels
+    (2, 6, 16, 24, 3, 1, 1, True),     # 6 -> 8
+    (2, 7, 12, 20, 3, 2, 1, True),     # 7 -> 8, stride 2
+    (2, 5, 16, 24, 3, 1, 1, False),    # 5 -> 8 would waste 3/8: the column path
+])
+def test_conv_dw_padded_channels(dev, n, c, hw, co, k, stride, pad, padded):
+    """dW + db of a layer whose c_in is not a multiple of 4: the implicit
+    weight gradient on the input padded with zero channels (where that adds at
+    most a third of the work), the real channels copied out with beta; against
+    the oracle, accumulating into existing gradients, bit-identical on a
+    repeat."""
+    x = oracle.normal((n, c, hw, hw), 61)
+    w = oracle.normal((co, c, k, k), 62)
+    ho = oracle.conv_out(hw, pad, k, stride)
+    dy = oracle.normal((n, co, ho, ho), 63)
+    dw0 = oracle.normal((co, c, k, k), 64)
+    db0 = oracle.normal((co,), 65)
+    X, dY = g(x, dev), g(dy, dev)
+    d = mt.Conv2dDesc(n, c, hw, hw, co, k, k, stride, pad)
+    ws = mt.workspace(mt.lib().mt_conv2d_bwd_workspace_f32(ctypes.byref(d)), dev)
+    outs = []
+    for _ in range(2):
+        dW, dB = g(dw0, dev), g(db0, dev)
+        rc = mt.lib().mt_conv2d_bwd_weight_bias_f32(ctypes.byref(d), X.data_ptr(), dY.data_ptr(),
+                                                    dW.data_ptr(), 0.5, dB.data_ptr(), 2.0,
+                                                    ws.data_ptr(), ws.numel(), None)
+        assert rc == 0, mt.lib().mt_strerror(rc).decode()
+        outs.append((sync_np(dW), sync_np(dB)))
+    cfg = mt.last_config()
+    print(f"[config] {cfg}", flush=True)
+    assert ("im2colT" in cfg) == padded, cfg
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+    _, wdw, wdb = oracle.conv2d_backward(x, w, dy, stride, pad)
+    K = n * ho * ho
+    assert_close(outs[0][0], 0.5 * dw0.astype(np.float64) + wdw, K, amax(dy), amax(x),
+                 "dW + 0.5 dW0", extra=1e-5)
+    assert_close(outs[0][1], 2.0 * db0.astype(np.float64) + wdb, K, amax(dy), 1.0,
+                 "db + 2 db0", extra=1e-5)
+
+
 @pytest.mark.parametrize("n,co,ho,wo,off", [
     (32, 64, 112, 112, 0),   # the ResNet stem's dY (102 MB): 16-byte loads
     (32, 64, 56, 56, 1),     # dY one float off 16-byte alignment: scalar loads
