@@ -18,6 +18,7 @@
 #include <cmath>
 #include <mutex>
 #include <cstdint>
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 
@@ -1464,18 +1465,40 @@ col2im_gather_f32(const float* dcol, float* dx, int C, int H, int W, int kh, int
 }
 
 // out[img][c][q] = c < C ? in[img][c][q] : 0 for c < CP (dense NCHW both):
-// blockIdx.y walks the output planes, threads the positions.
+// blockIdx.y walks the output planes, threads the positions, V floats each
+// (16-byte accesses when V == 4: HW % 4 == 0 and both tensors aligned).
+template <int V>
 __global__ void __launch_bounds__(256)
 pad_channels_f32(const float* in, float* out, int C, int CP, int64_t planes, int64_t HW) {
+    const int64_t items = HW / V;
     for (int64_t pl = blockIdx.y; pl < planes; pl += gridDim.y) {
         const int64_t img = pl / CP;
         const int c = (int)(pl - img * CP);
         float* o = out + pl * HW;
         const float* i = c < C ? in + (img * C + c) * HW : nullptr;
-        for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < HW;
-             q += (int64_t)gridDim.x * blockDim.x)
-            o[q] = i ? i[q] : 0.f;
+        for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < items;
+             q += (int64_t)gridDim.x * blockDim.x) {
+            if constexpr (V == 4) {
+                const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+                reinterpret_cast<f32x4*>(o)[q] = i ? reinterpret_cast<const f32x4*>(i)[q] : zero;
+            } else {
+                o[q] = i ? i[q] : 0.f;
+            }
+        }
     }
+}
+
+hipError_t launch_pad_channels(const float* in, float* out, int64_t n, int C, int CP, int64_t HW,
+                               hipStream_t s) {
+    const bool vec = (HW & 3) == 0 && ((uintptr_t)in & 15u) == 0 && ((uintptr_t)out & 15u) == 0;
+    const int64_t items = vec ? HW / 4 : HW, planes = n * CP;
+    const dim3 grid((unsigned)std::max<int64_t>(1, std::min<int64_t>((items + 255) / 256, 256)),
+                    (unsigned)std::max<int64_t>(1, std::min<int64_t>(planes, 65535)));
+    if (vec)
+        hipLaunchKernelGGL(pad_channels_f32<4>, grid, dim3(256), 0, s, in, out, C, CP, planes, HW);
+    else
+        hipLaunchKernelGGL(pad_channels_f32<1>, grid, dim3(256), 0, s, in, out, C, CP, planes, HW);
+    return capture_safe_last_error();
 }
 
 // db[c] = beta*db[c] + Σ_{img, hw} dY[img][c][hw]; one workgroup per channel
@@ -1838,7 +1861,7 @@ bool implicit_dw(const mt_conv2d_desc* d, int64_t np) {
 // weight gradient on its input padded with zero channels to c_in rounded up
 // to 4 (d4), where that adds at most a third of the work (c_in 3, 6, 7, 10,
 // 11, ...); the real channels of the padded gradient are then copied out.
-// The 7x7 stride-2 stem at batch 32: dW + db 229 against 288 us on the
+// The 7x7 stride-2 stem at batch 32: dW + db 231.8 against 288 us on the
 // column path.
 bool dw_padded(const mt_conv2d_desc* d, int64_t np, mt_conv2d_desc* d4) {
     if (d->c_in <= 0 || (d->c_in & 3) == 0) return false;
@@ -1855,6 +1878,21 @@ struct DwPadWs {
 DwPadWs dw_pad_ws(const mt_conv2d_desc* d4) {
     return {align_up((size_t)d4->n * d4->c_in * d4->h * d4->w * sizeof(float), 256),
             align_up((size_t)d4->c_out * d4->c_in * d4->kh * d4->kw * sizeof(float), 256)};
+}
+
+// The forward of a layer that would take the column path because c_in*kh*kw
+// % 4 != 0, with a kernel of at least 25 taps (the 7x7 RGB stem) and c_in
+// rounded up to 4 adding at most a third of the work: the NCHW-view kernel on
+// the input and weights padded with zero channels (d4).  The stem at batch 32:
+// 178.5 us against 187.5 on the column path.
+bool fwd_padded(const mt_conv2d_desc* d, mt_conv2d_desc* d4) {
+    if (d->c_in <= 0 || (d->c_in & 3) == 0 || d->kh * d->kw < 25) return false;
+    const int64_t cp = (d->c_in + 3) / 4 * 4;
+    if (3 * cp > 4 * d->c_in) return false;
+    *d4 = *d;
+    d4->c_in = cp;
+    int64_t ho, wo;
+    return conv_dims(d4, &ho, &wo) && nchw_implicit(d4);
 }
 
 // dX of a stride-1 convolution with a square kernel and pad <= kh - 1 is the
@@ -2374,8 +2412,16 @@ size_t mt_conv2d_workspace_f32(const mt_conv2d_desc* d) {
     // the NCHW-view kernel: split-K partials, and room for an aligned copy of
     // the weights (used only when the caller's are not 16-byte aligned)
     if (nchw_implicit(d)) return nchw_weight_ws(d) + implicit_gemm_ws(d->c_out, np, kg, false);
-    return align_up((size_t)kg * np * sizeof(float), 256) +
-           plan_ws(d->c_out, np, kg, 1, device_cu_count());
+    const size_t col = align_up((size_t)kg * np * sizeof(float), 256) +
+                       plan_ws(d->c_out, np, kg, 1, device_cu_count());
+    // a dense input takes the padded NCHW-view path; other views the column one
+    mt_conv2d_desc d4;
+    if (fwd_padded(d, &d4)) {
+        const DwPadWs pw = dw_pad_ws(&d4);
+        return std::max(col, pw.xp + pw.dw4 +
+                                 implicit_gemm_ws(d->c_out, np, d4.c_in * d->kh * d->kw, false));
+    }
+    return col;
 }
 
 int mt_conv2d_fwd_strided_f32(const mt_conv2d_desc* d, const float* input,
@@ -2435,6 +2481,28 @@ int mt_conv2d_fwd_strided_f32(const mt_conv2d_desc* d, const float* input,
                              ws_bytes - wb, s);
     }
 
+    // A dense input of a padded geometry (fwd_padded): the input and the
+    // weights padded with zero channels, then the NCHW-view kernel.
+    mt_conv2d_desc d4;
+    int64_t dst[4];
+    dense_strides(d, dst);
+    if (fwd_padded(d, &d4) && std::equal(dst, dst + 4, in_strides)) {
+        const DwPadWs pw = dw_pad_ws(&d4);   // the padded input and weights
+        if (!workspace || ws_bytes < pw.xp + pw.dw4 || ((uintptr_t)workspace & 15u) != 0)
+            return MT_ERR_WORKSPACE;
+        char* wsp = static_cast<char*>(workspace);
+        float* xp = reinterpret_cast<float*>(wsp);
+        float* wp = reinterpret_cast<float*>(wsp + pw.xp);
+        if (launch_pad_channels(input, xp, d->n, (int)d->c_in, (int)d4.c_in, d->h * d->w, s) !=
+                hipSuccess ||
+            launch_pad_channels(weight, wp, d->c_out, (int)d->c_in, (int)d4.c_in,
+                                d->kh * d->kw, s) != hipSuccess)
+            return MT_ERR_HIP;
+        int64_t st4[4];
+        dense_strides(&d4, st4);
+        return run_conv_nchw(&d4, Ho, Wo, xp, st4, wp, bias, output, wsp + pw.xp + pw.dw4,
+                             ws_bytes - pw.xp - pw.dw4, s);
+    }
     // Explicit im2col into the workspace, then the GEMM on the column buffer.
     const size_t col_bytes = align_up((size_t)kg * np * sizeof(float), 256);
     if (kg > 0 && (!workspace || ws_bytes < col_bytes)) return MT_ERR_WORKSPACE;
@@ -2520,12 +2588,9 @@ int conv_bwd_weight(const mt_conv2d_desc* d, const float* input, const float* gr
         char* wsp = static_cast<char*>(workspace);
         float* xp = reinterpret_cast<float*>(wsp);
         float* dw4 = reinterpret_cast<float*>(wsp + pw.xp);
-        const int64_t hwi = d->h * d->w, planes = d->n * d4.c_in;
-        const dim3 grid((unsigned)std::min<int64_t>((hwi + 255) / 256, 256),
-                        (unsigned)std::min<int64_t>(planes, 65535));
-        hipLaunchKernelGGL(pad_channels_f32, grid, dim3(256), 0, s, input, xp, (int)d->c_in,
-                           (int)d4.c_in, planes, hwi);
-        if (capture_safe_last_error() != hipSuccess) return MT_ERR_HIP;
+        if (launch_pad_channels(input, xp, d->n, (int)d->c_in, (int)d4.c_in, d->h * d->w, s) !=
+            hipSuccess)
+            return MT_ERR_HIP;
         const int rc = conv_bwd_weight(&d4, xp, grad_out, dw4, 0.f, grad_bias, beta_b,
                                        wsp + pw.xp + pw.dw4, ws_bytes - pw.xp - pw.dw4, s, db_done);
         if (rc != MT_OK) return rc;

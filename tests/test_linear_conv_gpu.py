@@ -215,6 +215,32 @@ def test_conv_backward_shapes(dev, n, c, h, wd, co, kh, kw, stride, pad):
     assert_close(db, wdb, n * ho * wo, amax(dy), 1.0, "conv db")
 
 
+def test_conv_forward_padded_stem(dev):
+    """The 7x7 stride-2 RGB stem at batch 4: a dense input takes the NCHW-view
+    kernel on the input and weights padded with a zero channel; a channel
+    slice of a 4-channel tensor (not dense) keeps the column path.  Both with
+    bias against the oracle."""
+    n, c, hw, co = 4, 3, 112, 64
+    x = oracle.normal((n, c, hw, hw), 71)
+    w = oracle.normal((co, c, 7, 7), 72)
+    b = oracle.normal((co,), 73)
+    want = oracle.conv2d(x, w, b, 2, 3)
+    y = mt.conv2d(g(x, dev), g(w, dev), g(b, dev), 2, 3)
+    cfg = mt.last_config()
+    print(f"[config] dense: {cfg}", flush=True)
+    assert "b=im2col_nchw" in cfg or "b=im2col_halo" in cfg, cfg
+    assert_close(sync_np(y), want, c * 49, amax(x), amax(w), "padded stem",
+                 extra=2e-6 * (1.0 + amax(b)))
+    wide = torch.zeros(n, c + 1, hw, hw, device=dev)
+    wide[:, 1:] = g(x, dev)
+    y = mt.conv2d(wide[:, 1:], g(w, dev), g(b, dev), 2, 3)
+    cfg = mt.last_config()
+    print(f"[config] slice: {cfg}", flush=True)
+    assert "im2col" not in cfg, cfg
+    assert_close(sync_np(y), want, c * 49, amax(x), amax(w), "stem on a slice",
+                 extra=2e-6 * (1.0 + amax(b)))
+
+
 @pytest.mark.parametrize("n,c,hw,co,k,stride,pad,padded", [
     (4, 3, 112, 64, 7, 2, 3, True),    # the RGB stem at batch 4: 3 -> 4 channels
     (2, 6, 16, 24, 3, 1, 1, True),     # 6 -> 8
