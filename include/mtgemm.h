@@ -157,7 +157,9 @@ typedef struct mt_conv2d_desc {
 
 /* A 1x1 kernel with stride 1 and no padding, c_in and h*w multiples of 4:
  * one product per image, Y_b[c_out][h*w] = W · X_b[c_in][h*w], over the NCHW
- * tensors themselves. */
+ * tensors themselves.  c_in 3, 6, 7, ... with a kernel of at least 25 taps
+ * (the RGB stem) and a dense input: the input and weights padded with zero
+ * channels in the workspace, then the implicit GEMM over the NCHW view. */
 int mt_conv2d_fwd_f32(const mt_conv2d_desc* d, const float* input, const float* weight,
                       const float* bias, float* output, void* workspace, size_t ws_bytes,
                       void* stream);
