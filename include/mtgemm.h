@@ -182,7 +182,9 @@ int mt_conv2d_fwd_strided_f32(const mt_conv2d_desc* d, const float* input,
  * 1x1, stride 1, no padding, c_in and h_out*w_out multiples of 4: dX_b =
  * Wᵀ · dY_b per image, and dW = Σ_b dY_b · X_bᵀ as per-image partial
  * products in the workspace, summed (with beta·dW, and db as the channel
- * sums of dY) by the split-K reduction launch.  Other geometries:
+ * sums of dY) by the split-K reduction launch; at strides 2-4 the dW takes
+ * the same product on the input pixels the stride reads, copied out into
+ * the workspace.  Other geometries:
  *   weight: dW[c_out, c_in*kh*kw] = dY[c_out, n*h_out*w_out] · colᵀ (+ beta·dW);
  *           when c_in % 4 == 0 and n*h_out*w_out % 4 == 0, colᵀ is gathered by
  *           the kernel from a channels-last copy of the input (no column

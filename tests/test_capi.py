@@ -218,7 +218,8 @@ def test_conv_backward_workspace_is_the_paths_need():
       dW implicit: channels-last x 16*8*8 floats (4096 B), dY read in NCHW;
     1x1 stride 2, n 2, 32 -> 64 channels, 8x8 -> 4x4:
       dX: the per-image product's phase-(0, 0) output 2*32*16 floats (4096 B);
-      dW: x copy 2*32*64 floats (16384 B)."""
+      dW: x's output positions 2*32*16 floats (4096 B) + the per-image
+      products and their row sums 2*64*(32 + 1) floats (16896 B)."""
     import ctypes
     lib = mt.lib()
     d = mt.Conv2dDesc(1, 16, 8, 8, 16, 3, 3, 2, 1)
@@ -226,7 +227,7 @@ def test_conv_backward_workspace_is_the_paths_need():
     with mt.forced_config(mt.FAMILY_DL, 1, 1):
         assert lib.mt_conv2d_bwd_workspace_f32(ctypes.byref(d)) == 1024 + 9216 + 4 * 1024
     d = mt.Conv2dDesc(2, 32, 8, 8, 64, 1, 1, 2, 0)
-    assert lib.mt_conv2d_bwd_workspace_f32(ctypes.byref(d)) == 16384
+    assert lib.mt_conv2d_bwd_workspace_f32(ctypes.byref(d)) == 4096 + 16896
     # the benchmark's 5a layer: far below its 57.8 MB column buffer
     d = mt.Conv2dDesc(32, 256, 14, 14, 256, 3, 3, 1, 1)
     need = lib.mt_conv2d_bwd_workspace_f32(ctypes.byref(d))

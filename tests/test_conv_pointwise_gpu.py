@@ -265,8 +265,9 @@ def test_pointwise_workspace_is_exact_and_graph_replays(dev):
 def test_pointwise_strided_dx(dev, n, c, h, w, co, stride):
     """dX of a strided 1x1 layer without padding: the product Wᵀ·dY_b per
     image into the phase-(0, 0) buffer, then the interleave writes dX with
-    zeros on every pixel no tap reaches; against the oracle, bit-identical on
-    a repeat."""
+    zeros on every pixel no tap reaches; dW + db: x's output positions copied
+    out, then the batch-summed 1x1 product.  Against the oracle, bit-identical
+    on a repeat."""
     x = oracle.normal((n, c, h, w), 51)
     wt = oracle.normal((co, c, 1, 1), 52)
     ho, wo = oracle.conv_out(h, 0, 1, stride), oracle.conv_out(w, 0, 1, stride)
@@ -280,8 +281,15 @@ def test_pointwise_strided_dx(dev, n, c, h, w, co, stride):
     print(f"[config] {cfg}", flush=True)
     assert "im2col" not in cfg and "a=mv b=mv" in cfg, cfg
     assert np.array_equal(outs[0], outs[1])
-    wdx, _, _ = oracle.conv2d_backward(x, wt, dy, stride, 0)
+    wdx, wdw, wdb = oracle.conv2d_backward(x, wt, dy, stride, 0)
     assert_close(outs[0], wdx, co, amax(dy), amax(wt), f"1x1 stride {stride} dX")
+    _, dW, dB = mt.conv2d_backward(X, Wt, dY, stride, 0, need_dx=False)
+    cfg = mt.last_config()
+    print(f"[config] dW {cfg}", flush=True)
+    assert "batch-summed" in cfg, cfg
+    K = n * ho * wo
+    assert_close(sync_np(dW), wdw, K, amax(dy), amax(x), f"1x1 stride {stride} dW")
+    assert_close(sync_np(dB), wdb, K, amax(dy), 1.0, f"1x1 stride {stride} db")
 
 
 def _random_cases(seed=20261202, count=24):
