@@ -1,7 +1,8 @@
-"""GPU: benchmark configurations 2, 3 and 5a checked element-wise over the
-whole output (forward, and 5a's dX, dW and db) against float64 products of the
-same seeded inputs (numpy BLAS; fp64_reference.py for the convolution, pinned
-to the CPU oracle in test_fp64_reference.py).  The oracle itself takes minutes
+"""GPU: benchmark configurations 2, 3 and 5a and the 63-row skinny product
+checked element-wise over the whole output (forward, and 5a's dX, dW and db)
+against float64 products of the same seeded inputs (numpy BLAS;
+fp64_reference.py for the convolution, pinned to the CPU oracle in
+test_fp64_reference.py).  The oracle itself takes minutes
 per full tensor at these sizes; the other tests check them on sampled rows,
 channels and images plus size-independent identities.  Bound: the fp32 parity
 bound 1e-5 * sqrt(K) * max|a| * max|b| against the exact sum."""
@@ -83,3 +84,14 @@ def test_resnet_downsampling_layer_every_element(dev, c_in, c_out, k, pad):
     assert_close(dx, wdx, c_out * k * k, amax(dy), amax(w), "stride-2 dX every element")
     assert_close(dw, wdw, npix, amax(dy), amax(x), "stride-2 dW every element")
     assert_close(db, wdb, npix, amax(dy), 1.0, "stride-2 db")
+
+
+def test_skinny_63_rows_every_element(dev):
+    # the reference benchmark's 63x4096·4096x4096 row (test/benchmark.cpp:738):
+    # 64x64 MFMA tiles with split-K over a 63-row ragged tile
+    a = oracle.uniform((63, 4096), 46)
+    b = oracle.uniform((4096, 4096), 47)
+    c = host(mt.gemm(g(a, dev), g(b, dev)))
+    print(f"[config] 63 rows {mt.last_config()}", flush=True)
+    assert_close(c, a.astype(np.float64) @ b.astype(np.float64), 4096, amax(a), amax(b),
+                 "63x4096x4096 every element")
