@@ -95,3 +95,23 @@ def test_skinny_63_rows_every_element(dev):
     print(f"[config] 63 rows {mt.last_config()}", flush=True)
     assert_close(c, a.astype(np.float64) @ b.astype(np.float64), 4096, amax(a), amax(b),
                  "63x4096x4096 every element")
+
+
+def test_resnet_stem_every_element(dev):
+    # the 7x7 stride-2 RGB stem at batch 32 (c_in = 3: forward and dW + db on
+    # the input padded with a zero channel, dX phased): every element
+    x = oracle.normal((32, 3, 224, 224), 55)
+    w = oracle.normal((64, 3, 7, 7), 56, std=(2.0 / 147) ** 0.5)
+    b = oracle.normal((64,), 57, std=0.1)
+    X, W = g(x, dev), g(w, dev)
+    y = host(mt.conv2d(X, W, g(b, dev), 2, 3))
+    print(f"[config] stem forward {mt.last_config()}", flush=True)
+    assert_close(y, f64.conv2d(x, w, b, 2, 3), 147, amax(x), amax(w), "stem forward",
+                 extra=1e-6)
+    dy = oracle.normal(y.shape, 58, std=0.01)
+    dx, dw, db = (host(t) for t in mt.conv2d_backward(X, W, g(dy, dev), 2, 3))
+    wdx, wdw, wdb = f64.conv2d_backward(x, w, dy, 2, 3)
+    npix = 32 * y.shape[2] * y.shape[3]
+    assert_close(dx, wdx, 64 * 49, amax(dy), amax(w), "stem dX every element")
+    assert_close(dw, wdw, npix, amax(dy), amax(x), "stem dW every element")
+    assert_close(db, wdb, npix, amax(dy), 1.0, "stem db")
